@@ -1,0 +1,235 @@
+#!/usr/bin/env python3
+"""Benchmark of the fly actor's batched inference and teaching step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 1024] [--no-cpu]
+
+Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
+1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
+fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in device memory.
+  value  : decisions / s of the batched forward (fc_forward: plug, 3 hops, read-out), K timed batches;
+  train  : samples / s of the full teaching step (fc_teach_step: forward, KL loss, backward, Adam + running
+           average), K timed steps;
+  roofline: the dominant kernel's algorithmic bytes per launch / its mean duration (HIP events on the library's
+           stream over the timed region), against 8 TB/s;
+  cpu_baseline: the reference's own CPU forward (fly_infer.cpp, compiled into oracle/_ref) on a bounded sample of
+           the same network, one core; train: the oracle's float32 restatement on a small batch.
+One JSON line on stdout.  Only one GPU: --gpus N > 1 exits with a message.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+PEAK_HBM = 8.0e12          # MI355X HBM3E, bytes / s
+METRIC = "decisions/sec (B=4096 fwd) + train samples/sec; % of MI355X HBM peak"
+
+
+def algorithmic_bytes(s: dict, B: int, sz: int = 4) -> dict:
+    """Compulsory traffic of the reference dataflow: every tensor written once and read once per consuming stage,
+    sources read once per hop, structure once per batch (no widx: synthetic connections belong to one hop).
+    Per hop launch and per whole batch, inference and train."""
+    N = list(s["sizes"])
+    E = [len(h["col"]) for h in s["hop"]]
+    D = [int((h["drow"] >= 0).sum()) for h in s["hop"]]
+    A, OD, K = s["n_act"], s["obs_dim"], s["hops"]
+    hop_fwd = [N[k] * B * sz + D[k] * B * sz + N[k + 1] * B * sz + E[k] * 8 + (N[k + 1] + 1) * 4 for k in range(K)]
+    infer = OD * B * 4 + 2 * N[0] * B * sz + s["fan"] * N[0] * 8 + N[0] * 4 + sum(hop_fwd) \
+        + N[K] * B * sz + A * B * 4 + A * N[K] * 4
+    n_neurons_in_play = len(set(s["n0"].tolist()).union(*[set(h["nid"].tolist()) for h in s["hop"]]))
+    n_params = s["n_w"] + 2 * n_neurons_in_play + s["n_s"] * s["fan"] + s["n_s"] + A * N[K] + A
+    hop_bwd = []
+    train = infer + sum(N[k] * B * sz for k in range(1, K + 1)) + 3 * A * B * 4 + A * B * 4 + 2 * N[K] * B * sz
+    for k in range(K, 0, -1):
+        b = 4 * N[k] * B * sz + (N[k] + N[k - 1]) * B * sz + (N[k] + N[k - 1]) * B * sz + 8 * E[k - 1] + 2 * D[k - 1] * B * sz
+        hop_bwd.insert(0, b)
+        train += b
+    train += 3 * N[0] * B * sz + 2 * N[0] * B * 4 + OD * B * 4 + 36 * n_params
+    return {"hop_fwd": hop_fwd, "hop_bwd": hop_bwd, "infer": infer, "train": train, "n_params": n_params}
+
+
+def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None, dict | None]:
+    import numpy as np
+    from oracle import refinfer
+    rng = np.random.default_rng(1)
+    fwd = None
+    if refinfer.available() and sample > 0:
+        ref = refinfer.RefInfer(s, params)
+        obs = rng.standard_normal((sample, s["obs_dim"])).astype(np.float32)
+        ref.forward(obs[:8])
+        t0 = time.perf_counter()
+        ref.forward(obs)
+        dt = time.perf_counter() - t0
+        fwd = {"value": sample / dt, "unit": "decisions/s", "cores": 1, "kind": "reference",
+               "sample": f"{sample} batch-1 decisions of the same network through fly_infer.cpp (compiled from the "
+                         f"reference), {dt:.1f} s"}
+    train = None
+    if train_batch > 0:
+        from flyguy_amd.export import net_bytes
+        from oracle.oracle import Oracle
+        o = Oracle(net_bytes(s), params, "f32")
+        obs = rng.standard_normal((train_batch, s["obs_dim"])).astype(np.float32)
+        tl = (rng.standard_normal((train_batch, s["n_act"])) * 2).astype(np.float32)
+        t0 = time.perf_counter()
+        lg = o.forward(obs)
+        dl, _, _ = o.loss(lg, tl)
+        grads = o.backward(dl)
+        for p, g in zip(params, grads):
+            z = np.zeros_like(g)
+            pp, e = p.astype(np.float32).copy(), p.astype(np.float32).copy()
+            o.adam(pp, g, z, z.copy(), e, 1e-4, 1, 1.0, 0.999)
+        dt = time.perf_counter() - t0
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        train = {"value": train_batch / dt, "unit": "samples/s", "cores": threads, "kind": "port",
+                 "sample": f"one teaching step (forward, KL, backward, Adam) on {train_batch} samples through the "
+                           f"oracle's float32 restatement, {dt:.1f} s"}
+    return fwd, train
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=4096)
+    ap.add_argument("--cpu-sample", type=int, default=1024)
+    ap.add_argument("--cpu-train-batch", type=int, default=32)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print(f"bench.py runs on one GPU only (asked for {max(args.gpus, world)}): this build measures the one-GPU "
+              f"share of the data-parallel path; how it shards is described in DESIGN.md", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    from flyguy_amd._lib import call, lib, profile_read
+    from flyguy_amd.export import net_bytes
+    from flyguy_amd.synth import synth_3hop
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    B, K, W = args.batch, args.steps, args.warmup
+    t_setup = time.perf_counter()
+    s, params = synth_3hop()
+    raw = net_bytes(s)
+    L = lib()
+    core = L.fc_create_from_memory(raw, len(raw), B)
+    if not core:
+        call("fc_create_from_memory")
+    dev = torch.device("cuda:0")
+    tens = [torch.as_tensor(p).to(dev).contiguous() for p in params]
+    ptrs = (ctypes.c_void_p * 7)(*[t.data_ptr() for t in tens])
+    call("fc_copy", core, 0, 1, ptrs)
+    call("fc_copy", core, 1, 1, ptrs)
+    g = torch.Generator(device=dev).manual_seed(0)
+    obs = torch.randn(B, s["obs_dim"], device=dev, generator=g)
+    teacher = torch.randn(B, s["n_act"], device=dev, generator=g) * 2.0
+    logits = torch.empty(B, s["n_act"], device=dev)
+    stats = torch.zeros(2, device=dev)
+    torch.cuda.synchronize()
+    print(f"# set-up {time.perf_counter() - t_setup:.1f} s", file=sys.stderr, flush=True)
+    ab = algorithmic_bytes(s, B)
+
+    # ---- batched forward
+    for _ in range(W):
+        call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)
+    torch.cuda.synchronize()
+    call("fc_profile", core, 1)
+    profile_read(core, reset=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)
+    torch.cuda.synchronize()
+    t_fwd = time.perf_counter() - t0
+    prof_fwd = profile_read(core, reset=True)
+    call("fc_profile", core, 0)
+    assert torch.isfinite(logits).all()
+    ms_fwd = 1e3 * t_fwd / K
+    dps = B * K / t_fwd
+    print(f"# forward: {ms_fwd:.3f} ms / batch of {B}, {dps:,.0f} decisions/s", file=sys.stderr, flush=True)
+
+    # ---- teaching step
+    for _ in range(W):
+        call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4, 3e-5, 1e-4, 0.0, 0.999, stats.data_ptr())
+    torch.cuda.synchronize()
+    call("fc_profile", core, 1)
+    profile_read(core, reset=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4, 3e-5, 1e-4, 0.0, 0.999, stats.data_ptr())
+    torch.cuda.synchronize()
+    t_train = time.perf_counter() - t0
+    prof_train = profile_read(core, reset=True)
+    call("fc_profile", core, 0)
+    assert np.isfinite(float(stats[0]))
+    ms_train = 1e3 * t_train / K
+    sps = B * K / t_train
+    print(f"# train: {ms_train:.3f} ms / step of {B}, {sps:,.0f} samples/s, kl {float(stats[0]) / B:.4f}",
+          file=sys.stderr, flush=True)
+
+    def stage_ms(prof, name):
+        tot, n = prof.get(name, (0.0, 0))
+        return tot / n if n else float("nan")
+
+    # dominant kernels: the largest hop of the forward, the largest hop backward of the step
+    fwd_hops = {f"hop{k + 1} fwd": stage_ms(prof_fwd, f"hop{k + 1} fwd") for k in range(s["hops"])}
+    dom_f = max(fwd_hops, key=fwd_hops.get)
+    kf = int(dom_f[3]) - 1
+    ach_f = ab["hop_fwd"][kf] / (fwd_hops[dom_f] * 1e-3)
+    bwd_hops = {f"hop{k + 1} bwd": stage_ms(prof_train, f"hop{k + 1} bwd") for k in range(s["hops"])}
+    dom_b = max(bwd_hops, key=bwd_hops.get)
+    kb = int(dom_b[3]) - 1
+    ach_b = ab["hop_bwd"][kb] / (bwd_hops[dom_b] * 1e-3)
+    traffic = None
+    tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_synth3hop_b4096.json")
+    if os.path.exists(tfile):
+        with open(tfile) as fh:
+            traffic = json.load(fh).get("k_fwd " + dom_f)
+
+    cpu_f = cpu_t = None
+    if not args.no_cpu:
+        cpu_f, cpu_t = cpu_baselines(s, params, args.cpu_sample, args.cpu_train_batch)
+
+    line = {
+        "metric": METRIC, "value": round(dps, 1), "unit": "decisions/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_fwd, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic: random 3-hop network of the benchmark shape, obs ~N(0,1), teacher ~N(0,2)",
+        "config": {"workload": "batched fp32 inference (plug, 3 sparse hops, read-out) on the synthetic 3-hop network "
+                               "16894/46393/37748/1332 rows, 1.2M/1.5M/292,734 connections, B=4096",
+                   "batch": B, "rows": s["sizes"], "connections": [len(h["col"]) for h in s["hop"]],
+                   "redrive_rows": [int((h["drow"] >= 0).sum()) for h in s["hop"]]},
+        "roofline": {"bound": "hbm", "kernel": "k_fwd " + dom_f, "achieved": round(ach_f / 1e9, 1), "peak": 8000.0,
+                     "unit": "GB/s", "frac": round(ach_f / PEAK_HBM, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": ab["hop_fwd"][kf], "mean_launch_ms": round(fwd_hops[dom_f], 4),
+                     "whole_batch_frac": round(ab["infer"] / (t_fwd / K) / PEAK_HBM, 4),
+                     "whole_batch_algorithmic_bytes": ab["infer"]},
+        "cpu_baseline": cpu_f,
+        "train": {"value": round(sps, 1), "unit": "samples/s", "ms_per_step": round(ms_train, 4),
+                  "workload": "fp32 teaching step: forward, KL(teacher||student) over 90 actions, fused backward, "
+                              "Adam (lr 1e-4, betas 0.9/0.999) + running average over 2,992,734 strengths, gains, "
+                              "thresholds and plugs, B=4096",
+                  "roofline": {"bound": "hbm", "kernel": "k_bwd " + dom_b, "achieved": round(ach_b / 1e9, 1),
+                               "peak": 8000.0, "unit": "GB/s", "frac": round(ach_b / PEAK_HBM, 4),
+                               "algorithmic_bytes_per_launch": ab["hop_bwd"][kb],
+                               "mean_launch_ms": round(bwd_hops[dom_b], 4),
+                               "whole_step_frac": round(ab["train"] / (t_train / K) / PEAK_HBM, 4),
+                               "whole_step_algorithmic_bytes": ab["train"]},
+                  "cpu_baseline": cpu_t},
+        "stages_ms": {"forward": {k: round(v[0] / v[1], 4) for k, v in prof_fwd.items()},
+                      "train": {k: round(v[0] / v[1], 4) for k, v in prof_train.items()}},
+    }
+    print(json.dumps(line), flush=True)
+    L.fc_free(core)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,104 @@
+"""ctypes binding of the MI355X library (flyguy_amd/libflyguy_core.so, include/flyguy_core.h).
+
+Loading never falls back: if the library is missing or a call fails, an exception says why.  The library
+records errors per thread (fc_last_error); every wrapper call here checks it.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libflyguy_core.so"
+_lib = None
+
+vp, ci, cll, cf = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float
+_SIGS = {
+    "fc_create": (vp, [ctypes.c_char_p, ci]),
+    "fc_create_from_memory": (vp, [ctypes.c_char_p, cll, ci]),
+    "fc_free": (None, [vp]),
+    "fc_set_stream": (None, [vp, vp]),
+    "fc_sizes": (None, [vp, ctypes.POINTER(cll)]),
+    "fc_copy": (None, [vp, ci, ci, ctypes.POINTER(vp)]),
+    "fc_forward": (None, [vp, vp, ci, vp, ci]),
+    "fc_zero_grad": (None, [vp]),
+    "fc_backward": (None, [vp, vp, ci]),
+    "fc_grad_norm": (cf, [vp]),
+    "fc_step": (cf, [vp, cf, cf, cf, cf, cf]),
+    "fc_adam_t": (cll, [vp, cll]),
+    "fc_sync": (None, [vp]),
+    "fc_last_error": (ctypes.c_char_p, []),
+    "fc_clear_error": (None, []),
+    "fc_kl_loss": (None, [vp, vp, vp, ci, cf, vp, vp]),
+    "fc_teach_step": (cf, [vp, vp, vp, ci, cf, cf, cf, cf, cf, cf, vp]),
+    "fc_export_state": (None, [vp, ci, ci, vp, ci]),
+    "fc_profile": (None, [vp, ci]),
+    "fc_profile_read": (ci, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(cll), ci, ci]),
+    "fc_plan_segments": (ci, [vp, ci, ci, vp, cll, vp, cll, ctypes.POINTER(cll)]),
+    "fh_spmm": (None, [vp, vp, vp, vp, vp, ci, ci, ci, cll, vp, ci, vp, ci, ci, vp, vp, vp]),
+    "fh_spmm_bwd": (None, [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, cll, vp, ci, vp, ci, ci, vp, vp, vp, vp]),
+}
+
+
+class LibraryError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library (loaded once).  Raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise LibraryError(f"{LIB_PATH} is not built (python -m flyguy_amd.build)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def check(what: str = "") -> None:
+    """Raise the library's pending error, if any."""
+    msg = lib().fc_last_error()
+    if msg:
+        lib().fc_clear_error()
+        raise LibraryError(f"{what}: {msg.decode()}" if what else msg.decode())
+
+
+def call(name: str, *args):
+    out = getattr(lib(), name)(*args)
+    check(name)
+    return out
+
+
+def plan_segments(rowptr, seg_max: int = 256):
+    """Row plan of a CSR row pointer (host only): (segments int32 [nseg, 4], split rows int32 [nsplit, 4], nslot)."""
+    import numpy as np
+    rp = np.ascontiguousarray(rowptr, dtype=np.int32)
+    rows = len(rp) - 1
+    counts = (cll * 3)()
+    lib().fc_plan_segments(rp.ctypes.data, rows, seg_max, None, 0, None, 0, counts)
+    lib().fc_clear_error()
+    nseg, nsplit, nslot = int(counts[0]), int(counts[1]), int(counts[2])
+    seg = np.zeros((max(nseg, 1), 4), np.int32)
+    split = np.zeros((max(nsplit, 1), 4), np.int32)
+    rc = lib().fc_plan_segments(rp.ctypes.data, rows, seg_max, seg.ctypes.data, nseg, split.ctypes.data, nsplit, counts)
+    if rc != 0:
+        check("fc_plan_segments")
+        raise LibraryError("fc_plan_segments failed")
+    return seg[:nseg], split[:nsplit], nslot
+
+
+STAGES = {0: "obs transpose", 1: "pack", 2: "plug", 11: "logits", 12: "loss", 13: "readout bwd", 22: "reduce",
+          23: "adam", 24: "zero"}
+for _k in range(8):
+    STAGES[3 + _k] = f"hop{_k + 1} fwd"
+    STAGES[14 + _k] = f"hop{_k + 1} bwd"
+
+
+def profile_read(core, reset: bool = True) -> dict:
+    """{stage name: (total ms, timed runs)} of the stages that ran since the last reset."""
+    ms = (ctypes.c_double * 25)()
+    n = (cll * 25)()
+    call("fc_profile_read", core, ms, n, 25, int(reset))
+    return {STAGES[i]: (ms[i], int(n[i])) for i in range(25) if n[i] and i in STAGES}

@@ -1,0 +1,707 @@
+// Host side of the flyguy MI355X library: NET.bin reading and checking, row plans, device buffers, and the
+// fc_* / fh_* entry points of include/flyguy_core.h.
+//
+// Device memory of a handle (max_batch = Bm, Tm = Bm / 32 tiles, states tiled [T][rows][32] fp32):
+//   parameters: one block of 5 sets x PT floats (sets in fc_copy order: weights, running average, m, v,
+//               gradient), each set holding the seven arrays at 64-float aligned offsets, so Adam is one launch;
+//   structure: NET.bin's index arrays, the packed (index, weight) pairs of every product (refreshed from the
+//              current weights at each pass), and the row plans (forward: CSR rows; backward: CSC rows);
+//   states: x, drive, h0, gdrive, z_k / h_k per hop, two gz buffers, logits / dlogits;
+//   partial sums: split rows, per-edge weight gradients [T][E_k], per-row gain / threshold gradients [T][rows],
+//                 plug gradients [T][n_s] / [T][E_in], read-out gradients [chunks][n_act * n_dn].
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "../../include/flyguy_core.h"
+#include "kernels.h"
+
+namespace fg {
+
+static thread_local std::string g_err;
+void set_error(const std::string& m) { g_err = m; }
+const char* last_error() { return g_err.c_str(); }
+void clear_error() { g_err.clear(); }
+
+// ------------------------------------------------------------------------------------------------ row plans
+struct HostPlan {
+    std::vector<int4> seg, split;
+    int nslot = 0;
+};
+
+// Cut rows into segments of at most seg_max edges (a longer row gets ceil(d / seg_max) segments of nearly equal
+// length), then order all segments longest first; equal lengths keep (row, segment) order.
+static bool make_plan(const int* rowptr, int rows, int seg_max, HostPlan& p) {
+    p.seg.clear();
+    p.split.clear();
+    p.nslot = 0;
+    if (rows < 0 || seg_max <= 0 || (rows > 0 && rowptr[0] != 0)) return false;
+    for (int r = 0; r < rows; ++r) {
+        const long long d = (long long)rowptr[r + 1] - rowptr[r];
+        if (d < 0) return false;
+        if (d <= seg_max) {
+            p.seg.push_back(make_int4(r, rowptr[r], rowptr[r + 1], -1));
+            continue;
+        }
+        const int ns = (int)((d + seg_max - 1) / seg_max);
+        p.split.push_back(make_int4(r, p.nslot, ns, 0));
+        for (int s = 0; s < ns; ++s) {
+            const int b = rowptr[r] + (int)(d * s / ns), e = rowptr[r] + (int)(d * (s + 1) / ns);
+            p.seg.push_back(make_int4(r, b, e, p.nslot + s));
+        }
+        p.nslot += ns;
+    }
+    std::stable_sort(p.seg.begin(), p.seg.end(), [](const int4& a, const int4& b) { return a.z - a.y > b.z - b.y; });
+    return true;
+}
+
+struct DevPlan {
+    int4* seg = nullptr;
+    int4* split = nullptr;
+    int nseg = 0, nsplit = 0, nslot = 0, rows = 0;
+    long long E = 0;
+    Plan view() const { return Plan{seg, nseg, split, nsplit, rows, nslot, E}; }
+};
+
+struct HopD {
+    int rows = 0, src = 0, E = 0;
+    int *nid = nullptr, *crow = nullptr, *col = nullptr, *widx = nullptr, *tcrow = nullptr, *tcol = nullptr,
+        *twidx = nullptr, *drow = nullptr;
+    bool has_drive = false;
+    int2 *cw = nullptr, *tcw = nullptr;
+    DevPlan fp, bp;
+    float *z = nullptr, *h = nullptr, *ggp = nullptr, *gsp = nullptr;
+};
+
+// Stages timed with HIP events on the library's stream when profiling is on (fc_profile): where the time of a
+// forward / backward / step goes, kernel by kernel.
+enum Stage {
+    ST_OBS = 0, ST_PACK = 1, ST_PLUG = 2, ST_HOP = 3,            // ST_HOP + k: forward of hop k+1 (k < 8)
+    ST_LOGITS = 11, ST_LOSS = 12, ST_RBWD = 13, ST_BHOP = 14,    // ST_BHOP + k: backward of hop k+1 (k < 8)
+    ST_REDUCE = 22, ST_ADAM = 23, ST_ZERO = 24, ST_COUNT = 25
+};
+
+struct Prof {
+    bool on = false;
+    std::vector<std::pair<hipEvent_t, int>> rec;   // (event, stage*2 + 0 start / 1 end) in recording order
+    std::vector<hipEvent_t> pool;
+    double ms[ST_COUNT] = {0};
+    long long n[ST_COUNT] = {0};
+    hipEvent_t get() {
+        if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+};
+
+struct Core {
+    int obs_dim = 0, n_act = 0, hops = 0, n_neurons = 0, n_w = 0, n_s = 0, fan = 0, n_dn = 0, E_in = 0;
+    std::vector<int> sizes, E;
+    int maxB = 0, Tm = 0;
+    int *in_crow = nullptr, *in_col = nullptr, *n0 = nullptr, *dn = nullptr, *dn_inv = nullptr;
+    int2* in_cw = nullptr;
+    DevPlan pp;
+    std::vector<HopD> hop;
+    float* pm = nullptr;
+    long long PT = 0, off[8] = {0}, psize[7] = {0};
+    float *x = nullptr, *drive = nullptr, *h0 = nullptr, *gdrive = nullptr, *gz[2] = {nullptr, nullptr};
+    float *lg = nullptr, *dl = nullptr, *part = nullptr, *gwpart = nullptr, *ggp0 = nullptr, *gsp0 = nullptr;
+    float *ginb = nullptr, *ginw = nullptr, *gow_p = nullptr, *gob_p = nullptr, *stats_part = nullptr;
+    float *stats = nullptr, *red = nullptr, *nrm = nullptr;
+    long long adam_t = 0;
+    int B = 0;
+    hipStream_t st = nullptr;
+    std::vector<void*> allocs;
+    Prof prof;
+    float* arr(int set, int i) const { return pm + (long long)set * PT + off[i]; }
+};
+
+// RAII: events before and after the launches of one stage (no-op unless profiling)
+struct Timed {
+    Core& c;
+    int stage;
+    Timed(Core& c_, int s) : c(c_), stage(s) { mark(0); }
+    ~Timed() { mark(1); }
+    void mark(int end) {
+        if (!c.prof.on) return;
+        hipEvent_t e = c.prof.get();
+        if (e && hipEventRecord(e, c.st) == hipSuccess) c.prof.rec.push_back({e, stage * 2 + end});
+    }
+};
+
+// fold the recorded events into per-stage totals (waits for them)
+static bool prof_collect(Core& c) {
+    std::vector<hipEvent_t> open(ST_COUNT, nullptr);
+    bool ok = true;
+    for (auto& r : c.prof.rec) {
+        const int stg = r.second / 2;
+        if (r.second % 2 == 0) { open[stg] = r.first; continue; }
+        if (open[stg]) {
+            float ms = 0.f;
+            if (hipEventSynchronize(r.first) != hipSuccess || hipEventElapsedTime(&ms, open[stg], r.first) != hipSuccess) ok = false;
+            c.prof.ms[stg] += ms;
+            c.prof.n[stg] += 1;
+            c.prof.pool.push_back(open[stg]);
+            open[stg] = nullptr;
+        }
+        c.prof.pool.push_back(r.first);
+    }
+    c.prof.rec.clear();
+    return ok;
+}
+
+enum { SET_P = 0, SET_EMA = 1, SET_M = 2, SET_V = 3, SET_G = 4 };
+
+template <class T>
+static T* dalloc(Core& c, size_t n) {
+    void* p = nullptr;
+    const size_t bytes = std::max<size_t>(n, 1) * sizeof(T);
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        set_error("out of device memory (" + std::to_string(bytes) + " bytes)");
+        return nullptr;
+    }
+    c.allocs.push_back(p);
+    if (hipMemset(p, 0, bytes) != hipSuccess) {
+        set_error("hipMemset failed");
+        return nullptr;
+    }
+    return (T*)p;
+}
+template <class T>
+static T* upload(Core& c, const std::vector<T>& v) {
+    T* p = dalloc<T>(c, v.size());
+    if (p && !v.empty() && hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess) {
+        set_error("hipMemcpy to device failed");
+        return nullptr;
+    }
+    return p;
+}
+static bool upload_plan(Core& c, const HostPlan& h, int rows, long long E, DevPlan& d) {
+    d.rows = rows;
+    d.E = E;
+    d.nseg = (int)h.seg.size();
+    d.nsplit = (int)h.split.size();
+    d.nslot = h.nslot;
+    d.seg = upload(c, h.seg);
+    d.split = upload(c, h.split);
+    return d.seg && d.split;
+}
+
+static void release(Core* c) {
+    if (!c) return;
+    for (auto& r : c->prof.rec) (void)hipEventDestroy(r.first);
+    for (auto e : c->prof.pool) (void)hipEventDestroy(e);
+    for (void* p : c->allocs) (void)hipFree(p);
+    delete c;
+}
+
+// ------------------------------------------------------------------------------------------------ NET.bin
+struct Reader {
+    const unsigned char* p;
+    long long n, at = 0;
+    bool ok = true;
+    std::vector<int> ints(long long k) {
+        std::vector<int> v;
+        if (k < 0 || at + 4 * k > n) {
+            ok = false;
+            return v;
+        }
+        v.resize((size_t)k);
+        if (k) std::memcpy(v.data(), p + at, (size_t)(4 * k));
+        at += 4 * k;
+        return v;
+    }
+};
+
+static bool in_range(const std::vector<int>& v, long long lo, long long hi) {   // lo <= v < hi
+    for (int x : v)
+        if (x < lo || x >= hi) return false;
+    return true;
+}
+static bool rowptr_ok(const std::vector<int>& rp, long long E) {
+    if (rp.empty() || rp[0] != 0 || rp.back() != E) return false;
+    for (size_t i = 1; i < rp.size(); ++i)
+        if (rp[i] < rp[i - 1]) return false;
+    return true;
+}
+static bool distinct(const std::vector<int>& v, long long n, bool skip_negative) {
+    std::vector<unsigned char> seen((size_t)std::max<long long>(n, 1), 0);
+    for (int x : v) {
+        if (x < 0 && skip_negative) continue;
+        if (x < 0 || x >= n || seen[x]) return false;
+        seen[x] = 1;
+    }
+    return true;
+}
+
+static Core* build(const unsigned char* bytes, long long len, int max_batch) {
+    clear_error();
+    if (!bytes || len < 36 || std::memcmp(bytes, "FLY1", 4) != 0) {
+        set_error("not a FLY1 network file");
+        return nullptr;
+    }
+    if (max_batch <= 0) {
+        set_error("max_batch must be positive");
+        return nullptr;
+    }
+    std::unique_ptr<Core, void (*)(Core*)> c(new Core, release);
+    Reader r{bytes, len, 4};
+    auto hd = r.ints(8);
+    if (!r.ok) { set_error("short network file (header)"); return nullptr; }
+    c->obs_dim = hd[0]; c->n_act = hd[1]; c->hops = hd[2]; c->n_neurons = hd[3];
+    c->n_w = hd[4]; c->n_s = hd[5]; c->fan = hd[6]; c->n_dn = hd[7];
+    if (c->obs_dim <= 0 || c->n_act <= 0 || c->hops <= 0 || c->hops > 64 || c->n_neurons <= 0 || c->n_w < 0 ||
+        c->n_s <= 0 || c->fan <= 0 || c->n_dn <= 0) {
+        set_error("bad network header");
+        return nullptr;
+    }
+    const int K = c->hops;
+    c->sizes = r.ints(K + 1);
+    c->E = r.ints(K);
+    if (!r.ok) { set_error("short network file (sizes)"); return nullptr; }
+    if (c->sizes[0] != c->n_s) { set_error("sizes[0] != n_s"); return nullptr; }
+    for (int k = 0; k <= K; ++k)
+        if (c->sizes[k] <= 0) { set_error("empty layer"); return nullptr; }
+    for (int k = 0; k < K; ++k)
+        if (c->E[k] < 0) { set_error("negative edge count"); return nullptr; }
+    c->E_in = c->n_s * c->fan;
+    auto in_crow = r.ints(c->n_s + 1), in_col = r.ints(c->E_in);
+    r.ints(c->obs_dim + 1); r.ints(c->E_in); r.ints(c->E_in);      // the plug's transposed form: not used here
+    auto n0 = r.ints(c->n_s);
+    if (!r.ok) { set_error("short network file (plug)"); return nullptr; }
+    if (!rowptr_ok(in_crow, c->E_in) || !in_range(in_col, 0, c->obs_dim) || !distinct(n0, c->n_neurons, false)) {
+        set_error("bad plug index arrays");
+        return nullptr;
+    }
+    struct HH { std::vector<int> nid, crow, col, widx, tcrow, tcol, twidx, drow; };
+    std::vector<HH> hh(K);
+    for (int k = 0; k < K; ++k) {
+        HH& h = hh[k];
+        const int rows = c->sizes[k + 1], src = c->sizes[k], E = c->E[k];
+        h.nid = r.ints(rows); h.crow = r.ints(rows + 1); h.col = r.ints(E); h.widx = r.ints(E);
+        h.tcrow = r.ints(src + 1); h.tcol = r.ints(E); h.twidx = r.ints(E); h.drow = r.ints(rows);
+        if (!r.ok) { set_error("short network file (hop " + std::to_string(k + 1) + ")"); return nullptr; }
+        bool ok = distinct(h.nid, c->n_neurons, false) && rowptr_ok(h.crow, E) && in_range(h.col, 0, src) &&
+                  distinct(h.widx, c->n_w, false) && rowptr_ok(h.tcrow, E) && in_range(h.tcol, 0, rows) &&
+                  distinct(h.twidx, c->n_w, false) && in_range(h.drow, -1, c->n_s) && distinct(h.drow, c->n_s, true);
+        if (!ok) { set_error("bad index arrays in hop " + std::to_string(k + 1)); return nullptr; }
+    }
+    auto dn = r.ints(c->n_dn);
+    r.ints(c->n_w);                                                 // wmap: the caller's business
+    if (!r.ok) { set_error("short network file (read-out)"); return nullptr; }
+    if (!distinct(dn, c->sizes[K], false)) { set_error("bad read-out rows"); return nullptr; }
+
+    // plans
+    const int bm = (max_batch + TW - 1) / TW * TW;
+    c->maxB = bm;
+    c->Tm = bm / TW;
+    HostPlan hp;
+    if (!make_plan(in_crow.data(), c->n_s, SEG_MAX, hp) || !upload_plan(*c, hp, c->n_s, c->E_in, c->pp)) {
+        if (!*last_error()) set_error("plug plan");
+        return nullptr;
+    }
+    long long max_slot = c->pp.nslot, max_E = 1, max_rows = 1;
+    c->hop.resize(K);
+    for (int k = 0; k < K; ++k) {
+        HopD& d = c->hop[k];
+        HH& h = hh[k];
+        d.rows = c->sizes[k + 1]; d.src = c->sizes[k]; d.E = c->E[k];
+        HostPlan f, b;
+        if (!make_plan(h.crow.data(), d.rows, SEG_MAX, f) || !make_plan(h.tcrow.data(), d.src, SEG_MAX, b)) {
+            set_error("row plan");
+            return nullptr;
+        }
+        if (!upload_plan(*c, f, d.rows, d.E, d.fp) || !upload_plan(*c, b, d.src, d.E, d.bp)) return nullptr;
+        d.has_drive = std::any_of(h.drow.begin(), h.drow.end(), [](int v) { return v >= 0; });
+        d.nid = upload(*c, h.nid); d.crow = upload(*c, h.crow); d.col = upload(*c, h.col); d.widx = upload(*c, h.widx);
+        d.tcrow = upload(*c, h.tcrow); d.tcol = upload(*c, h.tcol); d.twidx = upload(*c, h.twidx);
+        d.drow = upload(*c, h.drow);
+        d.cw = dalloc<int2>(*c, d.E);
+        d.tcw = dalloc<int2>(*c, d.E);
+        if (!d.nid || !d.crow || !d.col || !d.widx || !d.tcrow || !d.tcol || !d.twidx || !d.drow || !d.cw || !d.tcw)
+            return nullptr;
+        max_slot = std::max<long long>({max_slot, d.fp.nslot, d.bp.nslot});
+        max_E = std::max<long long>(max_E, d.E);
+        max_rows = std::max<long long>(max_rows, d.rows);
+    }
+    std::vector<int> dn_inv(c->sizes[K], -1);
+    for (int j = 0; j < c->n_dn; ++j) dn_inv[dn[j]] = j;
+    c->in_crow = upload(*c, in_crow); c->in_col = upload(*c, in_col); c->n0 = upload(*c, n0);
+    c->dn = upload(*c, dn); c->dn_inv = upload(*c, dn_inv);
+    c->in_cw = dalloc<int2>(*c, c->E_in);
+    if (!c->in_crow || !c->in_col || !c->n0 || !c->dn || !c->dn_inv || !c->in_cw) return nullptr;
+
+    // parameters: 5 sets x 7 arrays
+    const long long ps[7] = {c->n_w, c->n_neurons, c->n_neurons, c->E_in, c->n_s, (long long)c->n_act * c->n_dn, c->n_act};
+    long long o = 0;
+    for (int i = 0; i < 7; ++i) {
+        c->psize[i] = ps[i];
+        c->off[i] = o;
+        o += (ps[i] + 63) / 64 * 64;
+    }
+    c->off[7] = o;
+    c->PT = o;
+    c->pm = dalloc<float>(*c, (size_t)(5 * o));
+    if (!c->pm) return nullptr;
+
+    // states and partial sums
+    const size_t Tm = c->Tm, S = TW;
+    c->x = dalloc<float>(*c, Tm * c->obs_dim * S);
+    c->drive = dalloc<float>(*c, Tm * c->n_s * S);
+    c->h0 = dalloc<float>(*c, Tm * c->n_s * S);
+    c->gdrive = dalloc<float>(*c, Tm * c->n_s * S);
+    c->gz[0] = dalloc<float>(*c, Tm * max_rows * S);
+    c->gz[1] = dalloc<float>(*c, Tm * max_rows * S);
+    for (auto& d : c->hop) {
+        d.z = dalloc<float>(*c, Tm * d.rows * S);
+        d.h = dalloc<float>(*c, Tm * d.rows * S);
+        d.ggp = dalloc<float>(*c, Tm * d.rows);
+        d.gsp = dalloc<float>(*c, Tm * d.rows);
+        if (!d.z || !d.h || !d.ggp || !d.gsp) return nullptr;
+    }
+    c->lg = dalloc<float>(*c, (size_t)bm * c->n_act);
+    c->dl = dalloc<float>(*c, (size_t)bm * c->n_act);
+    c->part = dalloc<float>(*c, Tm * std::max<long long>(max_slot, 1) * S);
+    c->gwpart = dalloc<float>(*c, Tm * max_E);
+    c->ggp0 = dalloc<float>(*c, Tm * c->n_s);
+    c->gsp0 = dalloc<float>(*c, Tm * c->n_s);
+    c->ginb = dalloc<float>(*c, Tm * c->n_s);
+    c->ginw = dalloc<float>(*c, Tm * c->E_in);
+    c->gow_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act * c->n_dn);
+    c->gob_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act);
+    c->stats_part = dalloc<float>(*c, (size_t)2 * ((bm + WG - 1) / WG));
+    c->stats = dalloc<float>(*c, 4);
+    c->red = dalloc<float>(*c, 1024);
+    c->nrm = dalloc<float>(*c, 1);
+    if (!c->x || !c->drive || !c->h0 || !c->gdrive || !c->gz[0] || !c->gz[1] || !c->lg || !c->dl || !c->part ||
+        !c->gwpart || !c->ggp0 || !c->gsp0 || !c->ginb || !c->ginw || !c->gow_p || !c->gob_p || !c->stats_part ||
+        !c->stats || !c->red || !c->nrm)
+        return nullptr;
+    if (hipDeviceSynchronize() != hipSuccess) { set_error("device error after set-up"); return nullptr; }
+    return c.release();
+}
+
+static bool check_batch(const Core* c, int B) {
+    if (!c) { set_error("null handle"); return false; }
+    if (B <= 0 || B % TW != 0 || B > c->maxB) {
+        set_error("batch " + std::to_string(B) + " must be a positive multiple of 32 and at most " + std::to_string(c->maxB));
+        return false;
+    }
+    return true;
+}
+
+// ------------------------------------------------------------------------------------------------ passes
+static bool forward(Core& c, const float* obs, int B, float* logits, int set) {
+    const int T = B / TW;
+    hipStream_t st = c.st;
+    { Timed t(c, ST_OBS); FG_CHECK(launch_obs_in(obs, c.x, c.obs_dim, B, st), false); }
+    const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
+    {
+        Timed t(c, ST_PACK);
+        FG_CHECK(launch_pack(c.in_col, nullptr, c.arr(set, 3), c.in_cw, c.E_in, st), false);
+        for (auto& d : c.hop) FG_CHECK(launch_pack(d.col, d.widx, W, d.cw, d.E, st), false);
+    }
+    FwdEpi e0;
+    e0.bias = c.arr(set, 4);
+    e0.nid = c.n0; e0.gain = gain; e0.theta = theta;
+    e0.z = c.drive; e0.lz = tiled(c.n_s);
+    e0.h = c.h0; e0.lh = tiled(c.n_s);
+    { Timed t(c, ST_PLUG); FG_CHECK(launch_fwd(c.pp.view(), c.in_cw, c.x, tiled(c.obs_dim), e0, c.part, tiled(c.pp.nslot), T, st), false); }
+    const float* hp = c.h0;
+    int hk = 0;
+    for (auto& d : c.hop) {
+        FwdEpi e;
+        if (d.has_drive) { e.drow = d.drow; e.drive = c.drive; e.ldrive = tiled(c.n_s); }
+        e.nid = d.nid; e.gain = gain; e.theta = theta;
+        e.z = d.z; e.lz = tiled(d.rows);
+        e.h = d.h; e.lh = tiled(d.rows);
+        { Timed t(c, ST_HOP + std::min(hk, 7)); FG_CHECK(launch_fwd(d.fp.view(), d.cw, hp, tiled(d.src), e, c.part, tiled(d.fp.nslot), T, st), false); }
+        hp = d.h;
+        ++hk;
+    }
+    {
+        Timed t(c, ST_LOGITS);
+        FG_CHECK(launch_logits(hp, tiled(c.sizes[c.hops]), c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, logits, B, st),
+                 false);
+    }
+    c.B = B;
+    return true;
+}
+
+static bool backward(Core& c, const float* dlogits, int B) {
+    const int T = B / TW, K = c.hops;
+    hipStream_t st = c.st;
+    const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
+    float* G[7];
+    for (int i = 0; i < 7; ++i) G[i] = c.arr(SET_G, i);
+    { Timed t(c, ST_ZERO); FG_CHECK(launch_fill(c.gdrive, 0.f, (long long)T * c.n_s * TW, st), false); }
+    {
+        Timed t(c, ST_PACK);
+        for (auto& d : c.hop) FG_CHECK(launch_pack(d.tcol, d.twidx, W, d.tcw, d.E, st), false);
+    }
+
+    HopD& top = c.hop[K - 1];
+    BwdEpi et;
+    et.mode = 1;
+    et.h = top.h; et.lh = tiled(top.rows);
+    et.z = top.z; et.lz = tiled(top.rows);
+    et.nid = top.nid; et.gain = gain;
+    et.drow = top.has_drive ? top.drow : nullptr;
+    et.gz_out = c.gz[0]; et.lgz = tiled(top.rows);
+    et.gdrive = c.gdrive; et.lgd = tiled(c.n_s);
+    et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
+    {
+        Timed t(c, ST_RBWD);
+        FG_CHECK(launch_readout_bwd_h(dlogits, c.arr(SET_P, 5), c.dn_inv, c.n_dn, c.n_act, top.rows, et, B, st), false);
+        FG_CHECK(launch_readout_bwd_w(dlogits, top.h, tiled(top.rows), c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st), false);
+    }
+    const int nch = readout_chunks(B);
+    {
+        Timed t(c, ST_REDUCE);
+        FG_CHECK(launch_reduce(c.gow_p, (long long)c.n_act * c.n_dn, (long long)c.n_act * c.n_dn, nch, nullptr, nullptr, G[5], st), false);
+        FG_CHECK(launch_reduce(c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], st), false);
+        FG_CHECK(launch_reduce(top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1], st), false);
+        FG_CHECK(launch_reduce(top.gsp, top.rows, top.rows, T, top.nid, theta, G[2], st), false);
+    }
+
+    int cur = 0;
+    for (int k = K; k >= 1; --k) {
+        HopD& d = c.hop[k - 1];
+        BwdEpi e;
+        e.gdrive = c.gdrive; e.lgd = tiled(c.n_s);
+        e.gain = gain;
+        const float* hbelow;
+        int rows_below;
+        float *ggp, *gsp;
+        const int* nid_below;
+        if (k >= 2) {
+            HopD& b = c.hop[k - 2];
+            e.mode = 1;
+            e.h = b.h; e.lh = tiled(b.rows);
+            e.z = b.z; e.lz = tiled(b.rows);
+            e.nid = b.nid;
+            e.drow = b.has_drive ? b.drow : nullptr;
+            e.gz_out = c.gz[cur ^ 1]; e.lgz = tiled(b.rows);
+            hbelow = b.h; rows_below = b.rows; ggp = b.ggp; gsp = b.gsp; nid_below = b.nid;
+        } else {
+            e.mode = 2;
+            e.h = c.h0; e.lh = tiled(c.n_s);
+            e.z = c.drive; e.lz = tiled(c.n_s);
+            e.nid = c.n0;
+            e.in_crow = c.in_crow; e.in_cw = c.in_cw; e.x = c.x; e.lx = tiled(c.obs_dim);
+            e.ginb_part = c.ginb; e.gb_ld = c.n_s;
+            e.ginw_part = c.ginw; e.gw_ld = c.E_in;
+            hbelow = c.h0; rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
+        }
+        e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
+        {
+            Timed t(c, ST_BHOP + std::min(k - 1, 7));
+            FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), hbelow, tiled(rows_below), c.gwpart, d.E, e,
+                                c.part, tiled(d.bp.nslot), T, st), false);
+        }
+        Timed t(c, ST_REDUCE);
+        FG_CHECK(launch_reduce(c.gwpart, d.E, d.E, T, d.twidx, nullptr, G[0], st), false);
+        FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
+        FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
+        if (k == 1) {
+            FG_CHECK(launch_reduce(c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], st), false);
+            FG_CHECK(launch_reduce(c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], st), false);
+        }
+        cur ^= 1;
+    }
+    return true;
+}
+
+static float grad_norm(Core& c) {
+    if (launch_sumsq(c.arr(SET_G, 0), c.PT, c.red, c.nrm, c.st) != hipSuccess) { set_error("grad norm launch"); return -1.f; }
+    float ss = 0.f;
+    FG_CHECK(hipMemcpyAsync(&ss, c.nrm, 4, hipMemcpyDeviceToHost, c.st), -1.f);
+    FG_CHECK(hipStreamSynchronize(c.st), -1.f);
+    return sqrtf(ss);
+}
+
+static float step(Core& c, float lr, float lr_neuron, float lr_plug, float max_norm, float ema) {
+    float g = 0.f;
+    if (max_norm > 0.f) {
+        g = grad_norm(c);
+        if (g < 0.f) return -1.f;
+    }
+    const float gs = (max_norm > 0.f && g > max_norm) ? max_norm / g : 1.f;
+    ++c.adam_t;
+    const long long t = std::min<long long>(c.adam_t, 100000);
+    const float c1 = 1.f - (float)std::pow(0.9, (double)t), c2 = 1.f - (float)std::pow(0.999, (double)t);
+    AdamSeg s;
+    for (int i = 0; i < 8; ++i) s.off[i] = c.off[i];
+    for (int i = 0; i < 7; ++i) s.lr[i] = i == 0 ? lr : (i <= 2 ? lr_neuron : lr_plug);
+    Timed tm(c, ST_ADAM);
+    hipError_t e = launch_adam(c.arr(SET_P, 0), c.arr(SET_G, 0), c.arr(SET_M, 0), c.arr(SET_V, 0), c.arr(SET_EMA, 0), s,
+                               c1, c2, nullptr, gs, ema, c.st);
+    if (e != hipSuccess) { set_error(std::string("adam: ") + hipGetErrorString(e)); return -1.f; }
+    return g;
+}
+
+}  // namespace fg
+
+using namespace fg;
+
+// ================================================================================================ C-ABI
+extern "C" {
+
+const char* fc_last_error(void) { return fg::last_error(); }
+void fc_clear_error(void) { fg::clear_error(); }
+
+void* fc_create_from_memory(const void* net_bytes, long long len, int max_batch) {
+    return build((const unsigned char*)net_bytes, len, max_batch);
+}
+
+void* fc_create(const char* net_path, int max_batch) {
+    clear_error();
+    FILE* f = net_path ? fopen(net_path, "rb") : nullptr;
+    if (!f) { set_error(std::string("cannot open ") + (net_path ? net_path : "(null)")); return nullptr; }
+    std::vector<unsigned char> buf;
+    unsigned char tmp[1 << 16];
+    size_t k;
+    while ((k = fread(tmp, 1, sizeof tmp, f)) > 0) buf.insert(buf.end(), tmp, tmp + k);
+    fclose(f);
+    return build(buf.data(), (long long)buf.size(), max_batch);
+}
+
+void fc_free(void* h) { release((Core*)h); }
+
+void fc_set_stream(void* h, void* stream) {
+    if (h) ((Core*)h)->st = (hipStream_t)stream;
+}
+
+void fc_sizes(void* h, long long* out) {
+    Core* c = (Core*)h;
+    if (!c || !out) { set_error("null argument"); return; }
+    for (int i = 0; i < 7; ++i) out[i] = c->psize[i];
+    out[7] = c->obs_dim; out[8] = c->n_act; out[9] = c->maxB;
+}
+
+void fc_copy(void* h, int which, int to_core, float** ptrs) {
+    Core* c = (Core*)h;
+    if (!c || !ptrs || which < 0 || which > 4) { set_error("fc_copy: bad argument"); return; }
+    for (int i = 0; i < 7; ++i) {
+        if (!ptrs[i]) continue;
+        float* lib = c->arr(which, i);
+        FG_CHECK(hipMemcpyAsync(to_core ? lib : ptrs[i], to_core ? ptrs[i] : lib, c->psize[i] * 4, hipMemcpyDeviceToDevice,
+                                c->st), );
+    }
+    FG_CHECK(hipStreamSynchronize(c->st), );
+}
+
+void fc_forward(void* h, const float* obs, int B, float* logits, int ema) {
+    Core* c = (Core*)h;
+    if (!check_batch(c, B)) return;
+    if (!obs || !logits) { set_error("fc_forward: null pointer"); return; }
+    forward(*c, obs, B, logits, ema ? SET_EMA : SET_P);
+}
+
+void fc_zero_grad(void* h) {
+    Core* c = (Core*)h;
+    if (!c) { set_error("null handle"); return; }
+    FG_CHECK(launch_fill(c->arr(SET_G, 0), 0.f, c->PT, c->st), );
+}
+
+void fc_backward(void* h, const float* dlogits, int B) {
+    Core* c = (Core*)h;
+    if (!check_batch(c, B)) return;
+    if (!dlogits) { set_error("fc_backward: null pointer"); return; }
+    if (B != c->B) { set_error("fc_backward: batch differs from the last forward's"); return; }
+    backward(*c, dlogits, B);
+}
+
+float fc_grad_norm(void* h) {
+    Core* c = (Core*)h;
+    if (!c) { set_error("null handle"); return -1.f; }
+    return grad_norm(*c);
+}
+
+float fc_step(void* h, float lr, float lr_neuron, float lr_plug, float max_norm, float ema) {
+    Core* c = (Core*)h;
+    if (!c) { set_error("null handle"); return -1.f; }
+    return step(*c, lr, lr_neuron, lr_plug, max_norm, ema);
+}
+
+long long fc_adam_t(void* h, long long set) {
+    Core* c = (Core*)h;
+    if (!c) { set_error("null handle"); return -1; }
+    if (set >= 0) c->adam_t = set;
+    return c->adam_t;
+}
+
+void fc_sync(void*) { FG_CHECK(hipDeviceSynchronize(), ); }
+
+void fc_kl_loss(void* h, const float* logits, const float* teacher, int B, float it, float* dlogits, float* stats) {
+    Core* c = (Core*)h;
+    if (!c || !logits || !teacher || !dlogits || !stats || B <= 0 || B > c->maxB) { set_error("fc_kl_loss: bad argument"); return; }
+    FG_CHECK(launch_loss(logits, teacher, dlogits, c->stats_part, stats, c->n_act, B, it, c->st), );
+}
+
+float fc_teach_step(void* h, const float* obs, const float* teacher, int B, float it, float lr, float lr_neuron,
+                    float lr_plug, float max_norm, float ema, float* stats) {
+    Core* c = (Core*)h;
+    if (!check_batch(c, B)) return -1.f;
+    if (!obs || !teacher) { set_error("fc_teach_step: null pointer"); return -1.f; }
+    { Timed t(*c, ST_ZERO); FG_CHECK(launch_fill(c->arr(SET_G, 0), 0.f, c->PT, c->st), -1.f); }
+    if (!forward(*c, obs, B, c->lg, SET_P)) return -1.f;
+    {
+        Timed t(*c, ST_LOSS);
+        FG_CHECK(launch_loss(c->lg, teacher, c->dl, c->stats_part, stats ? stats : c->stats, c->n_act, B, it, c->st), -1.f);
+    }
+    if (!backward(*c, c->dl, B)) return -1.f;
+    return step(*c, lr, lr_neuron, lr_plug, max_norm, ema);
+}
+
+void fc_export_state(void* h, int layer, int what, float* dst, int B) {
+    Core* c = (Core*)h;
+    if (!check_batch(c, B) || !dst || what < 0 || what > 2 || layer < 0 || layer > (c ? c->hops : 0)) {
+        if (!*last_error()) set_error("fc_export_state: bad argument");
+        return;
+    }
+    const float* src;
+    int rows;
+    if (what == 2) { src = c->x; rows = c->obs_dim; }
+    else if (layer == 0) { src = what == 0 ? c->h0 : c->drive; rows = c->n_s; }
+    else { const HopD& d = c->hop[layer - 1]; src = what == 0 ? d.h : d.z; rows = d.rows; }
+    FG_CHECK(launch_export(src, tiled(rows), dst, rows, B, c->st), );
+}
+
+void fc_profile(void* h, int on) {
+    Core* c = (Core*)h;
+    if (!c) { set_error("null handle"); return; }
+    if (!on && c->prof.on) prof_collect(*c);
+    c->prof.on = on != 0;
+}
+
+int fc_profile_read(void* h, double* ms, long long* counts, int n, int reset) {
+    Core* c = (Core*)h;
+    if (!c || n < 0) { set_error("fc_profile_read: bad argument"); return -1; }
+    if (!prof_collect(*c)) { set_error("fc_profile_read: event error"); return -1; }
+    for (int i = 0; i < n && i < ST_COUNT; ++i) {
+        if (ms) ms[i] = c->prof.ms[i];
+        if (counts) counts[i] = c->prof.n[i];
+    }
+    if (reset)
+        for (int i = 0; i < ST_COUNT; ++i) { c->prof.ms[i] = 0; c->prof.n[i] = 0; }
+    return ST_COUNT;
+}
+
+int fc_plan_segments(const int* rowptr, int rows, int seg_max, int* seg_out, long long seg_cap, int* split_out,
+                     long long split_cap, long long* counts) {
+    HostPlan p;
+    if (!rowptr || !make_plan(rowptr, rows, seg_max, p)) { set_error("fc_plan_segments: malformed row pointer"); return -1; }
+    if (counts) { counts[0] = (long long)p.seg.size(); counts[1] = (long long)p.split.size(); counts[2] = p.nslot; }
+    if ((long long)p.seg.size() > seg_cap || (long long)p.split.size() > split_cap) { set_error("fc_plan_segments: capacity"); return -1; }
+    if (seg_out && !p.seg.empty()) std::memcpy(seg_out, p.seg.data(), p.seg.size() * sizeof(int4));
+    if (split_out && !p.split.empty()) std::memcpy(split_out, p.split.data(), p.split.size() * sizeof(int4));
+    return 0;
+}
+
+}  // extern "C"

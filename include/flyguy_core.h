@@ -1,0 +1,133 @@
+/* flyguy MI355X library: the C-ABI of the fly actor's batched forward, backward, KL loss and Adam on one GPU.
+ *
+ * Drop-in for the reference's FLYGUY_CORE library (flyguy/native/flyguy_train.cu:553-629, loaded by
+ * flyguy/fly_native.py:34,127-159 through ctypes).  The ten fc_* functions of the reference keep their names,
+ * argument meaning and ownership rules; the functions after them are additions, each marked as such.
+ *
+ * Conventions (as in the reference):
+ *   - all float pointers passed in or out are DEVICE pointers owned by the caller (PyTorch tensors), fp32,
+ *     row-major: obs [B][obs_dim], logits / dlogits / teacher logits [B][n_act];
+ *   - B is a multiple of 32 and at most the max_batch given to fc_create (fly_native.py:53,200);
+ *   - the seven weight arrays are, in this order: W (strengths in play, n_w), gain (n_neurons),
+ *     theta (n_neurons), in_w (n_s * fan), in_b (n_s), out_w (n_act * n_dn, row = action), out_b (n_act);
+ *   - work runs on one HIP stream (the null stream unless fc_set_stream names another), in call order.
+ * Errors: where the reference prints and ends the process (flyguy_train.cu:47), this library records a message,
+ * skips the work and returns (NULL / 0 / -1 where the function returns something); fc_last_error() reads it.
+ * Arguments are checked before any kernel is launched (sizes, B, and every index array read from NET.bin).
+ */
+#ifndef FLYGUY_CORE_H
+#define FLYGUY_CORE_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Reads NET.bin ("FLY1", written by export.write_net, flyguy/native/export.py:52-65) and allocates every device
+ * buffer for batches up to max_batch.  Replaces fc_create, flyguy_train.cu:569-575.  NULL on error. */
+void* fc_create(const char* net_path, int max_batch);
+
+/* out[0..6]: lengths of the seven weight arrays; out[7..9]: obs_dim, n_act, max_batch.
+ * Replaces fc_sizes, flyguy_train.cu:577-581. */
+void fc_sizes(void* core, long long* out);
+
+/* Copies the seven arrays of one set between the library and seven caller device arrays (NULL = skip).
+ * which: 0 weights, 1 running average (EMA), 2 Adam m, 3 Adam v, 4 gradient; to_core 1: caller -> library,
+ * 0: library -> caller.  Synchronous.  Replaces fc_copy, flyguy_train.cu:584-589. */
+void fc_copy(void* core, int which, int to_core, float** ptrs);
+
+/* obs [B][obs_dim] -> logits [B][n_act] with the weights (ema 0) or their running average (ema 1); the states
+ * stay in the library for fc_backward.  Replaces fc_forward, flyguy_train.cu:592-598. */
+void fc_forward(void* core, const float* obs, int B, float* logits, int ema);
+
+/* Sets the gradient of all seven arrays to zero.  Replaces fc_zero_grad, flyguy_train.cu:599-602. */
+void fc_zero_grad(void* core);
+
+/* dlogits [B][n_act]: gradient of the loss w.r.t. the logits of the last fc_forward(..., ema 0); the weights'
+ * gradients are ADDED to the library's.  Replaces fc_backward, flyguy_train.cu:604-609. */
+void fc_backward(void* core, const float* dlogits, int B);
+
+/* Length of the gathered gradient (all seven arrays).  Replaces fc_grad_norm, flyguy_train.cu:610-616. */
+float fc_grad_norm(void* core);
+
+/* One Adam step (beta 0.9 / 0.999, eps 1e-8, bias corrections with t capped at 100000) with rate lr for W,
+ * lr_neuron for gain and theta, lr_plug for the plugs; the gradient is first scaled down to max_norm when it is
+ * longer (0: no limit); the running average follows with decay `ema`.  Returns the gradient's length before
+ * scaling (0 when max_norm is 0).  Replaces fc_step, flyguy_train.cu:619-627. */
+float fc_step(void* core, float lr, float lr_neuron, float lr_plug, float max_norm, float ema);
+
+/* Adam's step count: set >= 0 sets it; returns the count.  Replaces fc_adam_t, flyguy_train.cu:628. */
+long long fc_adam_t(void* core, long long set);
+
+/* Waits for the device.  Replaces fc_sync, flyguy_train.cu:629. */
+void fc_sync(void* core);
+
+/* ---- additions (no counterpart in the reference's library) ---- */
+
+/* The last error message of the calling thread ("" if none); fc_clear_error() forgets it. */
+const char* fc_last_error(void);
+void fc_clear_error(void);
+
+/* fc_create from NET.bin bytes already in memory (len bytes). */
+void* fc_create_from_memory(const void* net_bytes, long long len, int max_batch);
+
+/* Frees every buffer of the handle (the reference's handles live until the process ends). */
+void fc_free(void* core);
+
+/* Runs the library's work on this HIP stream (hipStream_t; NULL = the null stream) from now on. */
+void fc_set_stream(void* core, void* stream);
+
+/* KL(teacher || student) over n_act actions for a batch: logits and teacher [B][n_act] device arrays,
+ * it = 1 / temperature of the teacher; writes dlogits [B][n_act] = d(mean KL)/d logits and stats[0] = sum of
+ * the per-sample KL, stats[1] = number of samples whose argmax agrees (first maximum wins).  The trainer's
+ * k_loss, flyguy_train.cu:104-123, as a function of its own. */
+void fc_kl_loss(void* core, const float* logits, const float* teacher, int B, float it, float* dlogits, float* stats);
+
+/* One teaching step as the standalone trainer's loop does it (flyguy_train.cu:361-365 then 758-764):
+ * zero the gradient, forward on obs, KL loss against teacher (it as above), backward, Adam step.  stats (device,
+ * 2 floats, or NULL) receives the loss sums as in fc_kl_loss.  Returns what fc_step returns. */
+float fc_teach_step(void* core, const float* obs, const float* teacher, int B, float it, float lr, float lr_neuron,
+                    float lr_plug, float max_norm, float ema, float* stats);
+
+/* Copies an internal state of the last forward to dst [rows][B] (device): layer 0 is the sensory layer,
+ * layer k the output of hop k; what 0: h (firing), 1: z (input before the neuron; layer 0: the drive),
+ * 2: the observation batch x [obs_dim][B] (layer ignored).  For tests and diagnostics. */
+void fc_export_state(void* core, int layer, int what, float* dst, int B);
+
+/* Profiling: with on = 1 every stage of the library's work is bracketed by HIP events on its stream.
+ * fc_profile_read waits for the recorded events and writes, per stage, the summed milliseconds and the number of
+ * timed runs (reset != 0 clears the totals); returns the number of stages (25) or -1.  Stages: 0 observation
+ * transpose, 1 (index, weight) packing, 2 plug + sensory layer, 3+k forward of hop k+1, 11 read-out, 12 loss,
+ * 13 read-out backward, 14+k backward of hop k+1, 22 gradient reductions, 23 Adam, 24 zeroing.  The reference
+ * timed its library from Python (flyguy/native/rl_profile.py:49-86). */
+void fc_profile(void* core, int on);
+int fc_profile_read(void* core, double* ms, long long* counts, int n, int reset);
+
+/* The row plan of one sparse product, computed on the host (no device needed): every row is cut into segments
+ * of at most seg_max edges, sorted longest first (ties: row, then segment order).  rowptr has rows+1 entries.
+ * seg_out receives 4 ints per segment {row, begin, end, slot} (slot -1: the whole row, else the index of its
+ * partial sum), split_out 4 ints per split row {row, first slot, segments, 0}.  counts[0..2] = segments, split
+ * rows, slots.  Returns 0, or -1 if the capacities are too small or rowptr is malformed. */
+int fc_plan_segments(const int* rowptr, int rows, int seg_max, int* seg_out, long long seg_cap, int* split_out,
+                     long long split_cap, long long* counts);
+
+/* ---- the HopCuda-style hop (flyguy/fly_cuda.py:78-115): states [rows][B] row-major, B % 32 == 0 ---- */
+
+/* out[n_rows][B] = A h, A in CSR form: rowptr (int64, n_rows+1), col (int32), w (E entries).  plan: int4 segments of
+ * rowptr from fc_plan_segments (nseg of them, nsplit split rows after them in split); cw: scratch for E (col,w)
+ * pairs; scratch: partial sums, nslot * B floats.  All device.  Replaces the spmm_f kernel, fly_cuda.py:27-33. */
+void fh_spmm(const long long* rowptr, const int* col, const float* w, const float* h, float* out, int n_rows,
+             int n_src, int B, long long E, const int* plan, int nseg, const int* split, int nsplit, int nslot, void* cw,
+             float* scratch, void* stream);
+
+/* Backward of fh_spmm: gh[n_src][B] = A^T gz and gw[tperm[e]] += sum_b gz[row_e][b] h[col_e][b] (gw is added to),
+ * from the transposed (CSC) form tcrow (int64, n_src+1) / tcol (int32) / tperm (int64, CSC position -> edge).
+ * plan / split / nslot: fc_plan_segments of tcrow; cw: scratch for E pairs; gwpart: scratch of E * B/32 floats;
+ * scratch: nslot * B floats.  Replaces sddmm_f + spmm_f over the CSC, fly_cuda.py:45-50,93-115. */
+void fh_spmm_bwd(const long long* tcrow, const int* tcol, const long long* tperm, const float* w, const float* gz,
+                 const float* h, float* gh, float* gw, int n_rows, int n_src, int B, long long E, const int* plan,
+                 int nseg, const int* split, int nsplit, int nslot, void* cw, float* gwpart, float* scratch, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

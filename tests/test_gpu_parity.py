@@ -1,0 +1,137 @@
+"""Parity of the MI355X library with the oracle, through the C-ABI (fc_*).
+
+Tolerances (from the target: fp32 logits within 1e-5 relative, weight gradients within 1e-4 relative, argmax
+identical), relative to the largest entry as flyguy/native/core_check.py:59 measures:
+  logits and every internal state vs the float64 oracle   <= 1e-5
+  logits vs the float32 oracle (the reference's arithmetic) <= 1e-6  (rows split over several waves are summed
+                                                                      in pieces; softplus may differ by an ulp)
+  each of the seven gradient arrays vs the float64 oracle    <= 1e-4
+  argmax identical wherever the top-2 margin exceeds 1e-4.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import CASES, lively, toy
+from flyguy_amd.export import net_bytes, params_from_torch, structure
+from flyguy_amd.fly import FlyActor
+from flyguy_amd.synth import scaled_3hop, synth_3hop
+from gpu_helpers import NAMES, Core, argmax_agrees, rel, say
+from oracle.oracle import Oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def toy_net(name, hops, fan, seed=0):
+    torch.manual_seed(seed)
+    f = lively(FlyActor(toy(name), 517, 90, hops=hops, fan=fan), seed)
+    s = structure(f)
+    return s, params_from_torch(f, s)
+
+
+def check_forward(s, params, obs, core=None, states=True):
+    core = core or Core(s, params, max_batch=obs.shape[0])
+    got = core.forward(obs)
+    o64 = Oracle(net_bytes(s), params, "f64")
+    o32 = Oracle(net_bytes(s), params, "f32")
+    want = o64.forward(obs)
+    w32 = o32.forward(obs)
+    assert np.isfinite(got).all()
+    assert rel(got, want) <= 1e-5, rel(got, want)
+    assert rel(got, w32) <= 1e-6, rel(got, w32)
+    ok, ties = argmax_agrees(got, want)
+    assert ok
+    if states:
+        B = obs.shape[0]
+        for layer in range(s["hops"] + 1):
+            rows = s["sizes"][layer]
+            for what in (0, 1):
+                g = core.state(layer, what, rows, B)
+                w = o64.state(layer, what, rows)
+                assert rel(g, w) <= 1e-5, (layer, what, rel(g, w))
+    return core, o64, got, want
+
+
+def check_backward(core, o64, s, logits, seed=1):
+    rng = np.random.default_rng(seed)
+    R = rng.standard_normal(logits.shape).astype(np.float32)
+    dl = (R + 0.2 * logits).astype(np.float32)
+    core.zero_grad()
+    core.backward(dl)
+    got = core.get(4)
+    want = o64.backward(dl)
+    for name, g, w in zip(NAMES, got, want):
+        r = rel(g, w)
+        say(f"      grad {name:6s} rel {r:.2e} (max {np.abs(w).max():.2e})")
+        assert r <= 1e-4, (name, r)
+
+
+@pytest.mark.parametrize("name,hops,fan", CASES)
+def test_toy_forward_backward(gpu_lib, name, hops, fan):
+    say(f"toy {name} hops {hops} fan {fan}")
+    s, params = toy_net(name, hops, fan)
+    obs = np.random.default_rng(0).standard_normal((64, 517)).astype(np.float32)
+    core, o64, got, _ = check_forward(s, params, obs)
+    check_backward(core, o64, s, got)
+
+
+@pytest.mark.parametrize("B", [32, 96, 256])
+def test_scaled_synthetic(gpu_lib, B):
+    """The 3-hop shape at 1/16 size: heavy rows split over several waves, re-drive rows, B not a multiple of 256."""
+    say(f"scaled synthetic 1/16, B {B}")
+    s, params = scaled_3hop(16)
+    assert max(int(np.diff(h["crow"]).max()) for h in s["hop"]) > 256        # split rows are exercised
+    obs = np.random.default_rng(B).standard_normal((B, 517)).astype(np.float32)
+    core, o64, got, _ = check_forward(s, params, obs)
+    check_backward(core, o64, s, got)
+
+
+@pytest.fixture(scope="module")
+def full():
+    return synth_3hop()
+
+
+def test_full_size_against_oracle(gpu_lib, full):
+    """The benchmark network (70k neurons in 3 hops, 2,992,734 strengths) at B = 64."""
+    s, params = full
+    say("full-size synthetic, B 64: forward")
+    obs = np.random.default_rng(7).standard_normal((64, 517)).astype(np.float32)
+    core, o64, got, _ = check_forward(s, params, obs, states=True)
+    say("full-size synthetic, B 64: backward")
+    check_backward(core, o64, s, got)
+
+
+def test_full_size_batch_independence(gpu_lib, full):
+    """At the benchmark batch (4096) every sample's logits are bit-identical to the same sample run in a batch of
+    32: a sample's arithmetic does not depend on the batch around it or on the tile it lands in."""
+    s, params = full
+    say("full-size synthetic, B 4096 vs 32")
+    core = Core(s, params, max_batch=4096)
+    obs = np.random.default_rng(11).standard_normal((4096, 517)).astype(np.float32)
+    big = core.forward(obs)
+    for start in (0, 1024, 4064):
+        small = core.forward(obs[start:start + 32])
+        assert np.array_equal(small, big[start:start + 32]), start
+    perm = np.random.default_rng(1).permutation(4096)
+    assert np.array_equal(core.forward(obs[perm]), big[perm])
+
+
+def test_gradients_add_up_over_pieces(gpu_lib, full):
+    """fc_backward ADDS: two half batches give the gradient of the whole batch (to rounding)."""
+    s, params = full
+    core = Core(s, params, max_batch=512)
+    obs = np.random.default_rng(5).standard_normal((512, 517)).astype(np.float32)
+    R = np.random.default_rng(6).standard_normal((512, 90)).astype(np.float32)
+    core.zero_grad()
+    core.forward(obs)
+    core.backward(R)
+    whole = core.get(4)
+    core.zero_grad()
+    for i in (0, 256):
+        core.forward(obs[i:i + 256])
+        core.backward(R[i:i + 256])
+    halves = core.get(4)
+    for name, a, b in zip(NAMES, halves, whole):
+        assert rel(a, b) <= 1e-5, name

@@ -1,0 +1,71 @@
+"""The C-ABI library loads on a machine without a GPU, exports every function include/flyguy_core.h declares,
+and refuses malformed network files before it touches the device."""
+from __future__ import annotations
+
+import ctypes
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, toy
+from flyguy_amd._lib import LIB_PATH, lib
+from flyguy_amd.export import net_bytes, structure
+from flyguy_amd.fly import FlyActor
+
+
+def declared() -> list[str]:
+    text = (ROOT / "include" / "flyguy_core.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(f[ch]_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared()
+    assert len(names) >= 20 and "fc_forward" in names and "fh_spmm_bwd" in names
+    L = ctypes.CDLL(str(LIB_PATH))
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_reference_entry_points_present():
+    # the ten functions the reference's library exports (flyguy/native/flyguy_train.cu:569-629)
+    for n in ("fc_create", "fc_sizes", "fc_copy", "fc_forward", "fc_zero_grad", "fc_backward", "fc_grad_norm",
+              "fc_step", "fc_adam_t", "fc_sync"):
+        assert n in declared()
+
+
+def _bad(raw: bytes) -> str:
+    L = lib()
+    h = L.fc_create_from_memory(raw, len(raw), 64)
+    assert not h
+    msg = L.fc_last_error().decode()
+    L.fc_clear_error()
+    return msg
+
+
+def test_malformed_networks_are_refused_on_the_host():
+    torch = pytest.importorskip("torch")
+    torch.manual_seed(0)
+    f = FlyActor(toy("a"), 517, 90, hops=3, fan=5)
+    s = structure(f)
+    good = net_bytes(s)
+    assert "FLY1" in _bad(b"NOPE" + good[4:])
+    assert "short" in _bad(good[: len(good) // 2])
+    # a connection whose source is outside the previous layer
+    s2 = structure(f)
+    s2["hop"][1]["col"] = np.array(s2["hop"][1]["col"]).copy()
+    s2["hop"][1]["col"][0] = s["sizes"][1] + 5
+    assert "hop 2" in _bad(net_bytes(s2))
+    # a strength index used twice in one hop
+    s3 = structure(f)
+    w = np.array(s3["hop"][0]["widx"]).copy()
+    w[1] = w[0]
+    s3["hop"][0]["widx"] = w
+    assert "hop 1" in _bad(net_bytes(s3))
+    # a re-drive row outside the sensory layer
+    s4 = structure(f)
+    d = np.array(s4["hop"][0]["drow"]).copy()
+    d[0] = s["n_s"] + 1
+    s4["hop"][0]["drow"] = d
+    assert "hop 1" in _bad(net_bytes(s4))
