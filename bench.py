@@ -98,6 +98,9 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=1024)
     ap.add_argument("--cpu-train-batch", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run 3 copies of 1 GiB (read 1 GiB, write 1 GiB each) so a counter run can scale "
+                         "FETCH_SIZE / WRITE_SIZE by what they read for a copy of known size")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -228,6 +231,12 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     L.fc_free(core)
+    if args.calibrate:
+        a = torch.ones(1 << 28, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
     return 0
 
 
