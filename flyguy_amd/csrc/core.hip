@@ -6,7 +6,8 @@
 //               gradient), each set holding the seven arrays at 64-float aligned offsets, so Adam is one launch;
 //   structure: NET.bin's index arrays, the packed (index, weight) pairs of every product (refreshed from the
 //              current weights at each pass), and the row plans (forward: CSR rows; backward: CSC rows);
-//   states: x, drive, h0, gdrive, z_k / h_k per hop, two gz buffers, logits / dlogits;
+//   states: x, drive, h0, gdrive, h_k per hop, two gz buffers, logits / dlogits (a hop layer's pre-activation z is
+//           not kept: the backward needs it only where h > 0, and there it is (h + softplus(theta)) / gain);
 //   partial sums: split rows, per-edge weight gradients [T][E_k], per-row gain / threshold gradients [T][rows],
 //                 plug gradients [T][n_s] / [T][E_in], read-out gradients [chunks][n_act * n_dn].
 #include <algorithm>
@@ -74,7 +75,8 @@ struct HopD {
     bool has_drive = false;
     int2 *cw = nullptr, *tcw = nullptr;
     DevPlan fp, bp;
-    float *z = nullptr, *h = nullptr, *ggp = nullptr, *gsp = nullptr;
+    float *h = nullptr, *ggp = nullptr, *gsp = nullptr;
+    float4* info = nullptr;          // per row {gain, softplus(theta), re-drive row}, refreshed at every pass
 };
 
 // Stages timed with HIP events on the library's stream when profiling is on (fc_profile): where the time of a
@@ -105,6 +107,7 @@ struct Core {
     int maxB = 0, Tm = 0;
     int *in_crow = nullptr, *in_col = nullptr, *n0 = nullptr, *dn = nullptr, *dn_inv = nullptr;
     int2* in_cw = nullptr;
+    float4* info0 = nullptr;
     DevPlan pp;
     std::vector<HopD> hop;
     float* pm = nullptr;
@@ -358,12 +361,14 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
     c->gz[0] = dalloc<float>(*c, Tm * max_rows * S);
     c->gz[1] = dalloc<float>(*c, Tm * max_rows * S);
     for (auto& d : c->hop) {
-        d.z = dalloc<float>(*c, Tm * d.rows * S);
         d.h = dalloc<float>(*c, Tm * d.rows * S);
         d.ggp = dalloc<float>(*c, Tm * d.rows);
         d.gsp = dalloc<float>(*c, Tm * d.rows);
-        if (!d.z || !d.h || !d.ggp || !d.gsp) return nullptr;
+        d.info = dalloc<float4>(*c, d.rows);
+        if (!d.h || !d.ggp || !d.gsp || !d.info) return nullptr;
     }
+    c->info0 = dalloc<float4>(*c, c->n_s);
+    if (!c->info0) return nullptr;
     c->lg = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->dl = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->part = dalloc<float>(*c, Tm * std::max<long long>(max_slot, 1) * S);
@@ -396,6 +401,14 @@ static bool check_batch(const Core* c, int B) {
 }
 
 // ------------------------------------------------------------------------------------------------ passes
+// the per-row neuron records of every layer from this set's gain and theta
+static hipError_t rowinfo(Core& c, const float* gain, const float* theta) {
+    hipError_t e = launch_rowinfo(c.n0, nullptr, gain, theta, c.info0, c.n_s, c.st);
+    for (auto& d : c.hop)
+        if (e == hipSuccess) e = launch_rowinfo(d.nid, d.has_drive ? d.drow : nullptr, gain, theta, d.info, d.rows, c.st);
+    return e;
+}
+
 static bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     const int T = B / TW;
     hipStream_t st = c.st;
@@ -405,22 +418,22 @@ static bool forward(Core& c, const float* obs, int B, float* logits, int set) {
         Timed t(c, ST_PACK);
         FG_CHECK(launch_pack(c.in_col, nullptr, c.arr(set, 3), c.in_cw, c.E_in, st), false);
         for (auto& d : c.hop) FG_CHECK(launch_pack(d.col, d.widx, W, d.cw, d.E, st), false);
+        FG_CHECK(rowinfo(c, gain, theta), false);
     }
     FwdEpi e0;
     e0.bias = c.arr(set, 4);
-    e0.nid = c.n0; e0.gain = gain; e0.theta = theta;
+    e0.info = c.info0;
     e0.z = c.drive; e0.lz = tiled(c.n_s);
     e0.h = c.h0; e0.lh = tiled(c.n_s);
-    { Timed t(c, ST_PLUG); FG_CHECK(launch_fwd(c.pp.view(), c.in_cw, c.x, tiled(c.obs_dim), e0, c.part, tiled(c.pp.nslot), T, st), false); }
+    { Timed t(c, ST_PLUG); FG_CHECK(launch_fwd(c.pp.view(), c.in_cw, c.x, tiled(c.obs_dim), c.obs_dim, e0, c.part, tiled(c.pp.nslot), T, st), false); }
     const float* hp = c.h0;
     int hk = 0;
     for (auto& d : c.hop) {
         FwdEpi e;
-        if (d.has_drive) { e.drow = d.drow; e.drive = c.drive; e.ldrive = tiled(c.n_s); }
-        e.nid = d.nid; e.gain = gain; e.theta = theta;
-        e.z = d.z; e.lz = tiled(d.rows);
+        e.info = d.info;
+        if (d.has_drive) { e.drive = c.drive; e.ldrive = tiled(c.n_s); }
         e.h = d.h; e.lh = tiled(d.rows);
-        { Timed t(c, ST_HOP + std::min(hk, 7)); FG_CHECK(launch_fwd(d.fp.view(), d.cw, hp, tiled(d.src), e, c.part, tiled(d.fp.nslot), T, st), false); }
+        { Timed t(c, ST_HOP + std::min(hk, 7)); FG_CHECK(launch_fwd(d.fp.view(), d.cw, hp, tiled(d.src), d.src, e, c.part, tiled(d.fp.nslot), T, st), false); }
         hp = d.h;
         ++hk;
     }
@@ -443,15 +456,14 @@ static bool backward(Core& c, const float* dlogits, int B) {
     {
         Timed t(c, ST_PACK);
         for (auto& d : c.hop) FG_CHECK(launch_pack(d.tcol, d.twidx, W, d.tcw, d.E, st), false);
+        FG_CHECK(rowinfo(c, gain, theta), false);
     }
 
     HopD& top = c.hop[K - 1];
     BwdEpi et;
     et.mode = 1;
     et.h = top.h; et.lh = tiled(top.rows);
-    et.z = top.z; et.lz = tiled(top.rows);
-    et.nid = top.nid; et.gain = gain;
-    et.drow = top.has_drive ? top.drow : nullptr;
+    et.info = top.info;
     et.gz_out = c.gz[0]; et.lgz = tiled(top.rows);
     et.gdrive = c.gdrive; et.lgd = tiled(c.n_s);
     et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
@@ -474,7 +486,6 @@ static bool backward(Core& c, const float* dlogits, int B) {
         HopD& d = c.hop[k - 1];
         BwdEpi e;
         e.gdrive = c.gdrive; e.lgd = tiled(c.n_s);
-        e.gain = gain;
         const float* hbelow;
         int rows_below;
         float *ggp, *gsp;
@@ -483,16 +494,14 @@ static bool backward(Core& c, const float* dlogits, int B) {
             HopD& b = c.hop[k - 2];
             e.mode = 1;
             e.h = b.h; e.lh = tiled(b.rows);
-            e.z = b.z; e.lz = tiled(b.rows);
-            e.nid = b.nid;
-            e.drow = b.has_drive ? b.drow : nullptr;
+            e.info = b.info;
             e.gz_out = c.gz[cur ^ 1]; e.lgz = tiled(b.rows);
             hbelow = b.h; rows_below = b.rows; ggp = b.ggp; gsp = b.gsp; nid_below = b.nid;
         } else {
             e.mode = 2;
             e.h = c.h0; e.lh = tiled(c.n_s);
             e.z = c.drive; e.lz = tiled(c.n_s);
-            e.nid = c.n0;
+            e.info = c.info0;
             e.in_crow = c.in_crow; e.in_cw = c.in_cw; e.x = c.x; e.lx = tiled(c.obs_dim);
             e.ginb_part = c.ginb; e.gb_ld = c.n_s;
             e.ginw_part = c.ginw; e.gw_ld = c.E_in;
@@ -501,7 +510,7 @@ static bool backward(Core& c, const float* dlogits, int B) {
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
-            FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), hbelow, tiled(rows_below), c.gwpart, d.E, e,
+            FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart, d.E, e,
                                 c.part, tiled(d.bp.nslot), T, st), false);
         }
         Timed t(c, ST_REDUCE);
@@ -669,7 +678,12 @@ void fc_export_state(void* h, int layer, int what, float* dst, int B) {
     int rows;
     if (what == 2) { src = c->x; rows = c->obs_dim; }
     else if (layer == 0) { src = what == 0 ? c->h0 : c->drive; rows = c->n_s; }
-    else { const HopD& d = c->hop[layer - 1]; src = what == 0 ? d.h : d.z; rows = d.rows; }
+    else {
+        if (what == 1) { set_error("fc_export_state: a hop layer's pre-activation is not kept (only h)"); return; }
+        const HopD& d = c->hop[layer - 1];
+        src = d.h;
+        rows = d.rows;
+    }
     FG_CHECK(launch_export(src, tiled(rows), dst, rows, B, c->st), );
 }
 

@@ -23,7 +23,7 @@ void fh_spmm(const long long* rowptr, const int* col, const float* w, const floa
     e.z = out;
     e.lz = plain(B);
     Plan p{(const int4*)plan, nseg, (const int4*)split, nsplit, n_rows, nslot, E};
-    FG_CHECK(launch_fwd(p, (const int2*)cw, h, plain(B), e, scratch, tiled(nslot), B / TW, st), );
+    FG_CHECK(launch_fwd(p, (const int2*)cw, h, plain(B), n_src, e, scratch, tiled(nslot), B / TW, st), );
 }
 
 void fh_spmm_bwd(const long long* tcrow, const int* tcol, const long long* tperm, const float* w, const float* gz,
@@ -46,7 +46,7 @@ void fh_spmm_bwd(const long long* tcrow, const int* tcol, const long long* tperm
     e.gh_out = gh;
     e.lgh = plain(B);
     Plan p{(const int4*)plan, nseg, (const int4*)split, nsplit, n_src, nslot, E};
-    FG_CHECK(launch_bwd(p, (const int2*)cw, gz, plain(B), h, plain(B), gw ? gwpart : nullptr, E, e, scratch, tiled(nslot),
+    FG_CHECK(launch_bwd(p, (const int2*)cw, gz, plain(B), n_rows, h, plain(B), gw ? gwpart : nullptr, E, e, scratch, tiled(nslot),
                         T, st), );
     if (gw) FG_CHECK(launch_reduce64(gwpart, E, E, T, tperm, gw, st), );
 }

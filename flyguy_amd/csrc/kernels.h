@@ -27,17 +27,16 @@ struct Plan {
     long long E = 0;
 };
 
+// Per row of a layer, refreshed from the weights at every pass (k_rowinfo): {gain[nid], softplus(theta[nid]),
+// re-drive row in the sensory layer as int bits (-1: none), 0}.  One 16-byte load gives a row's whole neuron.
 // What follows the sum over a row's edges in the forward pass (flyguy_train.cu:84-94):
-// acc (+ bias) (+ drive[drow]) -> z; h = relu(gain[nid] * z - softplus(theta[nid])).  gain == nullptr: z only.
+// acc (+ bias) (+ drive[drow]) -> z; h = relu(gain * z - softplus(theta)).  info == nullptr: z only (raw product).
 struct FwdEpi {
     const float* bias = nullptr;
-    const int* drow = nullptr;
-    const float* drive = nullptr;
+    const float4* info = nullptr;
+    const float* drive = nullptr;     // the sensory layer's drive, for re-drive rows (nullptr: none in this layer)
     Lay ldrive{};
-    const int* nid = nullptr;
-    const float* gain = nullptr;
-    const float* theta = nullptr;
-    float* z = nullptr;
+    float* z = nullptr;               // the pre-activation: stored for the sensory layer (the drive) and raw products
     Lay lz{};
     float* h = nullptr;
     Lay lh{};
@@ -51,11 +50,9 @@ struct BwdEpi {
     Lay lgh{};
     const float* h = nullptr;
     Lay lh{};
-    const float* z = nullptr;     // pre-activation (drive for the sensory layer)
-    Lay lz{};
-    const int* nid = nullptr;
-    const float* gain = nullptr;
-    const int* drow = nullptr;    // mode 1: re-drive row in the sensory layer or -1 (nullptr: none)
+    const float* z = nullptr;     // the sensory layer's pre-activation (the drive); hop layers do not keep theirs:
+    Lay lz{};                     //   where h > 0 it is (h + softplus(theta)) / gain, and elsewhere it is not needed
+    const float4* info = nullptr; // per row {gain, softplus(theta), re-drive row}
     float* gz_out = nullptr;      // mode 1
     Lay lgz{};
     float* gdrive = nullptr;
@@ -79,9 +76,10 @@ hipError_t launch_pack(const int* col, const int* idx, const float* w, int2* cw,
 hipError_t launch_pack64(const int* col, const long long* idx, const float* w, int2* cw, long long E, hipStream_t st);
 hipError_t launch_reduce64(const float* part, long long ld, long long n, int nt, const long long* idx, float* G,
                            hipStream_t st);
-hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, const FwdEpi& epi, float* part, Lay lp,
-                      int T, hipStream_t st);
-hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, const float* hsrc, Lay lhs,
+// src_rows / gz_rows: rows of the gathered state (a gather of a row outside it reads zeros)
+hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
+                      float* part, Lay lp, int T, hipStream_t st);
+hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
                       float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st);
 hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStream_t st);
 hipError_t launch_logits(const float* hK, Lay lh, const int* dn, int n_dn, const float* ow, const float* ob, int n_act,
@@ -104,5 +102,7 @@ struct AdamSeg {
 hipError_t launch_adam(float* P, const float* G, float* M, float* V, float* EMA, const AdamSeg& s, float c1, float c2,
                        const float* gs_dev, float gs, float decay, hipStream_t st);
 hipError_t launch_export(const float* src, Lay ls, float* dst, int rows, int B, hipStream_t st);
+hipError_t launch_rowinfo(const int* nid, const int* drow, const float* gain, const float* theta, float4* info, int rows,
+                          hipStream_t st);
 
 }  // namespace fg

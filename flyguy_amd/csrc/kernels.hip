@@ -5,8 +5,8 @@
 // wave.  A segment's 8 lanes each hold a float4 of the 32-sample tile and sum its edges in CSR (CSC) order,
 // so a row that is not split is summed exactly as flyguy_train.cu:88 / :171 sum it.  The (source, weight)
 // pairs of 8 consecutive edges are loaded by the 8 lanes at once (one coalesced 64-byte load, the next one
-// already in flight) and handed round the group with ds_swizzle; the 8 source rows are then gathered as
-// independent 128-byte lines of the tile's slab, which the XCD's L2 holds.
+// already in flight) and handed round the group through LDS; the 8 source rows are then gathered as independent
+// 128-byte lines of the tile's slab, with no branch per edge (slots past a segment's end read row 0 and add 0).
 #include "kernels.h"
 
 namespace fg {
@@ -70,64 +70,125 @@ __global__ void k_pack64(const int* __restrict__ col, const long long* __restric
 }
 
 // ------------------------------------------------------------------------------------------------ forward
-__device__ __forceinline__ void fwd_finish(const FwdEpi& e, int t, int tile, int sub, float4 acc) {
-    if (e.drow) {
-        int d = e.drow[t];
-        if (d >= 0) add4(*at4(e.drive, e.ldrive, tile, d, sub), acc);
+// The row's own inputs of the finish (re-drive row, gain, threshold), loaded before the edge loop so that their
+// latency hides behind the gathers.
+struct FwdIn {
+    float4 dv;
+    float g, sp;
+};
+__device__ __forceinline__ FwdIn fwd_inputs(const FwdEpi& e, int t, int tile, int sub) {
+    FwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f};
+    if (e.info) {
+        const float4 r = e.info[t];
+        in.g = r.x;
+        in.sp = r.y;
+        const int d = __float_as_int(r.z);
+        if (e.drive && d >= 0) in.dv = *at4(e.drive, e.ldrive, tile, d, sub);
     }
+    return in;
+}
+__device__ __forceinline__ void fwd_finish(const FwdEpi& e, int t, int tile, int sub, float4 acc, const FwdIn& in) {
+    if (e.drive) add4(in.dv, acc);              // (zero when the row has no re-drive)
     if (e.z) *at4w(e.z, e.lz, tile, t, sub) = acc;
-    if (e.gain) {
-        int n = e.nid[t];
-        float g = e.gain[n], sp = softplus_f(e.theta[n]);
-        float4 hv = make_float4(fmaxf(fmaf(g, acc.x, -sp), 0.f), fmaxf(fmaf(g, acc.y, -sp), 0.f),
-                                fmaxf(fmaf(g, acc.z, -sp), 0.f), fmaxf(fmaf(g, acc.w, -sp), 0.f));
+    if (e.info) {
+        const float g = in.g, sp = in.sp;
+        const float4 hv = make_float4(fmaxf(fmaf(g, acc.x, -sp), 0.f), fmaxf(fmaf(g, acc.y, -sp), 0.f),
+                                      fmaxf(fmaf(g, acc.z, -sp), 0.f), fmaxf(fmaf(g, acc.w, -sp), 0.f));
         *at4w(e.h, e.lh, tile, t, sub) = hv;
     }
 }
 
-#define FG_BCAST_ALL(my, c, w)                                                                       \
-    c[0] = bcast8<0>(my.x); c[1] = bcast8<1>(my.x); c[2] = bcast8<2>(my.x); c[3] = bcast8<3>(my.x); \
-    c[4] = bcast8<4>(my.x); c[5] = bcast8<5>(my.x); c[6] = bcast8<6>(my.x); c[7] = bcast8<7>(my.x); \
-    w[0] = __int_as_float(bcast8<0>(my.y)); w[1] = __int_as_float(bcast8<1>(my.y));                 \
-    w[2] = __int_as_float(bcast8<2>(my.y)); w[3] = __int_as_float(bcast8<3>(my.y));                 \
-    w[4] = __int_as_float(bcast8<4>(my.y)); w[5] = __int_as_float(bcast8<5>(my.y));                 \
-    w[6] = __int_as_float(bcast8<6>(my.y)); w[7] = __int_as_float(bcast8<7>(my.y));
+// The (index, weight) pairs of a group's next 8 edges reach all 8 lanes of the group through the wave's own LDS
+// slots: each lane writes the pair it loaded (one 8-byte store), then reads the group's 8 pairs back (four 16-byte
+// reads the 8 lanes share).  A wave only touches its own slots and its lanes run in lockstep; wave_barrier keeps
+// the compiler from moving the reads above the store or the next store above the reads.
+__device__ __forceinline__ void stage8(int2* slots, int sub, int2 my, int (&c)[8], float (&w)[8]) {
+    slots[sub] = my;
+    __builtin_amdgcn_wave_barrier();
+    const int4* q = reinterpret_cast<const int4*>(slots);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int4 v = q[i];
+        c[2 * i] = v.x;
+        w[2 * i] = __int_as_float(v.y);
+        c[2 * i + 1] = v.z;
+        w[2 * i + 1] = __int_as_float(v.w);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
 
+// A source index that no slab reaches: as a buffer offset (index * 128 B) it lies past every slab, so the buffer load
+// returns zeros without touching memory.
+constexpr int NO_ROW = 0x01FFFFFF;
+
+// Pair of edge e of a segment ending at e1, or (NO_ROW, weight 0) past the end: loaded from a clamped index, so no
+// lane branches.  e_last is the segment's last edge (0 for an empty segment; every array has one element at least).
+__device__ __forceinline__ int2 pair_at(const int2* __restrict__ cw, int e, int e1, int e_last) {
+    int2 v = cw[min(e, e_last)];
+    const bool ok = e < e1;
+    v.x = ok ? v.x : NO_ROW;
+    v.y = ok ? v.y : 0;
+    return v;
+}
+
+// Gathers of one tile's slab.  Tiled layout: a raw buffer over the slab (rows x 128 B), 32-bit offsets, so an offset
+// past the slab (NO_ROW, or any bad index) reads zeros.  Plain layout ([rows][B], the HopCuda boundary): global
+// loads with the run-time row stride; rows past the end are masked to zero.
+template <bool TILED>
+struct Slab {
+    __amdgpu_buffer_rsrc_t rsrc;
+    const float* base;
+    int stride, rows;
+    __device__ __forceinline__ Slab(const float* tile_base, int row_stride, int n_rows, int sub)
+        : base(tile_base + sub * 4), stride(row_stride), rows(n_rows) {
+        if (TILED)
+            rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)tile_base, (short)0, n_rows * (TW * 4), 0x00020000);
+    }
+    __device__ __forceinline__ float4 get(int row, int sub) const {
+        if (TILED) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (unsigned)row * (TW * 4u) + (unsigned)sub * 16u, 0, 0);
+            return make_float4(__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]), __int_as_float(v[3]));
+        }
+        const bool ok = (unsigned)row < (unsigned)rows;
+        const float4 v = *reinterpret_cast<const float4*>(base + (size_t)(ok ? row : 0) * stride);
+        return ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+};
+
+template <bool TILED>
 __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw, const float* __restrict__ src, Lay ls,
-                                            FwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB) {
+                                            int src_rows, FwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB) {
+    __shared__ __align__(16) int2 slots[WG / LPR][LPR];
     int rb;
     const int tile = tile_of(blockIdx.x, RB, T, rb);
-    const int si = rb * RPG + (threadIdx.x >> 3);
-    const int sub = threadIdx.x & 7;
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7;
+    const int si = rb * RPG + grp;
     int4 sg;
     const bool live = load_segment(p, si, sg);
-    const int e1 = sg.z;
-    const float* sb = src + (size_t)tile * ls.tile + sub * 4;
+    const int e1 = sg.z, e_last = max(sg.z - 1, 0);
+    const Slab<TILED> slab(src + (size_t)tile * ls.tile, ls.row, src_rows, sub);
     float4 acc = (live && sg.w < 0 && epi.bias) ? splat(epi.bias[sg.x]) : splat(0.f);
-    int2 nxt = make_int2(0, 0);
-    if (sg.y + sub < e1) nxt = cw[sg.y + sub];
+    int2 nxt = pair_at(cw, sg.y + sub, e1, e_last);
+    FwdIn in{};
+    if (live && sg.w < 0) in = fwd_inputs(epi, sg.x, tile, sub);
     for (int eb = sg.y; __any(eb < e1); eb += 8) {
         const int2 my = nxt;
-        nxt = make_int2(0, 0);
-        if (eb + 8 + sub < e1) nxt = cw[eb + 8 + sub];
-        const int n = min(max(e1 - eb, 0), 8);
+        nxt = pair_at(cw, eb + 8 + sub, e1, e_last);
         int c[8];
         float w[8];
-        FG_BCAST_ALL(my, c, w)
+        stage8(slots[grp], sub, my, c, w);
         float4 v[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-            if (s < n) v[s] = *reinterpret_cast<const float4*>(sb + (size_t)c[s] * ls.row);
+        for (int s = 0; s < 8; ++s) v[s] = slab.get(c[s], sub);
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-            if (s < n) fma4(w[s], v[s], acc);
+        for (int s = 0; s < 8; ++s) fma4(w[s], v[s], acc);
     }
     if (!live) return;
     if (sg.w >= 0) {
         *at4w(part, lp, tile, sg.w, sub) = acc;
         return;
     }
-    fwd_finish(epi, sg.x, tile, sub, acc);
+    fwd_finish(epi, sg.x, tile, sub, acc, in);
 }
 
 // split rows: partial sums in segment order, then the same finish
@@ -140,24 +201,55 @@ __global__ __launch_bounds__(WG) void k_fwd_combine(Plan p, const float* __restr
     int4 s;
     if (!load_split(p, i, s)) return;     // whole 8-lane groups leave together
     float4 acc = epi.bias ? splat(epi.bias[s.x]) : splat(0.f);
+    const FwdIn in = fwd_inputs(epi, s.x, tile, sub);
     for (int k = 0; k < s.z; ++k) add4(*at4(part, lp, tile, s.y + k, sub), acc);
-    fwd_finish(epi, s.x, tile, sub, acc);
+    fwd_finish(epi, s.x, tile, sub, acc, in);
 }
 
 // ------------------------------------------------------------------------------------------------ backward
+// The source row's own inputs of the neuron backward (h, z, gain, re-drive row; for the sensory layer the drive's
+// gradient so far), loaded before the edge loop so that their latency hides behind the gathers.
+struct BwdIn {
+    float4 h, z, gd;
+    float gn, sp;
+    int d;
+};
+__device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int tile, int sub) {
+    BwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f, -1};
+    if (e.mode == 0) return in;
+    in.h = *at4(e.h, e.lh, tile, j, sub);
+    if (e.z) in.z = *at4(e.z, e.lz, tile, j, sub);
+    const float4 r = e.info[j];
+    in.gn = r.x;
+    in.sp = r.y;
+    if (e.mode == 1) {
+        in.d = __float_as_int(r.z);
+        if (in.d >= 0) in.gd = *at4(e.gdrive, e.lgd, tile, in.d, sub);
+    } else {
+        in.d = j;
+        in.gd = *at4(e.gdrive, e.lgd, tile, j, sub);     // complete: every hop above has added its share
+    }
+    return in;
+}
+
 // gh: the gradient of this layer's output h for (row j, tile); every lane of the 8-lane group calls this
-__device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int sub, float4 gh) {
+__device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int sub, float4 gh, const BwdIn& in) {
     if (e.mode == 0) {
         *at4w(e.gh_out, e.lgh, tile, j, sub) = gh;
         return;
     }
-    const float4 hv = *at4(e.h, e.lh, tile, j, sub);
+    const float4 hv = in.h;
     const float4 g = make_float4(hv.x > 0.f ? gh.x : 0.f, hv.y > 0.f ? gh.y : 0.f, hv.z > 0.f ? gh.z : 0.f,
                                  hv.w > 0.f ? gh.w : 0.f);
-    const int n = e.nid[j];
-    const float gn = e.gain[n];
+    const float gn = in.gn;
     const float4 gzv = make_float4(g.x * gn, g.y * gn, g.z * gn, g.w * gn);
-    const float4 zv = *at4(e.z, e.lz, tile, j, sub);
+    float4 zv = in.z;
+    if (!e.z) {                                 // z where it matters (h > 0): h = gain * z - softplus(theta)
+        zv.x = hv.x > 0.f ? (hv.x + in.sp) / gn : 0.f;
+        zv.y = hv.y > 0.f ? (hv.y + in.sp) / gn : 0.f;
+        zv.z = hv.z > 0.f ? (hv.z + in.sp) / gn : 0.f;
+        zv.w = hv.w > 0.f ? (hv.w + in.sp) / gn : 0.f;
+    }
     const float pg = gsum8(dot4(g, zv));
     const float ps = gsum8(hsum4(g));
     if (sub == 0) {
@@ -166,19 +258,15 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     }
     if (e.mode == 1) {
         *at4w(e.gz_out, e.lgz, tile, j, sub) = gzv;
-        if (e.drow) {
-            const int d = e.drow[j];
-            if (d >= 0) {
-                float4* gd = at4w(e.gdrive, e.lgd, tile, d, sub);
-                float4 v = *gd;
-                add4(gzv, v);
-                *gd = v;
-            }
+        if (in.d >= 0) {
+            float4 v = in.gd;
+            add4(gzv, v);
+            *at4w(e.gdrive, e.lgd, tile, in.d, sub) = v;
         }
         return;
     }
     // the sensory layer: the drive's gradient is complete now -> the plug's bias and per-connection gradients
-    float4 gd = *at4(e.gdrive, e.lgd, tile, j, sub);
+    float4 gd = in.gd;
     add4(gzv, gd);
     const float pb = gsum8(hsum4(gd));
     if (sub == 0) e.ginb_part[(size_t)tile * e.gb_ld + j] = pb;
@@ -190,39 +278,37 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     }
 }
 
+template <bool TILED>
 __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw, const float* __restrict__ gz, Lay lg,
-                                            const float* __restrict__ hs, Lay lhs, float* __restrict__ gwpart,
+                                            int gz_rows, const float* __restrict__ hs, Lay lhs, float* __restrict__ gwpart,
                                             long long gw_ld, BwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB) {
+    __shared__ __align__(16) int2 slots[WG / LPR][LPR];
     int rb;
     const int tile = tile_of(blockIdx.x, RB, T, rb);
-    const int si = rb * RPG + (threadIdx.x >> 3);
-    const int sub = threadIdx.x & 7;
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7;
+    const int si = rb * RPG + grp;
     int4 sg;
     const bool live = load_segment(p, si, sg);
-    const int e1 = sg.z;
+    const int e1 = sg.z, e_last = max(sg.z - 1, 0);
     const float4 hj = live ? *at4(hs, lhs, tile, sg.x, sub) : splat(0.f);
-    const float* gb = gz + (size_t)tile * lg.tile + sub * 4;
+    const Slab<TILED> slab(gz + (size_t)tile * lg.tile, lg.row, gz_rows, sub);
     float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld : nullptr;
     float4 acc = splat(0.f);
-    int2 nxt = make_int2(0, 0);
-    if (sg.y + sub < e1) nxt = cw[sg.y + sub];
+    int2 nxt = pair_at(cw, sg.y + sub, e1, e_last);
+    BwdIn in{};
+    if (live && sg.w < 0) in = bwd_inputs(epi, sg.x, tile, sub);
     for (int eb = sg.y; __any(eb < e1); eb += 8) {
         const int2 my = nxt;
-        nxt = make_int2(0, 0);
-        if (eb + 8 + sub < e1) nxt = cw[eb + 8 + sub];
-        const int n = min(max(e1 - eb, 0), 8);
+        nxt = pair_at(cw, eb + 8 + sub, e1, e_last);
         int c[8];
         float w[8];
-        FG_BCAST_ALL(my, c, w)
+        stage8(slots[grp], sub, my, c, w);
+        const int n = e1 - eb;
         float4 v[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            v[s] = splat(0.f);
-            if (s < n) v[s] = *reinterpret_cast<const float4*>(gb + (size_t)c[s] * lg.row);
-        }
+        for (int s = 0; s < 8; ++s) v[s] = slab.get(c[s], sub);
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-            if (s < n) fma4(w[s], v[s], acc);
+        for (int s = 0; s < 8; ++s) fma4(w[s], v[s], acc);
         if (gwp) {
             float mine = 0.f;
 #pragma unroll
@@ -238,7 +324,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
         *at4w(part, lp, tile, sg.w, sub) = acc;
         return;
     }
-    bwd_finish(epi, sg.x, tile, sub, acc);
+    bwd_finish(epi, sg.x, tile, sub, acc, in);
 }
 
 __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restrict__ part, Lay lp, BwdEpi epi, int T) {
@@ -250,8 +336,9 @@ __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restr
     int4 s;
     if (!load_split(p, i, s)) return;     // whole 8-lane groups leave together
     float4 acc = splat(0.f);
+    const BwdIn in = bwd_inputs(epi, s.x, tile, sub);
     for (int k = 0; k < s.z; ++k) add4(*at4(part, lp, tile, s.y + k, sub), acc);
-    bwd_finish(epi, s.x, tile, sub, acc);
+    bwd_finish(epi, s.x, tile, sub, acc, in);
 }
 
 // ------------------------------------------------------------------------------------------------ obs / logits
@@ -340,7 +427,7 @@ __global__ __launch_bounds__(WG) void k_readout_bwd_h(const float* __restrict__ 
         const float4* d4 = reinterpret_cast<const float4*>(dlT) + sub;
         for (int a = 0; a < n_act; ++a) fma4(owc[r * n_act + a], d4[a * LPR], acc);
     }
-    bwd_finish(epi, t, tile, sub, acc);
+    bwd_finish(epi, t, tile, sub, acc, bwd_inputs(epi, t, tile, sub));
 }
 
 // per chunk of 16 tiles: gow[a][j] partial = sum_b dl[b][a] * hK[dn[j]][b], gob[a] partial = sum_b dl[b][a]
@@ -504,6 +591,15 @@ __global__ void k_adam(float* __restrict__ P, const float* __restrict__ G, float
     EMA[i] = fmaf(decay, EMA[i], (1.f - decay) * pi);
 }
 
+// per row of a layer: {gain[nid], softplus(theta[nid]), re-drive row (int bits, -1 none), 0}
+__global__ void k_rowinfo(const int* __restrict__ nid, const int* __restrict__ drow, const float* __restrict__ gain,
+                          const float* __restrict__ theta, float4* __restrict__ info, int rows) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows) return;
+    const int n = nid[t];
+    info[t] = make_float4(gain[n], softplus_f(theta[n]), __int_as_float(drow ? drow[t] : -1), 0.f);
+}
+
 // a state tensor (tiled) -> [rows][B] (tests and diagnostics)
 __global__ void k_export(const float* __restrict__ src, Lay ls, float* __restrict__ dst, int rows, int B) {
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -534,11 +630,14 @@ hipError_t launch_reduce64(const float* part, long long ld, long long n, int nt,
     return hipGetLastError();
 }
 
-hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, const FwdEpi& epi, float* part, Lay lp,
-                      int T, hipStream_t st) {
+hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
+                      float* part, Lay lp, int T, hipStream_t st) {
     if (p.nseg > 0) {
         const int RB = (p.nseg + RPG - 1) / RPG;
-        k_fwd<<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, epi, part, lp, T, RB);
+        if (ls.row == TW)
+            k_fwd<true><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB);
+        else
+            k_fwd<false><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -549,11 +648,16 @@ hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, c
     return hipSuccess;
 }
 
-hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, const float* hsrc, Lay lhs,
+hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
                       float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st) {
     if (p.nseg > 0) {
         const int RB = (p.nseg + RPG - 1) / RPG;
-        k_bwd<<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, RB);
+        if (lg.row == TW)
+            k_bwd<true><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part,
+                                                                      lp, T, RB);
+        else
+            k_bwd<false><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part,
+                                                                       lp, T, RB);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -628,6 +732,13 @@ hipError_t launch_adam(float* P, const float* G, float* M, float* V, float* EMA,
                        const float* gs_dev, float gs, float decay, hipStream_t st) {
     (void)gs_dev;
     k_adam<<<blocks(s.off[7]), WG, 0, st>>>(P, G, M, V, EMA, s, c1, c2, gs, decay);
+    return hipGetLastError();
+}
+
+hipError_t launch_rowinfo(const int* nid, const int* drow, const float* gain, const float* theta, float4* info, int rows,
+                          hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    k_rowinfo<<<blocks(rows), WG, 0, st>>>(nid, drow, gain, theta, info, rows);
     return hipGetLastError();
 }
 
