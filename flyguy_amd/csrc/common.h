@@ -19,6 +19,14 @@ constexpr int RPW = 64 / LPR;   // rows per wave (8)
 constexpr int WG = 256;         // threads per workgroup
 constexpr int RPG = WG / LPR;   // rows per workgroup (32)
 constexpr int SEG_MAX = 256;    // longest run of edges one lane group sums before a row is split into segments
+constexpr int SEG_MIN_PER_TILE = 8192;   // segments a product should have per tile: >= 256 workgroups, so that the
+                                         // workgroups resident on an XCD all work on one tile at a time
+
+// the segment cap of a product of E edges: SEG_MAX, lowered (not below 16) until there are SEG_MIN_PER_TILE segments
+inline int seg_cap(long long E) {
+    long long c = (E + SEG_MIN_PER_TILE - 1) / SEG_MIN_PER_TILE;
+    return (int)(c < 16 ? 16 : (c > SEG_MAX ? SEG_MAX : c));
+}
 
 // Last error of this thread (set by a failing entry point, read by fc_last_error).
 void set_error(const std::string& msg);

@@ -304,7 +304,7 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
     c->maxB = bm;
     c->Tm = bm / TW;
     HostPlan hp;
-    if (!make_plan(in_crow.data(), c->n_s, SEG_MAX, hp) || !upload_plan(*c, hp, c->n_s, c->E_in, c->pp)) {
+    if (!make_plan(in_crow.data(), c->n_s, seg_cap(c->E_in), hp) || !upload_plan(*c, hp, c->n_s, c->E_in, c->pp)) {
         if (!*last_error()) set_error("plug plan");
         return nullptr;
     }
@@ -315,7 +315,7 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
         HH& h = hh[k];
         d.rows = c->sizes[k + 1]; d.src = c->sizes[k]; d.E = c->E[k];
         HostPlan f, b;
-        if (!make_plan(h.crow.data(), d.rows, SEG_MAX, f) || !make_plan(h.tcrow.data(), d.src, SEG_MAX, b)) {
+        if (!make_plan(h.crow.data(), d.rows, seg_cap(d.E), f) || !make_plan(h.tcrow.data(), d.src, seg_cap(d.E), b)) {
             set_error("row plan");
             return nullptr;
         }

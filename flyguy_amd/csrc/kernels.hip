@@ -121,6 +121,13 @@ __device__ __forceinline__ void stage8(int2* slots, int sub, int2 my, int (&c)[8
 // returns zeros without touching memory.
 constexpr int NO_ROW = 0x01FFFFFF;
 
+// the largest value over the wave (every lane gets it, in an SGPR)
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    return __builtin_amdgcn_readfirstlane(v);
+}
+
 // Pair of edge e of a segment ending at e1, or (NO_ROW, weight 0) past the end: loaded from a clamped index, so no
 // lane branches.  e_last is the segment's last edge (0 for an empty segment; every array has one element at least).
 __device__ __forceinline__ int2 pair_at(const int2* __restrict__ cw, int e, int e1, int e_last) {
@@ -171,7 +178,8 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     int2 nxt = pair_at(cw, sg.y + sub, e1, e_last);
     FwdIn in{};
     if (live && sg.w < 0) in = fwd_inputs(epi, sg.x, tile, sub);
-    for (int eb = sg.y; __any(eb < e1); eb += 8) {
+    // edges left in the wave's longest segment: slots no group needs are not gathered at all
+    for (int eb = sg.y, left = wave_max(sg.z - sg.y); left > 0; eb += 8, left -= 8) {
         const int2 my = nxt;
         nxt = pair_at(cw, eb + 8 + sub, e1, e_last);
         int c[8];
@@ -179,7 +187,7 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
         stage8(slots[grp], sub, my, c, w);
         float4 v[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) v[s] = slab.get(c[s], sub);
+        for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(c[s], sub) : splat(0.f);
 #pragma unroll
         for (int s = 0; s < 8; ++s) fma4(w[s], v[s], acc);
     }
@@ -297,7 +305,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     int2 nxt = pair_at(cw, sg.y + sub, e1, e_last);
     BwdIn in{};
     if (live && sg.w < 0) in = bwd_inputs(epi, sg.x, tile, sub);
-    for (int eb = sg.y; __any(eb < e1); eb += 8) {
+    for (int eb = sg.y, left = wave_max(sg.z - sg.y); left > 0; eb += 8, left -= 8) {
         const int2 my = nxt;
         nxt = pair_at(cw, eb + 8 + sub, e1, e_last);
         int c[8];
@@ -306,7 +314,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
         const int n = e1 - eb;
         float4 v[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) v[s] = slab.get(c[s], sub);
+        for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(c[s], sub) : splat(0.f);
 #pragma unroll
         for (int s = 0; s < 8; ++s) fma4(w[s], v[s], acc);
         if (gwp) {
