@@ -33,9 +33,9 @@ _SIGS = {
     "fc_export_state": (None, [vp, ci, ci, vp, ci]),
     "fc_profile": (None, [vp, ci]),
     "fc_profile_read": (ci, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(cll), ci, ci]),
-    "fc_plan_segments": (ci, [vp, ci, ci, vp, cll, vp, cll, ctypes.POINTER(cll)]),
-    "fh_spmm": (None, [vp, vp, vp, vp, vp, ci, ci, ci, cll, vp, ci, vp, ci, ci, vp, vp, vp]),
-    "fh_spmm_bwd": (None, [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, cll, vp, ci, vp, ci, ci, vp, vp, vp, vp]),
+    "fc_plan_rows": (ci, [vp, ci, ci, vp, cll, vp, cll, vp, cll, vp, cll, ctypes.POINTER(cll)]),
+    "fh_spmm": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp, vp, vp]),
+    "fh_spmm_bwd": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp, vp]),
 }
 
 
@@ -71,22 +71,38 @@ def call(name: str, *args):
     return out
 
 
-def plan_segments(rowptr, seg_max: int = 256):
-    """Row plan of a CSR row pointer (host only): (segments int32 [nseg, 4], split rows int32 [nsplit, 4], nslot)."""
+NO_ROW = 0x01FFFFFF      # the source index of a plan position no edge uses (gathers read zeros for it)
+
+
+def seg_cap(n_edges: int) -> int:
+    """The segment length cap the library uses for a product of n_edges edges: at least 8192 segments per tile
+    (so that a tile's workgroups fill the chip), between 16 and 256 edges."""
+    return int(min(256, max(16, -(-int(n_edges) // 8192))))
+
+
+def plan_rows(rowptr, seg_max: int | None = None) -> dict:
+    """Row plan of a CSR row pointer (host only, fc_plan_rows): {"wave": int32 [nwave, 2], "seg": int32 [nseg, 4],
+    "split": int32 [nsplit, 4], "nslot": int, "pos": int32 [npos]} (pos: the CSR edge of each plan position, -1 none).
+    seg_max defaults to seg_cap of the edge count."""
     import numpy as np
     rp = np.ascontiguousarray(rowptr, dtype=np.int32)
     rows = len(rp) - 1
-    counts = (cll * 3)()
-    lib().fc_plan_segments(rp.ctypes.data, rows, seg_max, None, 0, None, 0, counts)
+    if seg_max is None:
+        seg_max = seg_cap(int(rp[-1]) if rows >= 0 and len(rp) else 0)
+    counts = (cll * 5)()
+    lib().fc_plan_rows(rp.ctypes.data, rows, seg_max, None, 0, None, 0, None, 0, None, 0, counts)
     lib().fc_clear_error()
-    nseg, nsplit, nslot = int(counts[0]), int(counts[1]), int(counts[2])
-    seg = np.zeros((max(nseg, 1), 4), np.int32)
-    split = np.zeros((max(nsplit, 1), 4), np.int32)
-    rc = lib().fc_plan_segments(rp.ctypes.data, rows, seg_max, seg.ctypes.data, nseg, split.ctypes.data, nsplit, counts)
+    nw, ns, nsp, nslot, npos = (int(counts[i]) for i in range(5))
+    wave = np.zeros((max(nw, 1), 2), np.int32)
+    seg = np.zeros((max(ns, 1), 4), np.int32)
+    split = np.zeros((max(nsp, 1), 4), np.int32)
+    pos = np.zeros(max(npos, 1), np.int32)
+    rc = lib().fc_plan_rows(rp.ctypes.data, rows, seg_max, wave.ctypes.data, nw, seg.ctypes.data, ns,
+                            split.ctypes.data, nsp, pos.ctypes.data, npos, counts)
     if rc != 0:
-        check("fc_plan_segments")
-        raise LibraryError("fc_plan_segments failed")
-    return seg[:nseg], split[:nsplit], nslot
+        check("fc_plan_rows")
+        raise LibraryError("fc_plan_rows failed")
+    return {"wave": wave[:nw], "seg": seg[:ns], "split": split[:nsp], "nslot": nslot, "pos": pos[:npos]}
 
 
 STAGES = {0: "obs transpose", 1: "pack", 2: "plug", 11: "logits", 12: "loss", 13: "readout bwd", 22: "reduce",

@@ -29,49 +29,75 @@ const char* last_error() { return g_err.c_str(); }
 void clear_error() { g_err.clear(); }
 
 // ------------------------------------------------------------------------------------------------ row plans
+// The row plan of one product (the Plan of kernels.h), built on the host.
 struct HostPlan {
-    std::vector<int4> seg, split;
+    std::vector<int2> wave;      // {first position, longest segment}
+    std::vector<int4> seg;       // {row, slot, re-drive row, 0}
+    std::vector<int4> split;     // {row, first slot, segments, re-drive row}
+    std::vector<int> pos;        // plan position -> CSR edge it holds (-1: none)
     int nslot = 0;
 };
 
 // Cut rows into segments of at most seg_max edges (a longer row gets ceil(d / seg_max) segments of nearly equal
-// length), then order all segments longest first; equal lengths keep (row, segment) order.
-static bool make_plan(const int* rowptr, int rows, int seg_max, HostPlan& p) {
-    p.seg.clear();
-    p.split.clear();
-    p.nslot = 0;
+// length), order all segments longest first (equal lengths keep (row, segment) order), deal them 8 to a wave and lay
+// the edges out in plan order: edge k of the segment of group g of wave w at position woff[w] + 64 (k / 8) + 8 g +
+// k % 8, each wave taking 64 positions per step of its longest segment.  drow (nullable): every row's re-drive row.
+static bool make_plan(const int* rowptr, int rows, int seg_max, const int* drow, HostPlan& p) {
+    p = HostPlan{};
     if (rows < 0 || seg_max <= 0 || (rows > 0 && rowptr[0] != 0)) return false;
+    struct S { int row, b, e, slot; };
+    std::vector<S> segs;
     for (int r = 0; r < rows; ++r) {
         const long long d = (long long)rowptr[r + 1] - rowptr[r];
         if (d < 0) return false;
+        const int dr = drow ? drow[r] : -1;
         if (d <= seg_max) {
-            p.seg.push_back(make_int4(r, rowptr[r], rowptr[r + 1], -1));
+            segs.push_back(S{r, rowptr[r], rowptr[r + 1], -1});
             continue;
         }
         const int ns = (int)((d + seg_max - 1) / seg_max);
-        p.split.push_back(make_int4(r, p.nslot, ns, 0));
+        p.split.push_back(make_int4(r, p.nslot, ns, dr));
         for (int s = 0; s < ns; ++s) {
             const int b = rowptr[r] + (int)(d * s / ns), e = rowptr[r] + (int)(d * (s + 1) / ns);
-            p.seg.push_back(make_int4(r, b, e, p.nslot + s));
+            segs.push_back(S{r, b, e, p.nslot + s});
         }
         p.nslot += ns;
     }
-    std::stable_sort(p.seg.begin(), p.seg.end(), [](const int4& a, const int4& b) { return a.z - a.y > b.z - b.y; });
+    std::stable_sort(segs.begin(), segs.end(), [](const S& a, const S& b) { return a.e - a.b > b.e - b.b; });
+    const size_t n = segs.size(), nw = (n + 7) / 8;
+    long long npos = 0;
+    p.wave.resize(nw);
+    for (size_t w = 0; w < nw; ++w) {
+        int longest = 0;
+        for (size_t i = 8 * w; i < std::min(n, 8 * w + 8); ++i) longest = std::max(longest, segs[i].e - segs[i].b);
+        p.wave[w] = make_int2((int)npos, longest);
+        npos += 64LL * ((longest + 7) / 8);
+        if (npos > 0x7fffff00LL) return false;              // positions are 32-bit
+    }
+    p.pos.assign((size_t)npos, -1);
+    p.seg.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+        const S& g = segs[i];
+        p.seg[i] = make_int4(g.row, g.slot, drow ? drow[g.row] : -1, 0);
+        const long long base = p.wave[i / 8].x + 8LL * (long long)(i % 8);
+        for (int k = 0; k < g.e - g.b; ++k) p.pos[(size_t)(base + 64LL * (k / 8) + k % 8)] = g.b + k;
+    }
     return true;
 }
 
 struct DevPlan {
+    int2* wave = nullptr;
     int4* seg = nullptr;
     int4* split = nullptr;
-    int nseg = 0, nsplit = 0, nslot = 0, rows = 0;
-    long long E = 0;
-    Plan view() const { return Plan{seg, nseg, split, nsplit, rows, nslot, E}; }
+    int *pcol = nullptr, *pidx = nullptr;      // per position: source row and weight index (-1: no edge)
+    int nwave = 0, nseg = 0, nsplit = 0, nslot = 0, rows = 0;
+    long long npos = 0;
+    Plan view() const { return Plan{wave, nwave, seg, nseg, split, nsplit, rows, nslot, npos}; }
 };
 
 struct HopD {
     int rows = 0, src = 0, E = 0;
-    int *nid = nullptr, *crow = nullptr, *col = nullptr, *widx = nullptr, *tcrow = nullptr, *tcol = nullptr,
-        *twidx = nullptr, *drow = nullptr;
+    int *nid = nullptr, *drow = nullptr;
     bool has_drive = false;
     int2 *cw = nullptr, *tcw = nullptr;
     DevPlan fp, bp;
@@ -184,15 +210,28 @@ static T* upload(Core& c, const std::vector<T>& v) {
     }
     return p;
 }
-static bool upload_plan(Core& c, const HostPlan& h, int rows, long long E, DevPlan& d) {
+// the plan on the device, with its positions resolved through col (source rows) and idx (weight index of a CSR edge;
+// nullptr: the edge itself)
+static bool upload_plan(Core& c, const HostPlan& h, int rows, const std::vector<int>& col, const std::vector<int>* idx,
+                        DevPlan& d) {
     d.rows = rows;
-    d.E = E;
+    d.nwave = (int)h.wave.size();
     d.nseg = (int)h.seg.size();
     d.nsplit = (int)h.split.size();
     d.nslot = h.nslot;
+    d.npos = (long long)h.pos.size();
+    std::vector<int> pcol(h.pos.size()), pidx(h.pos.size());
+    for (size_t i = 0; i < h.pos.size(); ++i) {
+        const int e = h.pos[i];
+        pcol[i] = e >= 0 ? col[(size_t)e] : NO_ROW;
+        pidx[i] = e >= 0 ? (idx ? (*idx)[(size_t)e] : e) : -1;
+    }
+    d.wave = upload(c, h.wave);
     d.seg = upload(c, h.seg);
     d.split = upload(c, h.split);
-    return d.seg && d.split;
+    d.pcol = upload(c, pcol);
+    d.pidx = upload(c, pidx);
+    return d.wave && d.seg && d.split && d.pcol && d.pidx;
 }
 
 static void release(Core* c) {
@@ -304,39 +343,42 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
     c->maxB = bm;
     c->Tm = bm / TW;
     HostPlan hp;
-    if (!make_plan(in_crow.data(), c->n_s, seg_cap(c->E_in), hp) || !upload_plan(*c, hp, c->n_s, c->E_in, c->pp)) {
+    if (!make_plan(in_crow.data(), c->n_s, seg_cap(c->E_in), nullptr, hp) ||
+        !upload_plan(*c, hp, c->n_s, in_col, nullptr, c->pp)) {
         if (!*last_error()) set_error("plug plan");
         return nullptr;
     }
-    long long max_slot = c->pp.nslot, max_E = 1, max_rows = 1;
+    c->in_cw = dalloc<int2>(*c, (size_t)c->pp.npos);
+    long long max_slot = c->pp.nslot, max_pos = 1, max_rows = 1;
     c->hop.resize(K);
     for (int k = 0; k < K; ++k) {
         HopD& d = c->hop[k];
         HH& h = hh[k];
         d.rows = c->sizes[k + 1]; d.src = c->sizes[k]; d.E = c->E[k];
+        // the transposed plan's rows are the layer below: its re-drive rows (none for the sensory layer)
+        const int* below_drow = k >= 1 ? hh[k - 1].drow.data() : nullptr;
         HostPlan f, b;
-        if (!make_plan(h.crow.data(), d.rows, seg_cap(d.E), f) || !make_plan(h.tcrow.data(), d.src, seg_cap(d.E), b)) {
+        if (!make_plan(h.crow.data(), d.rows, seg_cap(d.E), h.drow.data(), f) ||
+            !make_plan(h.tcrow.data(), d.src, seg_cap(d.E), below_drow, b)) {
             set_error("row plan");
             return nullptr;
         }
-        if (!upload_plan(*c, f, d.rows, d.E, d.fp) || !upload_plan(*c, b, d.src, d.E, d.bp)) return nullptr;
-        d.has_drive = std::any_of(h.drow.begin(), h.drow.end(), [](int v) { return v >= 0; });
-        d.nid = upload(*c, h.nid); d.crow = upload(*c, h.crow); d.col = upload(*c, h.col); d.widx = upload(*c, h.widx);
-        d.tcrow = upload(*c, h.tcrow); d.tcol = upload(*c, h.tcol); d.twidx = upload(*c, h.twidx);
-        d.drow = upload(*c, h.drow);
-        d.cw = dalloc<int2>(*c, d.E);
-        d.tcw = dalloc<int2>(*c, d.E);
-        if (!d.nid || !d.crow || !d.col || !d.widx || !d.tcrow || !d.tcol || !d.twidx || !d.drow || !d.cw || !d.tcw)
+        if (!upload_plan(*c, f, d.rows, h.col, &h.widx, d.fp) || !upload_plan(*c, b, d.src, h.tcol, &h.twidx, d.bp))
             return nullptr;
+        d.has_drive = std::any_of(h.drow.begin(), h.drow.end(), [](int v) { return v >= 0; });
+        d.nid = upload(*c, h.nid);
+        d.drow = upload(*c, h.drow);
+        d.cw = dalloc<int2>(*c, (size_t)d.fp.npos);
+        d.tcw = dalloc<int2>(*c, (size_t)d.bp.npos);
+        if (!d.nid || !d.drow || !d.cw || !d.tcw) return nullptr;
         max_slot = std::max<long long>({max_slot, d.fp.nslot, d.bp.nslot});
-        max_E = std::max<long long>(max_E, d.E);
+        max_pos = std::max<long long>(max_pos, d.bp.npos);
         max_rows = std::max<long long>(max_rows, d.rows);
     }
     std::vector<int> dn_inv(c->sizes[K], -1);
     for (int j = 0; j < c->n_dn; ++j) dn_inv[dn[j]] = j;
     c->in_crow = upload(*c, in_crow); c->in_col = upload(*c, in_col); c->n0 = upload(*c, n0);
     c->dn = upload(*c, dn); c->dn_inv = upload(*c, dn_inv);
-    c->in_cw = dalloc<int2>(*c, c->E_in);
     if (!c->in_crow || !c->in_col || !c->n0 || !c->dn || !c->dn_inv || !c->in_cw) return nullptr;
 
     // parameters: 5 sets x 7 arrays
@@ -372,7 +414,7 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
     c->lg = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->dl = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->part = dalloc<float>(*c, Tm * std::max<long long>(max_slot, 1) * S);
-    c->gwpart = dalloc<float>(*c, Tm * max_E);
+    c->gwpart = dalloc<float>(*c, Tm * max_pos);
     c->ggp0 = dalloc<float>(*c, Tm * c->n_s);
     c->gsp0 = dalloc<float>(*c, Tm * c->n_s);
     c->ginb = dalloc<float>(*c, Tm * c->n_s);
@@ -416,8 +458,8 @@ static bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
     {
         Timed t(c, ST_PACK);
-        FG_CHECK(launch_pack(c.in_col, nullptr, c.arr(set, 3), c.in_cw, c.E_in, st), false);
-        for (auto& d : c.hop) FG_CHECK(launch_pack(d.col, d.widx, W, d.cw, d.E, st), false);
+        FG_CHECK(launch_pack(c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos, st), false);
+        for (auto& d : c.hop) FG_CHECK(launch_pack(d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos, st), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
     FwdEpi e0;
@@ -455,7 +497,7 @@ static bool backward(Core& c, const float* dlogits, int B) {
     { Timed t(c, ST_ZERO); FG_CHECK(launch_fill(c.gdrive, 0.f, (long long)T * c.n_s * TW, st), false); }
     {
         Timed t(c, ST_PACK);
-        for (auto& d : c.hop) FG_CHECK(launch_pack(d.tcol, d.twidx, W, d.tcw, d.E, st), false);
+        for (auto& d : c.hop) FG_CHECK(launch_pack(d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos, st), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
 
@@ -464,6 +506,7 @@ static bool backward(Core& c, const float* dlogits, int B) {
     et.mode = 1;
     et.h = top.h; et.lh = tiled(top.rows);
     et.info = top.info;
+    et.drow = top.has_drive ? top.drow : nullptr;
     et.gz_out = c.gz[0]; et.lgz = tiled(top.rows);
     et.gdrive = c.gdrive; et.lgd = tiled(c.n_s);
     et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
@@ -502,7 +545,7 @@ static bool backward(Core& c, const float* dlogits, int B) {
             e.h = c.h0; e.lh = tiled(c.n_s);
             e.z = c.drive; e.lz = tiled(c.n_s);
             e.info = c.info0;
-            e.in_crow = c.in_crow; e.in_cw = c.in_cw; e.x = c.x; e.lx = tiled(c.obs_dim);
+            e.in_crow = c.in_crow; e.in_col = c.in_col; e.x = c.x; e.lx = tiled(c.obs_dim); e.x_rows = c.obs_dim;
             e.ginb_part = c.ginb; e.gb_ld = c.n_s;
             e.ginw_part = c.ginw; e.gw_ld = c.E_in;
             hbelow = c.h0; rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
@@ -510,11 +553,11 @@ static bool backward(Core& c, const float* dlogits, int B) {
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
-            FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart, d.E, e,
-                                c.part, tiled(d.bp.nslot), T, st), false);
+            FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart,
+                                d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st), false);
         }
         Timed t(c, ST_REDUCE);
-        FG_CHECK(launch_reduce(c.gwpart, d.E, d.E, T, d.twidx, nullptr, G[0], st), false);
+        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, T, d.bp.pidx, nullptr, G[0], st), false);
         FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
         FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
         if (k == 1) {
@@ -707,14 +750,27 @@ int fc_profile_read(void* h, double* ms, long long* counts, int n, int reset) {
     return ST_COUNT;
 }
 
-int fc_plan_segments(const int* rowptr, int rows, int seg_max, int* seg_out, long long seg_cap, int* split_out,
-                     long long split_cap, long long* counts) {
+int fc_plan_rows(const int* rowptr, int rows, int seg_max, int* wave_out, long long wave_cap, int* seg_out,
+                 long long seg_cap, int* split_out, long long split_cap, int* pos_out, long long pos_cap,
+                 long long* counts) {
     HostPlan p;
-    if (!rowptr || !make_plan(rowptr, rows, seg_max, p)) { set_error("fc_plan_segments: malformed row pointer"); return -1; }
-    if (counts) { counts[0] = (long long)p.seg.size(); counts[1] = (long long)p.split.size(); counts[2] = p.nslot; }
-    if ((long long)p.seg.size() > seg_cap || (long long)p.split.size() > split_cap) { set_error("fc_plan_segments: capacity"); return -1; }
+    if (!rowptr || !make_plan(rowptr, rows, seg_max, nullptr, p)) {
+        set_error("fc_plan_rows: malformed row pointer");
+        return -1;
+    }
+    if (counts) {
+        counts[0] = (long long)p.wave.size(); counts[1] = (long long)p.seg.size(); counts[2] = (long long)p.split.size();
+        counts[3] = p.nslot; counts[4] = (long long)p.pos.size();
+    }
+    if ((long long)p.wave.size() > wave_cap || (long long)p.seg.size() > seg_cap || (long long)p.split.size() > split_cap ||
+        (long long)p.pos.size() > pos_cap) {
+        set_error("fc_plan_rows: capacity");
+        return -1;
+    }
+    if (wave_out && !p.wave.empty()) std::memcpy(wave_out, p.wave.data(), p.wave.size() * sizeof(int2));
     if (seg_out && !p.seg.empty()) std::memcpy(seg_out, p.seg.data(), p.seg.size() * sizeof(int4));
     if (split_out && !p.split.empty()) std::memcpy(split_out, p.split.data(), p.split.size() * sizeof(int4));
+    if (pos_out && !p.pos.empty()) std::memcpy(pos_out, p.pos.data(), p.pos.size() * sizeof(int));
     return 0;
 }
 

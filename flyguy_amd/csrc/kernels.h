@@ -12,20 +12,35 @@ struct Lay {
 inline Lay tiled(int rows) { return Lay{(long long)rows * TW, TW}; }   // [T][rows][32]
 inline Lay plain(int B) { return Lay{TW, B}; }                          // [rows][B]
 
-// A segment is a run of at most SEG_MAX edges of one row: {row, e_begin, e_end, slot}; slot < 0: the whole row
-// (the kernel finishes it), else the index of its partial sum in the split scratch.  A split row is
-// {row, first slot, number of segments, 0}; its partial sums are added in segment order.
-// rows / E / nslot bound what a segment may name: a segment outside them is skipped (the library's own plans never
-// are; the bounds guard plans handed in through the fh_* entry points).
+// The row plan of one sparse product.  Every row is cut into segments of at most seg_cap edges, the segments are
+// sorted longest first and dealt out 8 to a wave (one per 8-lane group).  The (source, weight) pairs of a product
+// live in plan order, interleaved per wave: the pair of edge 8j+s of the segment of group g of wave w is at position
+// woff[w] + 64 j + 8 g + s, so the 64 pairs one wave uses in one step are one contiguous 512-byte block, and the
+// per-(edge, tile) partials of the weight gradient are stored the same way.  Positions no edge uses hold the pair
+// (NO_ROW, 0).
+//   wave[w]  = {woff, longest segment of the wave}: the wave runs ceil(longest / 8) steps
+//   seg[i]   = {row, slot, re-drive row, 0} of segment i (group i % 8 of wave i / 8); slot < 0: the whole row, which
+//              the kernel finishes; else the index of the segment's partial sum in the split scratch.  The re-drive
+//              row (-1: none) is the row's input from the sensory layer, handed in here so that its load does not
+//              wait for another one.
+//   split[k] = {row, first slot, number of segments, 0} of a split row; its partial sums are added in segment order
+// rows / nslot / npos bound what the plan may name: a wave or segment outside them is skipped (the library's own
+// plans never are; the bounds guard plans handed in through the fh_* entry points).
 struct Plan {
+    const int2* wave = nullptr;
+    int nwave = 0;
     const int4* seg = nullptr;
     int nseg = 0;
     const int4* split = nullptr;
     int nsplit = 0;
     int rows = 0;
     int nslot = 0;
-    long long E = 0;
+    long long npos = 0;
 };
+
+// A source index that no slab reaches: as a buffer offset (index * 128 B) it lies past every slab, so a buffer load
+// of it returns zeros without touching memory; a masked global load of it is skipped.
+constexpr int NO_ROW = 0x01FFFFFF;
 
 // Per row of a layer, refreshed from the weights at every pass (k_rowinfo): {gain[nid], softplus(theta[nid]),
 // re-drive row in the sensory layer as int bits (-1: none), 0}.  One 16-byte load gives a row's whole neuron.
@@ -53,6 +68,7 @@ struct BwdEpi {
     const float* z = nullptr;     // the sensory layer's pre-activation (the drive); hop layers do not keep theirs:
     Lay lz{};                     //   where h > 0 it is (h + softplus(theta)) / gain, and elsewhere it is not needed
     const float4* info = nullptr; // per row {gain, softplus(theta), re-drive row}
+    const int* drow = nullptr;    // per row: the re-drive row (-1: none), for kernels that do not follow a row plan
     float* gz_out = nullptr;      // mode 1
     Lay lgz{};
     float* gdrive = nullptr;
@@ -61,21 +77,20 @@ struct BwdEpi {
     float* gsum_part = nullptr;   // [T][rows]: sum over the tile of g
     long long gp_ld = 0;
     // mode 2: the plug
-    const int* in_crow = nullptr;
-    const int2* in_cw = nullptr;
-    const float* x = nullptr;
+    const int* in_crow = nullptr;     // the plug's CSR: connections in_crow[j] .. in_crow[j+1] of sensory row j
+    const int* in_col = nullptr;      //   read observation rows in_col[f]
+    const float* x = nullptr;         // the observations, tiled, x_rows of them
     Lay lx{};
+    int x_rows = 0;
     float* ginb_part = nullptr;   // [T][n_s]
     long long gb_ld = 0;
-    float* ginw_part = nullptr;   // [T][E_in]
+    float* ginw_part = nullptr;   // [T][E_in], in the plug's CSR order
     long long gw_ld = 0;
 };
 
 // launch wrappers (all asynchronous on `st`)
-hipError_t launch_pack(const int* col, const int* idx, const float* w, int2* cw, long long E, hipStream_t st);
-hipError_t launch_pack64(const int* col, const long long* idx, const float* w, int2* cw, long long E, hipStream_t st);
-hipError_t launch_reduce64(const float* part, long long ld, long long n, int nt, const long long* idx, float* G,
-                           hipStream_t st);
+// cw[p] = (pcol[p], w[pidx[p]]) for the npos positions of a plan; pidx[p] < 0: (NO_ROW, 0)
+hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* cw, long long npos, hipStream_t st);
 // src_rows / gz_rows: rows of the gathered state (a gather of a row outside it reads zeros)
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st);
@@ -89,6 +104,8 @@ hipError_t launch_readout_bwd_h(const float* dl, const float* ow, const int* dn_
 hipError_t launch_readout_bwd_w(const float* dl, const float* hK, Lay lh, const int* dn, int n_dn, int n_act,
                                 float* gow_part, float* gob_part, int B, hipStream_t st);
 int readout_chunks(int B);
+// G[idx[i]] += sum over nt tiles of part[t * ld + i] (times -sigmoid(theta[idx[i]]) if theta); idx[i] < 0: skipped,
+// idx == nullptr: i itself.  The indices a launch names are distinct, so no two threads add to one entry.
 hipError_t launch_reduce(const float* part, long long ld, long long n, int nt, const int* idx, const float* theta,
                          float* G, hipStream_t st);
 hipError_t launch_loss(const float* lg, const float* tl, float* dl, float* stats_part, float* stats, int n_act, int B,

@@ -1,12 +1,12 @@
 // Kernels of the flyguy MI355X library.
 //
 // The hot loops are the gather SpMM of a hop (k_fwd) and the fused transposed pass of its backward (k_bwd).
-// Both work on "segments": runs of at most SEG_MAX edges of one row, sorted longest first, 8 segments per
-// wave.  A segment's 8 lanes each hold a float4 of the 32-sample tile and sum its edges in CSR (CSC) order,
-// so a row that is not split is summed exactly as flyguy_train.cu:88 / :171 sum it.  The (source, weight)
-// pairs of 8 consecutive edges are loaded by the 8 lanes at once (one coalesced 64-byte load, the next one
-// already in flight) and handed round the group through LDS; the 8 source rows are then gathered as independent
-// 128-byte lines of the tile's slab, with no branch per edge (slots past a segment's end read row 0 and add 0).
+// Both follow a row plan (kernels.h): segments of at most seg_cap edges of one row, sorted longest first, 8 to a
+// wave.  A segment's 8 lanes each hold a float4 of the 32-sample tile and sum its edges in CSR (CSC) order, so a row
+// that is not split is summed exactly as flyguy_train.cu:88 / :171 sum it.  The (source, weight) pairs of a wave's
+// next step are one contiguous 512-byte block in plan order (one 8-byte load per lane, issued a step ahead) and
+// reach the 8 lanes of each group through LDS; the 8 source rows are then gathered as independent 128-byte lines
+// of the tile's slab, with no branch per edge (unused positions gather NO_ROW, which reads zeros).
 #include "kernels.h"
 
 namespace fg {
@@ -38,12 +38,21 @@ __device__ __forceinline__ float dot4(const float4& a, const float4& b) {
 }
 __device__ __forceinline__ float hsum4(const float4& a) { return ((a.x + a.y) + a.z) + a.w; }
 
-// segment si of the plan, or an empty dead segment when si is past the end or the entry is out of the plan's bounds
+// wave w of the plan ({woff, longest segment}); false when w is past the end or names positions outside the plan
+__device__ __forceinline__ bool load_wave(const Plan& p, int w, int2& wv) {
+    wv = make_int2(0, 0);
+    if (w >= p.nwave) return false;
+    const int2 v = p.wave[w];
+    if (v.x < 0 || v.y < 0 || (long long)v.x + 64 * (((long long)v.y + 7) / 8) > p.npos) return false;
+    wv = v;
+    return true;
+}
+// segment si ({row, slot, re-drive row, 0}); false when si is past the end or names a row or slot outside the plan
 __device__ __forceinline__ bool load_segment(const Plan& p, int si, int4& sg) {
-    sg = make_int4(0, 0, 0, -1);
+    sg = make_int4(0, -1, -1, 0);
     if (si >= p.nseg) return false;
     const int4 v = p.seg[si];
-    if (v.x < 0 || v.x >= p.rows || v.y < 0 || v.y > v.z || v.z > p.E || v.w >= p.nslot) return false;
+    if (v.x < 0 || v.x >= p.rows || v.y >= p.nslot) return false;
     sg = v;
     return true;
 }
@@ -54,47 +63,47 @@ __device__ __forceinline__ bool load_split(const Plan& p, long long i, int4& s) 
 }
 
 // ------------------------------------------------------------------------------------------------ packing
-__global__ void k_pack(const int* __restrict__ col, const int* __restrict__ idx, const float* __restrict__ w,
-                       int2* __restrict__ cw, long long E) {
-    long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    long long i = idx ? idx[e] : e;
-    cw[e] = make_int2(col[e], __float_as_int(w[i]));
-}
-
-__global__ void k_pack64(const int* __restrict__ col, const long long* __restrict__ idx, const float* __restrict__ w,
-                         int2* __restrict__ cw, long long E) {
-    long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    cw[e] = make_int2(col[e], __float_as_int(w[idx[e]]));
+// the (source, weight) pair of every plan position, from the current weights
+__global__ void k_pack(const int* __restrict__ pcol, const int* __restrict__ pidx, const float* __restrict__ w,
+                       int2* __restrict__ cw, long long n) {
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= n) return;
+    const int i = pidx[p];
+    cw[p] = i >= 0 ? make_int2(pcol[p], __float_as_int(w[i])) : make_int2(NO_ROW, 0);
 }
 
 // ------------------------------------------------------------------------------------------------ forward
-// The row's own inputs of the finish (re-drive row, gain, threshold), loaded before the edge loop so that their
+// The row's own inputs of the finish (re-drive row d, gain, threshold), loaded before the edge loop so that their
 // latency hides behind the gathers.
 struct FwdIn {
     float4 dv;
     float g, sp;
 };
-__device__ __forceinline__ FwdIn fwd_inputs(const FwdEpi& e, int t, int tile, int sub) {
+__device__ __forceinline__ FwdIn fwd_inputs(const FwdEpi& e, int t, int d, int tile, int sub) {
     FwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f};
+    if (e.drive && d >= 0) in.dv = *at4(e.drive, e.ldrive, tile, d, sub);
     if (e.info) {
         const float4 r = e.info[t];
         in.g = r.x;
         in.sp = r.y;
-        const int d = __float_as_int(r.z);
-        if (e.drive && d >= 0) in.dv = *at4(e.drive, e.ldrive, tile, d, sub);
     }
     return in;
 }
+// 16-byte store that does not keep the line in L2: the states a pass writes are read by the next kernel, long after
+// the L2 has moved on to other tiles, and should not push the slab being gathered out of it
+__device__ __forceinline__ void st_stream(float4* p, const float4& v) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<f4v*>(p));
+}
 __device__ __forceinline__ void fwd_finish(const FwdEpi& e, int t, int tile, int sub, float4 acc, const FwdIn& in) {
     if (e.drive) add4(in.dv, acc);              // (zero when the row has no re-drive)
-    if (e.z) *at4w(e.z, e.lz, tile, t, sub) = acc;
+    if (e.z) st_stream(at4w(e.z, e.lz, tile, t, sub), acc);
     if (e.info) {
         const float g = in.g, sp = in.sp;
         const float4 hv = make_float4(fmaxf(fmaf(g, acc.x, -sp), 0.f), fmaxf(fmaf(g, acc.y, -sp), 0.f),
                                       fmaxf(fmaf(g, acc.z, -sp), 0.f), fmaxf(fmaf(g, acc.w, -sp), 0.f));
-        *at4w(e.h, e.lh, tile, t, sub) = hv;
+        st_stream(at4w(e.h, e.lh, tile, t, sub), hv);
     }
 }
 
@@ -117,26 +126,6 @@ __device__ __forceinline__ void stage8(int2* slots, int sub, int2 my, int (&c)[8
     __builtin_amdgcn_wave_barrier();
 }
 
-// A source index that no slab reaches: as a buffer offset (index * 128 B) it lies past every slab, so the buffer load
-// returns zeros without touching memory.
-constexpr int NO_ROW = 0x01FFFFFF;
-
-// the largest value over the wave (every lane gets it, in an SGPR)
-__device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
-    return __builtin_amdgcn_readfirstlane(v);
-}
-
-// Pair of edge e of a segment ending at e1, or (NO_ROW, weight 0) past the end: loaded from a clamped index, so no
-// lane branches.  e_last is the segment's last edge (0 for an empty segment; every array has one element at least).
-__device__ __forceinline__ int2 pair_at(const int2* __restrict__ cw, int e, int e1, int e_last) {
-    int2 v = cw[min(e, e_last)];
-    const bool ok = e < e1;
-    v.x = ok ? v.x : NO_ROW;
-    v.y = ok ? v.y : 0;
-    return v;
-}
 
 // Gathers of one tile's slab.  Tiled layout: a raw buffer over the slab (rows x 128 B), 32-bit offsets, so an offset
 // past the slab (NO_ROW, or any bad index) reads zeros.  Plain layout ([rows][B], the HopCuda boundary): global
@@ -168,32 +157,37 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     __shared__ __align__(16) int2 slots[WG / LPR][LPR];
     int rb;
     const int tile = tile_of(blockIdx.x, RB, T, rb);
-    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7;
-    const int si = rb * RPG + grp;
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
+    int2 wv;
+    const bool wok = load_wave(p, w, wv);
+    const int2* q = cw + wv.x + lane;
+    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
     int4 sg;
-    const bool live = load_segment(p, si, sg);
-    const int e1 = sg.z, e_last = max(sg.z - 1, 0);
+    const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     const Slab<TILED> slab(src + (size_t)tile * ls.tile, ls.row, src_rows, sub);
-    float4 acc = (live && sg.w < 0 && epi.bias) ? splat(epi.bias[sg.x]) : splat(0.f);
-    int2 nxt = pair_at(cw, sg.y + sub, e1, e_last);
+    float4 acc = (live && sg.y < 0 && epi.bias) ? splat(epi.bias[sg.x]) : splat(0.f);
     FwdIn in{};
-    if (live && sg.w < 0) in = fwd_inputs(epi, sg.x, tile, sub);
-    // edges left in the wave's longest segment: slots no group needs are not gathered at all
-    for (int eb = sg.y, left = wave_max(sg.z - sg.y); left > 0; eb += 8, left -= 8) {
-        const int2 my = nxt;
-        nxt = pair_at(cw, eb + 8 + sub, e1, e_last);
+    if (live && sg.y < 0) in = fwd_inputs(epi, sg.x, sg.z, tile, sub);
+    // steps of the wave's longest segment; a step gathers only the slots some group still needs
+    for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
-        float w[8];
-        stage8(slots[grp], sub, my, c, w);
+        float wt[8];
+        stage8(slots[grp], sub, nxt, c, wt);
         float4 v[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(c[s], sub) : splat(0.f);
+        // the next step's pairs are requested after this step's gathers: loads complete in order, so the gathers
+        // do not wait for them
+        __builtin_amdgcn_sched_barrier(0);
+        if (left > 8) nxt = q[64 * (j + 1)];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) fma4(w[s], v[s], acc);
+        for (int s = 0; s < 8; ++s) fma4(wt[s], v[s], acc);
     }
     if (!live) return;
-    if (sg.w >= 0) {
-        *at4w(part, lp, tile, sg.w, sub) = acc;
+    if (sg.y >= 0) {
+        *at4w(part, lp, tile, sg.y, sub) = acc;
         return;
     }
     fwd_finish(epi, sg.x, tile, sub, acc, in);
@@ -209,7 +203,7 @@ __global__ __launch_bounds__(WG) void k_fwd_combine(Plan p, const float* __restr
     int4 s;
     if (!load_split(p, i, s)) return;     // whole 8-lane groups leave together
     float4 acc = epi.bias ? splat(epi.bias[s.x]) : splat(0.f);
-    const FwdIn in = fwd_inputs(epi, s.x, tile, sub);
+    const FwdIn in = fwd_inputs(epi, s.x, s.w, tile, sub);
     for (int k = 0; k < s.z; ++k) add4(*at4(part, lp, tile, s.y + k, sub), acc);
     fwd_finish(epi, s.x, tile, sub, acc, in);
 }
@@ -222,27 +216,40 @@ struct BwdIn {
     float gn, sp;
     int d;
 };
-__device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int tile, int sub) {
+// MODE (the epilogue's kind, a compile-time constant so that each kernel is straight-line code for its own case):
+// 0 the raw product, 1 a hop layer (d: the row's re-drive row), 2 the sensory layer
+template <int MODE>
+__device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int tile, int sub) {
     BwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f, -1};
-    if (e.mode == 0) return in;
+    if constexpr (MODE == 0) return in;
+    in.d = MODE == 2 ? j : d;                              // the sensory layer's own drive gradient is complete now:
+    if (in.d >= 0) in.gd = *at4(e.gdrive, e.lgd, tile, in.d, sub);     //   every hop above has added its share
     in.h = *at4(e.h, e.lh, tile, j, sub);
-    if (e.z) in.z = *at4(e.z, e.lz, tile, j, sub);
+    if constexpr (MODE == 2) in.z = *at4(e.z, e.lz, tile, j, sub);
     const float4 r = e.info[j];
     in.gn = r.x;
     in.sp = r.y;
-    if (e.mode == 1) {
-        in.d = __float_as_int(r.z);
-        if (in.d >= 0) in.gd = *at4(e.gdrive, e.lgd, tile, in.d, sub);
-    } else {
-        in.d = j;
-        in.gd = *at4(e.gdrive, e.lgd, tile, j, sub);     // complete: every hop above has added its share
-    }
     return in;
 }
 
+// Reduce-scatter over the 8 lanes of a group: lane s ends with the sum over the group's lanes of d[s].  Three
+// butterfly steps, each pairing lanes that hold the same set of slots and keeping the half named by a lane bit:
+// lanes i and 7-i (row_half_mirror) split the slots by bit 2, then i and i^2, then i and i^1 (quad perms).
+__device__ __forceinline__ float rs8(const float (&d)[8], int sub) {
+    const bool b2 = sub & 4, b1 = sub & 2, b0 = sub & 1;
+    float a[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) a[t] = (b2 ? d[4 + t] : d[t]) + dppf<0x141>(b2 ? d[t] : d[4 + t]);
+    float b[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) b[u] = (b1 ? a[2 + u] : a[u]) + dppf<0x4E>(b1 ? a[u] : a[2 + u]);
+    return (b0 ? b[1] : b[0]) + dppf<0xB1>(b0 ? b[0] : b[1]);
+}
+
 // gh: the gradient of this layer's output h for (row j, tile); every lane of the 8-lane group calls this
+template <int MODE>
 __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int sub, float4 gh, const BwdIn& in) {
-    if (e.mode == 0) {
+    if constexpr (MODE == 0) {
         *at4w(e.gh_out, e.lgh, tile, j, sub) = gh;
         return;
     }
@@ -252,7 +259,7 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     const float gn = in.gn;
     const float4 gzv = make_float4(g.x * gn, g.y * gn, g.z * gn, g.w * gn);
     float4 zv = in.z;
-    if (!e.z) {                                 // z where it matters (h > 0): h = gain * z - softplus(theta)
+    if constexpr (MODE == 1) {                  // z where it matters (h > 0): h = gain * z - softplus(theta)
         zv.x = hv.x > 0.f ? (hv.x + in.sp) / gn : 0.f;
         zv.y = hv.y > 0.f ? (hv.y + in.sp) / gn : 0.f;
         zv.z = hv.z > 0.f ? (hv.z + in.sp) / gn : 0.f;
@@ -264,7 +271,7 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
         e.ggain_part[(size_t)tile * e.gp_ld + j] = pg;
         e.gsum_part[(size_t)tile * e.gp_ld + j] = ps;
     }
-    if (e.mode == 1) {
+    if constexpr (MODE == 1) {
         *at4w(e.gz_out, e.lgz, tile, j, sub) = gzv;
         if (in.d >= 0) {
             float4 v = in.gd;
@@ -278,63 +285,77 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     add4(gzv, gd);
     const float pb = gsum8(hsum4(gd));
     if (sub == 0) e.ginb_part[(size_t)tile * e.gb_ld + j] = pb;
+    // connections 8 at a time: each lane fetches one column, the group shares them, gathers the 8 observation rows
+    // (a column outside the observations reads zeros) and lane s keeps connection s's sum over the tile
+    float* gwo = e.ginw_part + (size_t)tile * e.gw_ld;
     const int f0 = e.in_crow[j], f1 = e.in_crow[j + 1];
-    for (int f = f0; f < f1; ++f) {
-        const int c = e.in_cw[f].x;
-        const float pw = gsum8(dot4(gd, *at4(e.x, e.lx, tile, c, sub)));
-        if (sub == 0) e.ginw_part[(size_t)tile * e.gw_ld + f] = pw;
+    for (int f = f0; f < f1; f += 8) {
+        const int mc = f + sub < f1 ? e.in_col[f + sub] : NO_ROW;
+        int c[8];
+        c[0] = bcast8<0>(mc); c[1] = bcast8<1>(mc); c[2] = bcast8<2>(mc); c[3] = bcast8<3>(mc);
+        c[4] = bcast8<4>(mc); c[5] = bcast8<5>(mc); c[6] = bcast8<6>(mc); c[7] = bcast8<7>(mc);
+        float dd[8];
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) {
+            const bool ok = (unsigned)c[s2] < (unsigned)e.x_rows;
+            const float4 xv = *at4(e.x, e.lx, tile, ok ? c[s2] : 0, sub);
+            dd[s2] = ok ? dot4(gd, xv) : 0.f;
+        }
+        const float pw = rs8(dd, sub);
+        if (f + sub < f1) gwo[f + sub] = pw;
     }
 }
 
-template <bool TILED>
+template <bool TILED, int MODE>
 __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw, const float* __restrict__ gz, Lay lg,
                                             int gz_rows, const float* __restrict__ hs, Lay lhs, float* __restrict__ gwpart,
                                             long long gw_ld, BwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB) {
     __shared__ __align__(16) int2 slots[WG / LPR][LPR];
     int rb;
     const int tile = tile_of(blockIdx.x, RB, T, rb);
-    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7;
-    const int si = rb * RPG + grp;
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
+    int2 wv;
+    const bool wok = load_wave(p, w, wv);
+    const int2* q = cw + wv.x + lane;
+    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
     int4 sg;
-    const bool live = load_segment(p, si, sg);
-    const int e1 = sg.z, e_last = max(sg.z - 1, 0);
+    const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     const float4 hj = live ? *at4(hs, lhs, tile, sg.x, sub) : splat(0.f);
     const Slab<TILED> slab(gz + (size_t)tile * lg.tile, lg.row, gz_rows, sub);
-    float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld : nullptr;
+    // the partial of (position, tile) of this lane's slot: one contiguous 256-byte block per wave and step
+    float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
     float4 acc = splat(0.f);
-    int2 nxt = pair_at(cw, sg.y + sub, e1, e_last);
     BwdIn in{};
-    if (live && sg.w < 0) in = bwd_inputs(epi, sg.x, tile, sub);
-    for (int eb = sg.y, left = wave_max(sg.z - sg.y); left > 0; eb += 8, left -= 8) {
-        const int2 my = nxt;
-        nxt = pair_at(cw, eb + 8 + sub, e1, e_last);
+    if (live && sg.y < 0) in = bwd_inputs<MODE>(epi, sg.x, sg.z, tile, sub);
+    for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
-        float w[8];
-        stage8(slots[grp], sub, my, c, w);
-        const int n = e1 - eb;
+        float wt[8];
+        stage8(slots[grp], sub, nxt, c, wt);
         float4 v[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(c[s], sub) : splat(0.f);
+        __builtin_amdgcn_sched_barrier(0);
+        if (left > 8) nxt = q[64 * (j + 1)];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) fma4(w[s], v[s], acc);
+        for (int s = 0; s < 8; ++s) fma4(wt[s], v[s], acc);
         if (gwp) {
-            float mine = 0.f;
+            float d[8];
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const float ps = gsum8(dot4(hj, v[s]));
-                mine = sub == s ? ps : mine;
-            }
-            if (sub < n) gwp[eb + sub] = mine;
+            for (int s = 0; s < 8; ++s) d[s] = dot4(hj, v[s]);
+            gwp[64 * j] = rs8(d, sub);
         }
     }
     if (!live) return;
-    if (sg.w >= 0) {
-        *at4w(part, lp, tile, sg.w, sub) = acc;
+    if (sg.y >= 0) {
+        *at4w(part, lp, tile, sg.y, sub) = acc;
         return;
     }
-    bwd_finish(epi, sg.x, tile, sub, acc, in);
+    bwd_finish<MODE>(epi, sg.x, tile, sub, acc, in);
 }
 
+template <int MODE>
 __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restrict__ part, Lay lp, BwdEpi epi, int T) {
     long long q = ((long long)blockIdx.x * WG + threadIdx.x);
     const int sub = (int)(q & 7);
@@ -344,9 +365,9 @@ __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restr
     int4 s;
     if (!load_split(p, i, s)) return;     // whole 8-lane groups leave together
     float4 acc = splat(0.f);
-    const BwdIn in = bwd_inputs(epi, s.x, tile, sub);
+    const BwdIn in = bwd_inputs<MODE>(epi, s.x, s.w, tile, sub);
     for (int k = 0; k < s.z; ++k) add4(*at4(part, lp, tile, s.y + k, sub), acc);
-    bwd_finish(epi, s.x, tile, sub, acc, in);
+    bwd_finish<MODE>(epi, s.x, tile, sub, acc, in);
 }
 
 // ------------------------------------------------------------------------------------------------ obs / logits
@@ -435,7 +456,7 @@ __global__ __launch_bounds__(WG) void k_readout_bwd_h(const float* __restrict__ 
         const float4* d4 = reinterpret_cast<const float4*>(dlT) + sub;
         for (int a = 0; a < n_act; ++a) fma4(owc[r * n_act + a], d4[a * LPR], acc);
     }
-    bwd_finish(epi, t, tile, sub, acc, bwd_inputs(epi, t, tile, sub));
+    bwd_finish<1>(epi, t, tile, sub, acc, bwd_inputs<1>(epi, t, epi.drow ? epi.drow[t] : -1, tile, sub));
 }
 
 // per chunk of 16 tiles: gow[a][j] partial = sum_b dl[b][a] * hK[dn[j]][b], gob[a] partial = sum_b dl[b][a]
@@ -485,25 +506,18 @@ __global__ __launch_bounds__(WG) void k_readout_bwd_w(const float* __restrict__ 
 }
 
 // ------------------------------------------------------------------------------------------------ reductions
-// G[idx[i]] += sum_t part[t * ld + i]  (times -sigmoid(theta[idx[i]]) when theta is given: the threshold's gradient)
+// G[idx[i]] += sum_t part[t * ld + i]  (times -sigmoid(theta[idx[i]]) when theta is given: the threshold's gradient);
+// idx[i] < 0 (a plan position no edge uses) adds nothing
 __global__ void k_reduce(const float* __restrict__ part, long long ld, long long n, int nt, const int* __restrict__ idx,
                          const float* __restrict__ theta, float* __restrict__ G) {
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
+    const long long o = idx ? idx[i] : i;
+    if (o < 0) return;
     float s = 0.f;
     for (int t = 0; t < nt; ++t) s += part[(size_t)t * ld + i];
-    const long long o = idx ? idx[i] : i;
     if (theta) s *= -sigmoid_f(theta[o]);
     G[o] += s;
-}
-
-__global__ void k_reduce64(const float* __restrict__ part, long long ld, long long n, int nt,
-                           const long long* __restrict__ idx, float* __restrict__ G) {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    float s = 0.f;
-    for (int t = 0; t < nt; ++t) s += part[(size_t)t * ld + i];
-    G[idx[i]] += s;
 }
 
 // KL(teacher || student) per sample, dl = d(mean loss)/d logits (flyguy_train.cu:104-123); one thread per sample
@@ -619,29 +633,16 @@ __global__ void k_export(const float* __restrict__ src, Lay ls, float* __restric
 // ------------------------------------------------------------------------------------------------ launchers
 static inline unsigned blocks(long long n, int per = WG) { return (unsigned)((n + per - 1) / per); }
 
-hipError_t launch_pack(const int* col, const int* idx, const float* w, int2* cw, long long E, hipStream_t st) {
-    if (E <= 0) return hipSuccess;
-    k_pack<<<blocks(E), WG, 0, st>>>(col, idx, w, cw, E);
-    return hipGetLastError();
-}
-
-hipError_t launch_pack64(const int* col, const long long* idx, const float* w, int2* cw, long long E, hipStream_t st) {
-    if (E <= 0) return hipSuccess;
-    k_pack64<<<blocks(E), WG, 0, st>>>(col, idx, w, cw, E);
-    return hipGetLastError();
-}
-
-hipError_t launch_reduce64(const float* part, long long ld, long long n, int nt, const long long* idx, float* G,
-                           hipStream_t st) {
-    if (n <= 0) return hipSuccess;
-    k_reduce64<<<blocks(n), WG, 0, st>>>(part, ld, n, nt, idx, G);
+hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* cw, long long npos, hipStream_t st) {
+    if (npos <= 0) return hipSuccess;
+    k_pack<<<blocks(npos), WG, 0, st>>>(pcol, pidx, w, cw, npos);
     return hipGetLastError();
 }
 
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st) {
-    if (p.nseg > 0) {
-        const int RB = (p.nseg + RPG - 1) / RPG;
+    if (p.nwave > 0) {
+        const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
         if (ls.row == TW)
             k_fwd<true><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB);
         else
@@ -656,24 +657,40 @@ hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, i
     return hipSuccess;
 }
 
-hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
-                      float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st) {
-    if (p.nseg > 0) {
-        const int RB = (p.nseg + RPG - 1) / RPG;
-        if (lg.row == TW)
-            k_bwd<true><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part,
-                                                                      lp, T, RB);
-        else
-            k_bwd<false><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part,
-                                                                       lp, T, RB);
+template <bool TILED, int MODE>
+static hipError_t launch_bwd_as(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc,
+                                Lay lhs, float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T,
+                                hipStream_t st) {
+    if (p.nwave > 0) {
+        const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
+        k_bwd<TILED, MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld,
+                                                                         epi, part, lp, T, RB);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     if (p.nsplit > 0) {
-        k_bwd_combine<<<blocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, lp, epi, T);
+        k_bwd_combine<MODE><<<blocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, lp, epi, T);
         return hipGetLastError();
     }
     return hipSuccess;
+}
+
+hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
+                      float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st) {
+    const bool tiled_ = lg.row == TW;
+    switch (epi.mode) {
+        case 0:
+            return tiled_ ? launch_bwd_as<true, 0>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, st)
+                          : launch_bwd_as<false, 0>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, st);
+        case 1:
+            if (!tiled_) return hipErrorInvalidValue;
+            return launch_bwd_as<true, 1>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, st);
+        case 2:
+            if (!tiled_) return hipErrorInvalidValue;
+            return launch_bwd_as<true, 2>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, st);
+        default:
+            return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStream_t st) {

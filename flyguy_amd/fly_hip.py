@@ -9,12 +9,13 @@ from __future__ import annotations
 
 from collections import OrderedDict
 
+import numpy as np
 import torch
 
-from ._lib import call, lib, plan_segments
+from ._lib import NO_ROW, call, lib, plan_rows
 
-# Row plans per structure tensor.  An entry holds the tensor itself: while it is cached its memory cannot be handed
-# to another tensor, so the key (address, length, version) cannot come to name different contents.
+# Row plans per structure.  An entry holds the index tensors themselves: while they are cached their memory cannot be
+# handed to other tensors, so the key (addresses, lengths, versions) cannot come to name different contents.
 _plans: OrderedDict = OrderedDict()
 _checked: OrderedDict = OrderedDict()
 _CACHE = 64
@@ -35,21 +36,44 @@ def _remember(cache: OrderedDict, key, value):
         cache.popitem(last=False)
 
 
-def _plan(rowptr: torch.Tensor, n_edges: int):
-    key = (rowptr.data_ptr(), rowptr.numel(), rowptr.device, rowptr._version)
+def _key(t: torch.Tensor | None):
+    return None if t is None else (t.data_ptr(), t.numel(), t.device, t._version)
+
+
+def _plan(rowptr: torch.Tensor, col: torch.Tensor, idx: torch.Tensor | None, n_edges: int):
+    """The device plan of a product: its row plan, and per plan position the source row (col[edge]) and the weight
+    index (idx[edge], or the edge itself)."""
+    key = (_key(rowptr), _key(col), _key(idx))
     hit = _plans.get(key)
-    if hit is not None and hit[0] is rowptr:
+    if hit is not None and hit[0] is rowptr and hit[1] is col and hit[2] is idx:
         _plans.move_to_end(key)
-        return hit[1]
+        return hit[3]
     rp = rowptr.detach().cpu().numpy()
     if rp[0] != 0 or rp[-1] != n_edges or (len(rp) > 1 and (rp[1:] < rp[:-1]).any()):
         raise ValueError("HopHip: row pointer does not describe the connection arrays it came with")
-    seg, split, nslot = plan_segments(rp)
+    p = plan_rows(rp)
+    pos = p["pos"].astype(np.int64)
+    used = pos >= 0
+    c = col.detach().cpu().numpy()
+    pcol = np.full(len(pos), NO_ROW, np.int32)
+    pcol[used] = c[pos[used]]
+    pidx = np.full(len(pos), -1, np.int32)
+    pidx[used] = (idx.detach().cpu().numpy()[pos[used]] if idx is not None else pos[used])
     dev = rowptr.device
-    p = (torch.as_tensor(seg, device=dev).contiguous(), torch.as_tensor(split, device=dev).contiguous(), len(seg),
-         len(split), nslot)
-    _remember(_plans, key, (rowptr, p))
-    return p
+
+    def put(a, width=None):
+        a = a if len(a) else np.zeros((1,) + ((width,) if width else ()), np.int32)
+        return torch.as_tensor(np.ascontiguousarray(a), device=dev)
+    d = {"wave": put(p["wave"], 2), "seg": put(p["seg"], 4), "split": put(p["split"], 4), "pcol": put(pcol),
+         "pidx": put(pidx), "nwave": len(p["wave"]), "nseg": len(p["seg"]), "nsplit": len(p["split"]),
+         "nslot": p["nslot"], "npos": len(pos)}
+    _remember(_plans, key, (rowptr, col, idx, d))
+    return d
+
+
+def _args(d):
+    return (d["wave"].data_ptr(), d["nwave"], d["seg"].data_ptr(), d["nseg"], d["split"].data_ptr(), d["nsplit"],
+            d["nslot"], d["pcol"].data_ptr(), d["pidx"].data_ptr(), d["npos"])
 
 
 def _check_index(idx: torch.Tensor, bound: int, what: str) -> None:
@@ -76,14 +100,13 @@ class HopHip(torch.autograd.Function):
         E = col.numel()
         if w.numel() != E or col.dtype != torch.int32 or crow.dtype != torch.int64:
             raise ValueError("HopHip: w / col / crow do not match (float32 w[E], int32 col[E], int64 crow)")
-        seg, split, nseg, nsplit, nslot = _plan(crow, E)
         _check_index(col, h.shape[0], "source index")
+        d = _plan(crow, col, None, E)
         out = torch.empty(n_rows, B, device=h.device)
-        cw = torch.empty(max(E, 1), 2, dtype=torch.int32, device=h.device)
-        scratch = torch.empty(max(nslot * B, 1), device=h.device)
-        call("fh_spmm", crow.data_ptr(), col.data_ptr(), w.data_ptr(), h.data_ptr(), out.data_ptr(), n_rows, h.shape[0],
-             B, E, seg.data_ptr(), nseg, split.data_ptr(), nsplit, nslot, cw.data_ptr(), scratch.data_ptr(),
-             torch.cuda.current_stream(h.device).cuda_stream)
+        cw = torch.empty(max(d["npos"], 1), 2, dtype=torch.int32, device=h.device)
+        scratch = torch.empty(max(d["nslot"] * B, 1), device=h.device)
+        call("fh_spmm", *_args(d), w.data_ptr(), h.data_ptr(), out.data_ptr(), n_rows, h.shape[0], B, cw.data_ptr(),
+             scratch.data_ptr(), torch.cuda.current_stream(h.device).cuda_stream)
         ctx.save_for_backward(w, h, tcrow, tcol, tperm)
         ctx.n_rows = n_rows
         return out
@@ -97,17 +120,16 @@ class HopHip(torch.autograd.Function):
         E = tcol.numel()
         if tperm.numel() != E or w.numel() != E or tcol.dtype != torch.int32 or tperm.dtype != torch.int64:
             raise ValueError("HopHip: tcol / tperm / w do not match")
-        seg, split, nseg, nsplit, nslot = _plan(tcrow, E)
         _check_index(tcol, ctx.n_rows, "target index")
         _check_index(tperm, E, "transposed order")
+        d = _plan(tcrow, tcol, tperm, E)
         gh = torch.empty(n_src, B, device=h.device)
         gw = torch.zeros_like(w) if ctx.needs_input_grad[0] else None
-        cw = torch.empty(max(E, 1), 2, dtype=torch.int32, device=h.device)
-        gwpart = torch.empty(max(E * (B // 32), 1), device=h.device) if gw is not None else None
-        scratch = torch.empty(max(nslot * B, 1), device=h.device)
-        call("fh_spmm_bwd", tcrow.data_ptr(), tcol.data_ptr(), tperm.data_ptr(), w.data_ptr(),
-             gz.data_ptr(), h.data_ptr(), gh.data_ptr(), gw.data_ptr() if gw is not None else None, ctx.n_rows, n_src, B,
-             E, seg.data_ptr(), nseg, split.data_ptr(), nsplit, nslot, cw.data_ptr(),
+        cw = torch.empty(max(d["npos"], 1), 2, dtype=torch.int32, device=h.device)
+        gwpart = torch.empty(max(d["npos"] * (B // 32), 1), device=h.device) if gw is not None else None
+        scratch = torch.empty(max(d["nslot"] * B, 1), device=h.device)
+        call("fh_spmm_bwd", *_args(d), w.data_ptr(), gz.data_ptr(), h.data_ptr(), gh.data_ptr(),
+             gw.data_ptr() if gw is not None else None, ctx.n_rows, n_src, B, cw.data_ptr(),
              gwpart.data_ptr() if gwpart is not None else None, scratch.data_ptr(),
              torch.cuda.current_stream(h.device).cuda_stream)
         return gw, (gh if ctx.needs_input_grad[1] else None), None, None, None, None, None, None

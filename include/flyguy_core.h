@@ -102,30 +102,40 @@ void fc_export_state(void* core, int layer, int what, float* dst, int B);
 void fc_profile(void* core, int on);
 int fc_profile_read(void* core, double* ms, long long* counts, int n, int reset);
 
-/* The row plan of one sparse product, computed on the host (no device needed): every row is cut into segments
- * of at most seg_max edges, sorted longest first (ties: row, then segment order).  rowptr has rows+1 entries.
- * seg_out receives 4 ints per segment {row, begin, end, slot} (slot -1: the whole row, else the index of its
- * partial sum), split_out 4 ints per split row {row, first slot, segments, 0}.  counts[0..2] = segments, split
- * rows, slots.  Returns 0, or -1 if the capacities are too small or rowptr is malformed. */
-int fc_plan_segments(const int* rowptr, int rows, int seg_max, int* seg_out, long long seg_cap, int* split_out,
-                     long long split_cap, long long* counts);
+/* The row plan of one sparse product, computed on the host (no device needed).  Every row is cut into segments of
+ * at most seg_max edges; the segments are sorted longest first (ties: row, then segment order) and dealt 8 to a
+ * wave; the edges are laid out in plan order, edge k of the segment of group g of wave w at position
+ * woff[w] + 64 (k / 8) + 8 g + k % 8 (a wave takes 64 positions per 8 edges of its longest segment).
+ *   wave_out:  2 ints per wave {woff, longest segment}
+ *   seg_out:   4 ints per segment {row, slot, -1, 0} (slot -1: the whole row, else the index of its partial sum)
+ *   split_out: 4 ints per split row {row, first slot, segments, -1}
+ *   pos_out:   per position the CSR edge it holds (-1: none)
+ * counts[0..4] = waves, segments, split rows, slots, positions.  Null outputs with zero capacities return the counts
+ * only.  Returns 0, or -1 if a capacity is too small or rowptr (rows+1 entries) is malformed.  (No counterpart in
+ * the reference, whose kernels take plain CSR arrays, flyguy_train.cu:75-101.) */
+int fc_plan_rows(const int* rowptr, int rows, int seg_max, int* wave_out, long long wave_cap, int* seg_out,
+                 long long seg_cap, int* split_out, long long split_cap, int* pos_out, long long pos_cap,
+                 long long* counts);
 
 /* ---- the HopCuda-style hop (flyguy/fly_cuda.py:78-115): states [rows][B] row-major, B % 32 == 0 ---- */
 
-/* out[n_rows][B] = A h, A in CSR form: rowptr (int64, n_rows+1), col (int32), w (E entries).  plan: int4 segments of
- * rowptr from fc_plan_segments (nseg of them, nsplit split rows after them in split); cw: scratch for E (col,w)
- * pairs; scratch: partial sums, nslot * B floats.  All device.  Replaces the spmm_f kernel, fly_cuda.py:27-33. */
-void fh_spmm(const long long* rowptr, const int* col, const float* w, const float* h, float* out, int n_rows,
-             int n_src, int B, long long E, const int* plan, int nseg, const int* split, int nsplit, int nslot, void* cw,
-             float* scratch, void* stream);
+/* out[n_rows][B] = A h for the CSR matrix A (n_rows rows over n_src sources, E weights w in CSR order), through the
+ * row plan of its row pointer (fc_plan_rows, copied to the device): wave (2 ints per wave), seg (4 ints per
+ * segment), split (4 ints per split row), nslot; pcol / pidx: per plan position its source row col[pos] and weight
+ * index pos (both for an unused position: pidx -1).  cw: scratch of npos (col, w) pairs; scratch: nslot * B floats.
+ * All device.  Replaces the spmm_f kernel, fly_cuda.py:27-33. */
+void fh_spmm(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+             const int* pcol, const int* pidx, long long npos, const float* w, const float* h, float* out, int n_rows,
+             int n_src, int B, void* cw, float* scratch, void* stream);
 
-/* Backward of fh_spmm: gh[n_src][B] = A^T gz and gw[tperm[e]] += sum_b gz[row_e][b] h[col_e][b] (gw is added to),
- * from the transposed (CSC) form tcrow (int64, n_src+1) / tcol (int32) / tperm (int64, CSC position -> edge).
- * plan / split / nslot: fc_plan_segments of tcrow; cw: scratch for E pairs; gwpart: scratch of E * B/32 floats;
- * scratch: nslot * B floats.  Replaces sddmm_f + spmm_f over the CSC, fly_cuda.py:45-50,93-115. */
-void fh_spmm_bwd(const long long* tcrow, const int* tcol, const long long* tperm, const float* w, const float* gz,
-                 const float* h, float* gh, float* gw, int n_rows, int n_src, int B, long long E, const int* plan,
-                 int nseg, const int* split, int nsplit, int nslot, void* cw, float* gwpart, float* scratch, void* stream);
+/* Backward of fh_spmm: gh[n_src][B] = A^T gz and gw[e] += sum_b gz[row_e][b] h[col_e][b] (gw is added to), through the
+ * row plan of the transposed (CSC) row pointer: pcol / pidx per position the CSC column tcol[pos] (a row of gz) and
+ * the CSR edge tperm[pos] it is.  gwpart: scratch of npos * B/32 floats (unused when gw is null); scratch: nslot * B
+ * floats.  Replaces sddmm_f + spmm_f over the CSC, fly_cuda.py:45-50,93-115. */
+void fh_spmm_bwd(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                 const int* pcol, const int* pidx, long long npos, const float* w, const float* gz, const float* h,
+                 float* gh, float* gw, int n_rows, int n_src, int B, void* cw, float* gwpart, float* scratch,
+                 void* stream);
 
 #ifdef __cplusplus
 }
