@@ -421,7 +421,7 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
     c->ginw = dalloc<float>(*c, Tm * c->E_in);
     c->gow_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act * c->n_dn);
     c->gob_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act);
-    c->stats_part = dalloc<float>(*c, (size_t)2 * ((bm + WG - 1) / WG));
+    c->stats_part = dalloc<float>(*c, (size_t)2 * ((bm + 63) / 64));     // one pair per 64 samples (k_loss)
     c->stats = dalloc<float>(*c, 4);
     c->red = dalloc<float>(*c, 1024);
     c->nrm = dalloc<float>(*c, 1);

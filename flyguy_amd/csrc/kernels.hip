@@ -386,49 +386,38 @@ __global__ __launch_bounds__(WG) void k_obs_in(const float* __restrict__ obs, fl
     }
 }
 
-// logits[b][a] = ob[a] + sum_j ow[a][j] * hK[dn[j]][b], summed in j order (flyguy_train.cu:95-101)
+// logits[b][a] = ob[a] + sum_j ow[a][j] * hK[dn[j]][b], summed in j order (flyguy_train.cu:95-101).  One workgroup per
+// (tile, 32 actions): lane group g (8 lanes, a float4 of the tile's samples each) owns action a0 + g; chunks of 64
+// read-out rows and the matching weights are staged in LDS.
+constexpr int LG_J = 64;
 __global__ __launch_bounds__(WG) void k_logits(const float* __restrict__ hK, Lay lh, const int* __restrict__ dn, int n_dn,
                                                const float* __restrict__ ow, const float* __restrict__ ob, int n_act,
                                                float* __restrict__ logits) {
-    __shared__ float4 hs[64][LPR];
-    __shared__ float ws[64][97];
-    const int tile = blockIdx.x, c4 = threadIdx.x & 7, ag = threadIdx.x >> 3;
-    for (int a0 = 0; a0 < n_act; a0 += 96) {
-        float4 acc[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int a = a0 + ag + 32 * i;
-            acc[i] = splat(a < n_act ? ob[a] : 0.f);
+    __shared__ float4 hs[LG_J][LPR];
+    __shared__ float ws[RPG][LG_J + 1];
+    const int tile = blockIdx.x, a0 = blockIdx.y * RPG;
+    const int g = threadIdx.x >> 3, sub = threadIdx.x & 7, a = a0 + g;
+    float4 acc = splat(a < n_act ? ob[a] : 0.f);
+    for (int j0 = 0; j0 < n_dn; j0 += LG_J) {
+        const int nj = min(LG_J, n_dn - j0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < LG_J * LPR; i += WG) {
+            const int jj = i / LPR, q = i % LPR;
+            hs[jj][q] = jj < nj ? *at4(hK, lh, tile, dn[j0 + jj], q) : splat(0.f);
         }
-        for (int j0 = 0; j0 < n_dn; j0 += 64) {
-            const int nj = min(64, n_dn - j0);
-            __syncthreads();
-            for (int i = threadIdx.x; i < 64 * LPR; i += WG) {
-                const int jj = i / LPR, q = i % LPR;
-                hs[jj][q] = jj < nj ? *at4(hK, lh, tile, dn[j0 + jj], q) : splat(0.f);
-            }
-            for (int i = threadIdx.x; i < 64 * 96; i += WG) {
-                const int aa = i / 64, jj = i % 64;
-                ws[jj][aa] = (jj < nj && a0 + aa < n_act) ? ow[(size_t)(a0 + aa) * n_dn + j0 + jj] : 0.f;
-            }
-            __syncthreads();
-            for (int jj = 0; jj < nj; ++jj) {
-                const float4 h4 = hs[jj][c4];
-#pragma unroll
-                for (int i = 0; i < 3; ++i) fma4(ws[jj][ag + 32 * i], h4, acc[i]);
-            }
+        for (int i = threadIdx.x; i < RPG * LG_J; i += WG) {
+            const int aa = i / LG_J, jj = i % LG_J;
+            ws[aa][jj] = (jj < nj && a0 + aa < n_act) ? ow[(size_t)(a0 + aa) * n_dn + j0 + jj] : 0.f;
         }
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int a = a0 + ag + 32 * i;
-            if (a >= n_act) continue;
-            float* o = logits + (size_t)(tile * TW + c4 * 4) * n_act + a;
-            o[0] = acc[i].x;
-            o[n_act] = acc[i].y;
-            o[2 * n_act] = acc[i].z;
-            o[3 * n_act] = acc[i].w;
-        }
+        __syncthreads();
+        for (int jj = 0; jj < nj; ++jj) fma4(ws[g][jj], hs[jj][sub], acc);
     }
+    if (a >= n_act) return;
+    float* o = logits + (size_t)(tile * TW + sub * 4) * n_act + a;
+    o[0] = acc.x;
+    o[n_act] = acc.y;
+    o[2 * n_act] = acc.z;
+    o[3 * n_act] = acc.w;
 }
 
 // gh of the top layer from the logits' gradient, then the neuron backward (flyguy_train.cu:136-141, 143-156)
@@ -515,53 +504,70 @@ __global__ void k_reduce(const float* __restrict__ part, long long ld, long long
     const long long o = idx ? idx[i] : i;
     if (o < 0) return;
     float s = 0.f;
-    for (int t = 0; t < nt; ++t) s += part[(size_t)t * ld + i];
+    int t = 0;
+    for (; t + 8 <= nt; t += 8) {              // 8 loads in flight, added in tile order
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = part[(size_t)(t + k) * ld + i];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s += v[k];
+    }
+    for (; t < nt; ++t) s += part[(size_t)t * ld + i];
     if (theta) s *= -sigmoid_f(theta[o]);
     G[o] += s;
 }
 
-// KL(teacher || student) per sample, dl = d(mean loss)/d logits (flyguy_train.cu:104-123); one thread per sample
-__global__ __launch_bounds__(WG) void k_loss(const float* __restrict__ lg, const float* __restrict__ tl, float* __restrict__ dl,
-                                             float* __restrict__ stats_part, int n_act, int B, float it) {
-    __shared__ float red[2][WG];
-    const int b = blockIdx.x * WG + threadIdx.x;
+// KL(teacher || student) per sample, dl = d(mean loss)/d logits (flyguy_train.cu:104-123).  One wave per 64 samples:
+// the samples' logits are staged through LDS with coalesced loads (and dl leaves the same way); each lane then does
+// one sample's softmax arithmetic.  Per-block sums of KL and argmax agreement go to stats_part.
+constexpr int LOSS_S = 64;
+__global__ __launch_bounds__(LOSS_S) void k_loss(const float* __restrict__ lg, const float* __restrict__ tl,
+                                                 float* __restrict__ dl, float* __restrict__ stats_part, int n_act,
+                                                 int B, float it) {
+    extern __shared__ float sm[];
+    float* S = sm;                              // [LOSS_S][n_act] student logits, then dl
+    float* Tt = sm + (size_t)LOSS_S * n_act;    // [LOSS_S][n_act] teacher logits * (1 / temperature)
+    const int b0 = blockIdx.x * LOSS_S, nb = min(LOSS_S, B - b0);
+    const size_t base = (size_t)b0 * n_act;
+    for (int i = threadIdx.x; i < nb * n_act; i += LOSS_S) {
+        S[i] = lg[base + i];
+        Tt[i] = tl[base + i] * it;
+    }
+    __syncthreads();
     float kl = 0.f, agree = 0.f;
-    if (b < B) {
-        const float* s = lg + (size_t)b * n_act;
-        const float* t = tl + (size_t)b * n_act;
+    if ((int)threadIdx.x < nb) {
+        float* s = S + (size_t)threadIdx.x * n_act;
+        const float* t = Tt + (size_t)threadIdx.x * n_act;
         float ms = -1e30f, mt = -1e30f;
         int as = 0, at = 0;
         for (int a = 0; a < n_act; ++a) {
-            const float sv = s[a], tv = t[a] * it;
+            const float sv = s[a], tv = t[a];
             if (sv > ms) { ms = sv; as = a; }
             if (tv > mt) { mt = tv; at = a; }
         }
         float zs = 0.f, zt = 0.f;
         for (int a = 0; a < n_act; ++a) {
             zs += expf(s[a] - ms);
-            zt += expf(t[a] * it - mt);
+            zt += expf(t[a] - mt);
         }
         const float ls = ms + logf(zs), lt = mt + logf(zt);
         for (int a = 0; a < n_act; ++a) {
-            const float lps = s[a] - ls, lpt = t[a] * it - lt, pt = expf(lpt);
+            const float lps = s[a] - ls, lpt = t[a] - lt, pt = expf(lpt);
             kl += pt * (lpt - lps);
-            dl[(size_t)b * n_act + a] = (expf(lps) - pt) / (float)B;
+            s[a] = (expf(lps) - pt) / (float)B;
         }
         agree = as == at ? 1.f : 0.f;
     }
-    red[0][threadIdx.x] = kl;
-    red[1][threadIdx.x] = agree;
     __syncthreads();
-    for (int s = WG / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            red[0][threadIdx.x] += red[0][threadIdx.x + s];
-            red[1][threadIdx.x] += red[1][threadIdx.x + s];
-        }
-        __syncthreads();
+    for (int i = threadIdx.x; i < nb * n_act; i += LOSS_S) dl[base + i] = S[i];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        kl += __shfl_xor(kl, o, 64);
+        agree += __shfl_xor(agree, o, 64);
     }
     if (threadIdx.x == 0) {
-        stats_part[2 * blockIdx.x] = red[0][0];
-        stats_part[2 * blockIdx.x + 1] = red[1][0];
+        stats_part[2 * blockIdx.x] = kl;
+        stats_part[2 * blockIdx.x + 1] = agree;
     }
 }
 __global__ void k_sum_pairs(const float* __restrict__ part, int n, float* __restrict__ out) {
@@ -701,7 +707,8 @@ hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStre
 
 hipError_t launch_logits(const float* hK, Lay lh, const int* dn, int n_dn, const float* ow, const float* ob, int n_act,
                          float* logits, int B, hipStream_t st) {
-    k_logits<<<(unsigned)(B / TW), WG, 0, st>>>(hK, lh, dn, n_dn, ow, ob, n_act, logits);
+    k_logits<<<dim3((unsigned)(B / TW), (unsigned)((n_act + RPG - 1) / RPG)), WG, 0, st>>>(hK, lh, dn, n_dn, ow, ob, n_act,
+                                                                                         logits);
     return hipGetLastError();
 }
 
@@ -730,8 +737,9 @@ hipError_t launch_reduce(const float* part, long long ld, long long n, int nt, c
 
 hipError_t launch_loss(const float* lg, const float* tl, float* dl, float* stats_part, float* stats, int n_act, int B,
                        float it, hipStream_t st) {
-    const unsigned nb = blocks(B);
-    k_loss<<<nb, WG, 0, st>>>(lg, tl, dl, stats_part, n_act, B, it);
+    if (n_act > 128) return hipErrorInvalidValue;       // the staged logits must fit the LDS
+    const unsigned nb = blocks(B, LOSS_S);
+    k_loss<<<nb, LOSS_S, (size_t)2 * LOSS_S * n_act * sizeof(float), st>>>(lg, tl, dl, stats_part, n_act, B, it);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     k_sum_pairs<<<1, 64, 0, st>>>(stats_part, (int)nb, stats);
