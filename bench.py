@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the fly actor's batched inference and teaching step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 1024] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096] [--no-cpu]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -95,8 +95,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=4096)
-    ap.add_argument("--cpu-sample", type=int, default=1024)
-    ap.add_argument("--cpu-train-batch", type=int, default=32)
+    ap.add_argument("--cpu-sample", type=int, default=8192)
+    ap.add_argument("--cpu-train-batch", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 copies of 1 GiB (read 1 GiB, write 1 GiB each) so a counter run can scale "
