@@ -16,8 +16,8 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libflyguy_core.so"
-SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "hop_api.hip")]
-HEADERS = [PKG / "csrc" / "common.h", PKG / "csrc" / "kernels.h", ROOT / "include" / "flyguy_core.h"]
+SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "hop_api.hip", "half.hip")]
+HEADERS = [PKG / "csrc" / "common.h", PKG / "csrc" / "kernels.h", PKG / "csrc" / "device.h", ROOT / "include" / "flyguy_core.h"]
 ARCH = os.environ.get("FLYGUY_OFFLOAD_ARCH", "gfx950")
 
 

@@ -7,60 +7,9 @@
 // next step are one contiguous 512-byte block in plan order (one 8-byte load per lane, issued a step ahead) and
 // reach the 8 lanes of each group through LDS; the 8 source rows are then gathered as independent 128-byte lines
 // of the tile's slab, with no branch per edge (unused positions gather NO_ROW, which reads zeros).
-#include "kernels.h"
+#include "device.h"
 
 namespace fg {
-
-__device__ __forceinline__ const float4* at4(const float* base, Lay L, int tile, int row, int sub) {
-    return reinterpret_cast<const float4*>(base + (size_t)tile * L.tile + (size_t)row * L.row) + sub;
-}
-__device__ __forceinline__ float4* at4w(float* base, Lay L, int tile, int row, int sub) {
-    return reinterpret_cast<float4*>(base + (size_t)tile * L.tile + (size_t)row * L.row) + sub;
-}
-__device__ __forceinline__ float4 splat(float v) { return make_float4(v, v, v, v); }
-
-template <int C>
-__device__ __forceinline__ float dppf(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), C, 0xf, 0xf, true));
-}
-// sum over the 8 lanes of a group with DPP (quad swaps, then the half-row mirror); every lane gets the total
-__device__ __forceinline__ float gsum8(float v) {
-    v += dppf<0xB1>(v);      // quad_perm [1,0,3,2]
-    v += dppf<0x4E>(v);      // quad_perm [2,3,0,1]
-    v += dppf<0x141>(v);     // row_half_mirror
-    return v;
-}
-__device__ __forceinline__ float dot4(const float4& a, const float4& b) {
-    float p = a.x * b.x;
-    p = fmaf(a.y, b.y, p);
-    p = fmaf(a.z, b.z, p);
-    return fmaf(a.w, b.w, p);
-}
-__device__ __forceinline__ float hsum4(const float4& a) { return ((a.x + a.y) + a.z) + a.w; }
-
-// wave w of the plan ({woff, longest segment}); false when w is past the end or names positions outside the plan
-__device__ __forceinline__ bool load_wave(const Plan& p, int w, int2& wv) {
-    wv = make_int2(0, 0);
-    if (w >= p.nwave) return false;
-    const int2 v = p.wave[w];
-    if (v.x < 0 || v.y < 0 || (long long)v.x + 64 * (((long long)v.y + 7) / 8) > p.npos) return false;
-    wv = v;
-    return true;
-}
-// segment si ({row, slot, re-drive row, 0}); false when si is past the end or names a row or slot outside the plan
-__device__ __forceinline__ bool load_segment(const Plan& p, int si, int4& sg) {
-    sg = make_int4(0, -1, -1, 0);
-    if (si >= p.nseg) return false;
-    const int4 v = p.seg[si];
-    if (v.x < 0 || v.x >= p.rows || v.y >= p.nslot) return false;
-    sg = v;
-    return true;
-}
-__device__ __forceinline__ bool load_split(const Plan& p, long long i, int4& s) {
-    if (i >= p.nsplit) return false;
-    s = p.split[i];
-    return s.x >= 0 && s.x < p.rows && s.y >= 0 && s.z >= 0 && (long long)s.y + s.z <= p.nslot;
-}
 
 // ------------------------------------------------------------------------------------------------ packing
 // the (source, weight) pair of every plan position, from the current weights
@@ -106,50 +55,6 @@ __device__ __forceinline__ void fwd_finish(const FwdEpi& e, int t, int tile, int
         st_stream(at4w(e.h, e.lh, tile, t, sub), hv);
     }
 }
-
-// The (index, weight) pairs of a group's next 8 edges reach all 8 lanes of the group through the wave's own LDS
-// slots: each lane writes the pair it loaded (one 8-byte store), then reads the group's 8 pairs back (four 16-byte
-// reads the 8 lanes share).  A wave only touches its own slots and its lanes run in lockstep; wave_barrier keeps
-// the compiler from moving the reads above the store or the next store above the reads.
-__device__ __forceinline__ void stage8(int2* slots, int sub, int2 my, int (&c)[8], float (&w)[8]) {
-    slots[sub] = my;
-    __builtin_amdgcn_wave_barrier();
-    const int4* q = reinterpret_cast<const int4*>(slots);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int4 v = q[i];
-        c[2 * i] = v.x;
-        w[2 * i] = __int_as_float(v.y);
-        c[2 * i + 1] = v.z;
-        w[2 * i + 1] = __int_as_float(v.w);
-    }
-    __builtin_amdgcn_wave_barrier();
-}
-
-
-// Gathers of one tile's slab.  Tiled layout: a raw buffer over the slab (rows x 128 B), 32-bit offsets, so an offset
-// past the slab (NO_ROW, or any bad index) reads zeros.  Plain layout ([rows][B], the HopCuda boundary): global
-// loads with the run-time row stride; rows past the end are masked to zero.
-template <bool TILED>
-struct Slab {
-    __amdgpu_buffer_rsrc_t rsrc;
-    const float* base;
-    int stride, rows;
-    __device__ __forceinline__ Slab(const float* tile_base, int row_stride, int n_rows, int sub)
-        : base(tile_base + sub * 4), stride(row_stride), rows(n_rows) {
-        if (TILED)
-            rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)tile_base, (short)0, n_rows * (TW * 4), 0x00020000);
-    }
-    __device__ __forceinline__ float4 get(int row, int sub) const {
-        if (TILED) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (unsigned)row * (TW * 4u) + (unsigned)sub * 16u, 0, 0);
-            return make_float4(__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]), __int_as_float(v[3]));
-        }
-        const bool ok = (unsigned)row < (unsigned)rows;
-        const float4 v = *reinterpret_cast<const float4*>(base + (size_t)(ok ? row : 0) * stride);
-        return ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-};
 
 template <bool TILED>
 __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw, const float* __restrict__ src, Lay ls,
@@ -230,20 +135,6 @@ __device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int t
     in.gn = r.x;
     in.sp = r.y;
     return in;
-}
-
-// Reduce-scatter over the 8 lanes of a group: lane s ends with the sum over the group's lanes of d[s].  Three
-// butterfly steps, each pairing lanes that hold the same set of slots and keeping the half named by a lane bit:
-// lanes i and 7-i (row_half_mirror) split the slots by bit 2, then i and i^2, then i and i^1 (quad perms).
-__device__ __forceinline__ float rs8(const float (&d)[8], int sub) {
-    const bool b2 = sub & 4, b1 = sub & 2, b0 = sub & 1;
-    float a[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) a[t] = (b2 ? d[4 + t] : d[t]) + dppf<0x141>(b2 ? d[t] : d[4 + t]);
-    float b[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) b[u] = (b1 ? a[2 + u] : a[u]) + dppf<0x4E>(b1 ? a[u] : a[2 + u]);
-    return (b0 ? b[1] : b[0]) + dppf<0xB1>(b0 ? b[0] : b[1]);
 }
 
 // gh: the gradient of this layer's output h for (row j, tile); every lane of the 8-lane group calls this

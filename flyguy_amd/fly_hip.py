@@ -4,6 +4,10 @@ z[target, b] = sum over connections (source -> target) of w * h[source, b]; stat
 batch contiguous and a multiple of 32.  crow / col: the connections by target (CSR, int64 / int32); tcrow / tcol /
 tperm: the same by source.  The backward is one pass over the transposed form that gives both the state gradient
 and the per-connection gradient (fh_spmm_bwd).
+
+half=True reads the states as IEEE binary16 (rounded to nearest even) and the backward reads the output gradient as
+binary16 after dividing it by its largest magnitude (fly_cuda.py:93, 100-114); all sums stay float32.  The
+conversions and the scale are computed by the library (fh_to_half, fh_absmax).
 """
 from __future__ import annotations
 
@@ -87,28 +91,40 @@ def _check_index(idx: torch.Tensor, bound: int, what: str) -> None:
     _remember(_checked, key, idx)
 
 
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
 class HopHip(torch.autograd.Function):
     @staticmethod
     def forward(ctx, w, h, crow, col, tcrow, tcol, tperm, half: bool):
-        if half:
-            raise NotImplementedError("16-bit hop states are not available in this library yet")
         n_rows, B = crow.numel() - 1, h.shape[1]
         if B % 32 or not h.is_contiguous() or h.dtype != torch.float32:
             raise ValueError("HopHip: h must be contiguous float32 [n_src, B] with B a multiple of 32")
         w = w.contiguous().float()
         col = col.contiguous()
-        E = col.numel()
+        E, n_src = col.numel(), h.shape[0]
         if w.numel() != E or col.dtype != torch.int32 or crow.dtype != torch.int64:
             raise ValueError("HopHip: w / col / crow do not match (float32 w[E], int32 col[E], int64 crow)")
-        _check_index(col, h.shape[0], "source index")
+        _check_index(col, n_src, "source index")
         d = _plan(crow, col, None, E)
         out = torch.empty(n_rows, B, device=h.device)
         cw = torch.empty(max(d["npos"], 1), 2, dtype=torch.int32, device=h.device)
-        scratch = torch.empty(max(d["nslot"] * B, 1), device=h.device)
-        call("fh_spmm", *_args(d), w.data_ptr(), h.data_ptr(), out.data_ptr(), n_rows, h.shape[0], B, cw.data_ptr(),
-             scratch.data_ptr(), torch.cuda.current_stream(h.device).cuda_stream)
+        if half:
+            t64 = (B + 63) // 64
+            hs = torch.empty(max(t64 * n_src * 64, 1), dtype=torch.float16, device=h.device)
+            call("fh_to_half", h.data_ptr(), n_src, B, None, hs.data_ptr(), _stream(h))
+            scratch = torch.empty(max(d["nslot"] * t64 * 64, 1), device=h.device)
+            call("fh_spmm_h", *_args(d), w.data_ptr(), hs.data_ptr(), out.data_ptr(), n_rows, n_src, B, cw.data_ptr(),
+                 scratch.data_ptr(), _stream(h))
+            ctx.hs = hs
+        else:
+            scratch = torch.empty(max(d["nslot"] * B, 1), device=h.device)
+            call("fh_spmm", *_args(d), w.data_ptr(), h.data_ptr(), out.data_ptr(), n_rows, n_src, B, cw.data_ptr(),
+                 scratch.data_ptr(), _stream(h))
+            ctx.hs = None
         ctx.save_for_backward(w, h, tcrow, tcol, tperm)
-        ctx.n_rows = n_rows
+        ctx.n_rows, ctx.half = n_rows, half
         return out
 
     @staticmethod
@@ -126,10 +142,21 @@ class HopHip(torch.autograd.Function):
         gh = torch.empty(n_src, B, device=h.device)
         gw = torch.zeros_like(w) if ctx.needs_input_grad[0] else None
         cw = torch.empty(max(d["npos"], 1), 2, dtype=torch.int32, device=h.device)
-        gwpart = torch.empty(max(d["npos"] * (B // 32), 1), device=h.device) if gw is not None else None
-        scratch = torch.empty(max(d["nslot"] * B, 1), device=h.device)
-        call("fh_spmm_bwd", *_args(d), w.data_ptr(), gz.data_ptr(), h.data_ptr(), gh.data_ptr(),
-             gw.data_ptr() if gw is not None else None, ctx.n_rows, n_src, B, cw.data_ptr(),
-             gwpart.data_ptr() if gwpart is not None else None, scratch.data_ptr(),
-             torch.cuda.current_stream(h.device).cuda_stream)
+        if ctx.half:
+            t64 = (B + 63) // 64
+            scale = torch.empty(1, device=h.device)
+            call("fh_absmax", gz.data_ptr(), gz.numel(), scale.data_ptr(), _stream(gz))
+            gzs = torch.empty(max(t64 * ctx.n_rows * 64, 1), dtype=torch.float16, device=h.device)
+            call("fh_to_half", gz.data_ptr(), ctx.n_rows, B, scale.data_ptr(), gzs.data_ptr(), _stream(gz))
+            gwpart = torch.empty(max(d["npos"] * t64, 1), device=h.device) if gw is not None else None
+            scratch = torch.empty(max(d["nslot"] * t64 * 64, 1), device=h.device)
+            call("fh_spmm_bwd_h", *_args(d), w.data_ptr(), gzs.data_ptr(), ctx.hs.data_ptr(), scale.data_ptr(),
+                 gh.data_ptr(), gw.data_ptr() if gw is not None else None, ctx.n_rows, n_src, B, cw.data_ptr(),
+                 gwpart.data_ptr() if gwpart is not None else None, scratch.data_ptr(), _stream(gz))
+        else:
+            gwpart = torch.empty(max(d["npos"] * (B // 32), 1), device=h.device) if gw is not None else None
+            scratch = torch.empty(max(d["nslot"] * B, 1), device=h.device)
+            call("fh_spmm_bwd", *_args(d), w.data_ptr(), gz.data_ptr(), h.data_ptr(), gh.data_ptr(),
+                 gw.data_ptr() if gw is not None else None, ctx.n_rows, n_src, B, cw.data_ptr(),
+                 gwpart.data_ptr() if gwpart is not None else None, scratch.data_ptr(), _stream(gz))
         return gw, (gh if ctx.needs_input_grad[1] else None), None, None, None, None, None, None

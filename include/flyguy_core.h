@@ -137,6 +137,33 @@ void fh_spmm_bwd(const int* wave, int nwave, const int* seg, int nseg, const int
                  float* gh, float* gw, int n_rows, int n_src, int B, void* cw, float* gwpart, float* scratch,
                  void* stream);
 
+/* ---- 16-bit states (the reference's half path, fly_cuda.py:34-56, 93-115): products read states and gradients as
+ * IEEE binary16 and accumulate in float32.  A 16-bit state tensor is tiled: [ceil(B/64)][rows][64] halves, samples
+ * past B zero. ---- */
+
+/* out (tiled binary16) = x / (*scale, when scale is not null) rounded to nearest even; x is row-major float32
+ * [rows][B], B % 32 == 0.  The reference's h.half() and (gz / scale).half(), fly_cuda.py:93, 103-104. */
+void fh_to_half(const float* x, int rows, int B, const float* scale, void* out, void* stream);
+
+/* *out = max(max |x[i]|, 1e-30) over n floats (device scalar): the reference's gz.abs().max().clamp_min(1e-30),
+ * fly_cuda.py:103 (a NaN in x is not propagated). */
+void fh_absmax(const float* x, long long n, float* out, void* stream);
+
+/* fh_spmm with the states hs in binary16 (tiled, from fh_to_half): out[n_rows][B] float32.  scratch: nslot *
+ * ceil(B/64) * 64 floats.  Replaces spmm_h, fly_cuda.py:34-39. */
+void fh_spmm_h(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+               const int* pcol, const int* pidx, long long npos, const float* w, const void* hs, float* out, int n_rows,
+               int n_src, int B, void* cw, float* scratch, void* stream);
+
+/* fh_spmm_bwd with binary16 gradients gzs = half(gz / scale) and states hs (both tiled): gh[n_src][B] = scale *
+ * A^T gzs, and gw[e] += scale * sum_b gzs[row_e][b] hs[col_e][b].  scale: device scalar (fh_absmax).  gwpart:
+ * npos * ceil(B/64) floats; scratch: nslot * ceil(B/64) * 64 floats.  Replaces sddmm_h + spmm_h over the CSC and
+ * the scaling of fly_cuda.py:100-114. */
+void fh_spmm_bwd_h(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                   const int* pcol, const int* pidx, long long npos, const float* w, const void* gzs, const void* hs,
+                   const float* scale, float* gh, float* gw, int n_rows, int n_src, int B, void* cw, float* gwpart,
+                   float* scratch, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -203,3 +203,61 @@ def test_hop_hip_matches_torch(gpu_lib):
     ref.kernel = "torch"
     ref_out = ref.double()(x.double())
     assert rel(got.detach().cpu().numpy(), ref_out.detach().numpy()) <= 1e-5
+
+
+def _half_case(a, r, c, w, n_src, n_rows, B, crow, col, tcrow, tcol, tperm, seed):
+    """One HopHip(half=True) product and its backward against the reference's half arithmetic in float64:
+    states rounded to binary16, the output gradient divided by its largest magnitude and rounded to binary16,
+    products rescaled (fly_cuda.py:93, 100-114)."""
+    from flyguy_amd.fly_hip import HopHip
+    g = torch.Generator().manual_seed(seed)
+    h32 = torch.rand(n_src, B, generator=g)
+    gz32 = torch.randn(n_rows, B, generator=g)
+    hs = h32.half().double()
+    scale = gz32.abs().max().clamp_min(1e-30)
+    gzs = (gz32 / scale).half().double()
+    want = (a @ hs).numpy()
+    want_gh = ((a.t() @ gzs) * float(scale)).numpy()
+    want_gw = ((gzs[r] * hs[c]).sum(1) * float(scale)).numpy()
+    wd = w.float().cuda().requires_grad_(True)
+    hd = h32.cuda().requires_grad_(True)
+    out = HopHip.apply(wd, hd, crow.cuda(), col.cuda(), tcrow.cuda(), tcol.cuda(), tperm.cuda(), True)
+    out.backward(gz32.cuda())
+    for name, got, ref in (("out", out, want), ("gh", hd.grad, want_gh), ("gw", wd.grad, want_gw)):
+        r_ = rel(got.detach().cpu().numpy(), ref)
+        say(f"      half B {B} {name} rel {r_:.2e}")
+        assert r_ <= 1e-5, (name, B, r_)
+
+
+def test_hop_hip_half_matches_reference_rounding(gpu_lib):
+    """HopHip(half=True), the fp16 variant of HopCuda: relative to the largest entry <= 1e-5 (float32 sums of the
+    same binary16 operands), on toy hops and on a hop of the scaled benchmark shape whose heavy rows are split,
+    at B = 64 and at B = 96 (a 64-sample tile that is half past the batch)."""
+    say("hop hip half")
+    from flyguy_amd.synth import scaled_3hop
+    torch.manual_seed(0)
+    f = lively(FlyActor(toy("b"), 517, 90, hops=3, fan=16))
+    for B in (64, 96):
+        for k in (1, 2, 3):
+            n_src, crow, col = f.sizes[k - 1], getattr(f, f"crow{k}"), getattr(f, f"ci{k}")
+            w = f.w.detach()[getattr(f, f"e{k}")].double()
+            a = torch.sparse_csr_tensor(crow, col.long(), w, size=(len(crow) - 1, n_src))
+            _half_case(a, getattr(f, f"r{k}"), getattr(f, f"c{k}"), w, n_src, len(crow) - 1, B, crow, col,
+                       getattr(f, f"tcrow{k}"), getattr(f, f"tci{k}"), getattr(f, f"tperm{k}"), 10 * B + k)
+    s, params = scaled_3hop(16)
+    h = s["hop"][1]
+    crow = torch.as_tensor(np.asarray(h["crow"], np.int64))
+    col = torch.as_tensor(np.asarray(h["col"], np.int32))
+    E = len(col)
+    widx, twidx = np.asarray(h["widx"]), np.asarray(h["twidx"])
+    inv = np.full(int(widx.max()) + 1, -1, np.int64)
+    inv[widx] = np.arange(E)                                  # weight index -> CSR edge
+    tperm = torch.as_tensor(inv[twidx])                       # CSC position -> CSR edge
+    assert (tperm >= 0).all()
+    rows_t = np.repeat(np.arange(len(crow) - 1), np.diff(np.asarray(h["crow"])))
+    w = torch.as_tensor(params[0][widx].astype(np.float64))
+    n_src, n_rows = s["sizes"][1], s["sizes"][2]
+    a = torch.sparse_csr_tensor(crow, col.long(), w, size=(n_rows, n_src))
+    _half_case(a, torch.as_tensor(rows_t), col.long(), w, n_src, n_rows, 96, crow, col,
+               torch.as_tensor(np.asarray(h["tcrow"], np.int64)), torch.as_tensor(np.asarray(h["tcol"], np.int32)),
+               tperm, 7)
