@@ -12,6 +12,14 @@ __device__ __forceinline__ float4* at4w(float* base, Lay L, int tile, int row, i
     return reinterpret_cast<float4*>(base + (size_t)tile * L.tile + (size_t)row * L.row) + sub;
 }
 __device__ __forceinline__ float4 splat(float v) { return make_float4(v, v, v, v); }
+// The same element of a tiled state ([T][rows][32]) as a wave-uniform tile base plus a 32-bit element offset (cheaper
+// addressing than at4's 64-bit products; a tiled slab is far below 2^32 elements)
+__device__ __forceinline__ const float4* at4u(const float* base, Lay L, int tile, int row, int sub) {
+    return reinterpret_cast<const float4*>(base + (size_t)tile * L.tile + (unsigned)(row * L.row + sub * 4));
+}
+__device__ __forceinline__ float4* at4uw(float* base, Lay L, int tile, int row, int sub) {
+    return reinterpret_cast<float4*>(base + (size_t)tile * L.tile + (unsigned)(row * L.row + sub * 4));
+}
 
 template <int C>
 __device__ __forceinline__ float dppf(float v) {

@@ -30,7 +30,7 @@ struct FwdIn {
 };
 __device__ __forceinline__ FwdIn fwd_inputs(const FwdEpi& e, int t, int d, int tile, int sub) {
     FwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f};
-    if (e.drive && d >= 0) in.dv = *at4(e.drive, e.ldrive, tile, d, sub);
+    if (e.drive && d >= 0) in.dv = *at4u(e.drive, e.ldrive, tile, d, sub);
     if (e.info) {
         const float4 r = e.info[t];
         in.g = r.x;
@@ -52,7 +52,7 @@ __device__ __forceinline__ void fwd_finish(const FwdEpi& e, int t, int tile, int
         const float g = in.g, sp = in.sp;
         const float4 hv = make_float4(fmaxf(fmaf(g, acc.x, -sp), 0.f), fmaxf(fmaf(g, acc.y, -sp), 0.f),
                                       fmaxf(fmaf(g, acc.z, -sp), 0.f), fmaxf(fmaf(g, acc.w, -sp), 0.f));
-        st_stream(at4w(e.h, e.lh, tile, t, sub), hv);
+        st_stream(at4uw(e.h, e.lh, tile, t, sub), hv);
     }
 }
 
@@ -71,10 +71,13 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     const Slab<TILED> slab(src + (size_t)tile * ls.tile, ls.row, src_rows, sub);
-    float4 acc = (live && sg.y < 0 && epi.bias) ? splat(epi.bias[sg.x]) : splat(0.f);
+    const bool whole = live && sg.y < 0;
+    float4 acc = splat(0.f);
     FwdIn in{};
-    if (live && sg.y < 0) in = fwd_inputs(epi, sg.x, sg.z, tile, sub);
-    // steps of the wave's longest segment; a step gathers only the slots some group still needs
+    // steps of the wave's longest segment; a step gathers only the slots some group still needs.  The row's own
+    // inputs (bias, re-drive row, gain, threshold) are requested right after the first step's gathers: loads
+    // complete in order, so requested earlier they would hold up the first gathers.  The bias still starts the sum
+    // (flyguy_train.cu:75).
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
         float wt[8];
@@ -82,13 +85,20 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
         float4 v[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(c[s], sub) : splat(0.f);
-        // the next step's pairs are requested after this step's gathers: loads complete in order, so the gathers
-        // do not wait for them
+        // the next step's pairs are requested after this step's gathers, so the gathers do not wait for them
         __builtin_amdgcn_sched_barrier(0);
         if (left > 8) nxt = q[64 * (j + 1)];
+        if (j == 0 && whole) {
+            in = fwd_inputs(epi, sg.x, sg.z, tile, sub);
+            if (epi.bias) acc = splat(epi.bias[sg.x]);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 8; ++s) fma4(wt[s], v[s], acc);
+    }
+    if (whole && !(wok && wv.y > 0)) {          // a wave without edges
+        in = fwd_inputs(epi, sg.x, sg.z, tile, sub);
+        if (epi.bias) acc = splat(epi.bias[sg.x]);
     }
     if (!live) return;
     if (sg.y >= 0) {
@@ -128,9 +138,9 @@ __device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int t
     BwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f, -1};
     if constexpr (MODE == 0) return in;
     in.d = MODE == 2 ? j : d;                              // the sensory layer's own drive gradient is complete now:
-    if (in.d >= 0) in.gd = *at4(e.gdrive, e.lgd, tile, in.d, sub);     //   every hop above has added its share
-    in.h = *at4(e.h, e.lh, tile, j, sub);
-    if constexpr (MODE == 2) in.z = *at4(e.z, e.lz, tile, j, sub);
+    if (in.d >= 0) in.gd = *at4u(e.gdrive, e.lgd, tile, in.d, sub);    //   every hop above has added its share
+    in.h = *at4u(e.h, e.lh, tile, j, sub);
+    if constexpr (MODE == 2) in.z = *at4u(e.z, e.lz, tile, j, sub);
     const float4 r = e.info[j];
     in.gn = r.x;
     in.sp = r.y;
@@ -149,25 +159,25 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
                                  hv.w > 0.f ? gh.w : 0.f);
     const float gn = in.gn;
     const float4 gzv = make_float4(g.x * gn, g.y * gn, g.z * gn, g.w * gn);
-    float4 zv = in.z;
-    if constexpr (MODE == 1) {                  // z where it matters (h > 0): h = gain * z - softplus(theta)
-        zv.x = hv.x > 0.f ? (hv.x + in.sp) / gn : 0.f;
-        zv.y = hv.y > 0.f ? (hv.y + in.sp) / gn : 0.f;
-        zv.z = hv.z > 0.f ? (hv.z + in.sp) / gn : 0.f;
-        zv.w = hv.w > 0.f ? (hv.w + in.sp) / gn : 0.f;
-    }
-    const float pg = gsum8(dot4(g, zv));
     const float ps = gsum8(hsum4(g));
+    float pg;
+    if constexpr (MODE == 1) {
+        // sum over the tile of g * z without z: where h > 0, z = (h + softplus(theta)) / gain, and elsewhere g = 0,
+        // so the sum is (sum g h + softplus(theta) sum g) / gain
+        pg = (gsum8(dot4(g, hv)) + in.sp * ps) / gn;
+    } else {
+        pg = gsum8(dot4(g, in.z));              // the sensory layer keeps its pre-activation (the drive)
+    }
     if (sub == 0) {
         e.ggain_part[(size_t)tile * e.gp_ld + j] = pg;
         e.gsum_part[(size_t)tile * e.gp_ld + j] = ps;
     }
     if constexpr (MODE == 1) {
-        *at4w(e.gz_out, e.lgz, tile, j, sub) = gzv;
+        *at4uw(e.gz_out, e.lgz, tile, j, sub) = gzv;
         if (in.d >= 0) {
             float4 v = in.gd;
             add4(gzv, v);
-            *at4w(e.gdrive, e.lgd, tile, in.d, sub) = v;
+            *at4uw(e.gdrive, e.lgd, tile, in.d, sub) = v;
         }
         return;
     }
@@ -189,7 +199,7 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
 #pragma unroll
         for (int s2 = 0; s2 < 8; ++s2) {
             const bool ok = (unsigned)c[s2] < (unsigned)e.x_rows;
-            const float4 xv = *at4(e.x, e.lx, tile, ok ? c[s2] : 0, sub);
+            const float4 xv = *at4u(e.x, e.lx, tile, ok ? c[s2] : 0, sub);
             dd[s2] = ok ? dot4(gd, xv) : 0.f;
         }
         const float pw = rs8(dd, sub);
@@ -212,13 +222,13 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
-    const float4 hj = live ? *at4(hs, lhs, tile, sg.x, sub) : splat(0.f);
+    float4 hj = splat(0.f);
     const Slab<TILED> slab(gz + (size_t)tile * lg.tile, lg.row, gz_rows, sub);
     // the partial of (position, tile) of this lane's slot: one contiguous 256-byte block per wave and step
     float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
     float4 acc = splat(0.f);
     BwdIn in{};
-    if (live && sg.y < 0) in = bwd_inputs<MODE>(epi, sg.x, sg.z, tile, sub);
+    const bool whole = live && sg.y < 0;
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
         float wt[8];
@@ -228,6 +238,10 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
         for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(c[s], sub) : splat(0.f);
         __builtin_amdgcn_sched_barrier(0);
         if (left > 8) nxt = q[64 * (j + 1)];
+        if (j == 0) {                           // the row's own inputs, after the first gathers (see k_fwd)
+            if (live) hj = MODE == 0 ? *at4(hs, lhs, tile, sg.x, sub) : *at4u(hs, lhs, tile, sg.x, sub);
+            if (whole) in = bwd_inputs<MODE>(epi, sg.x, sg.z, tile, sub);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 8; ++s) fma4(wt[s], v[s], acc);
@@ -238,6 +252,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
             gwp[64 * j] = rs8(d, sub);
         }
     }
+    if (whole && !(wok && wv.y > 0)) in = bwd_inputs<MODE>(epi, sg.x, sg.z, tile, sub);
     if (!live) return;
     if (sg.y >= 0) {
         *at4w(part, lp, tile, sg.y, sub) = acc;
