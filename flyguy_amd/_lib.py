@@ -41,6 +41,18 @@ _SIGS = {
     "fh_spmm_h": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp, vp, vp]),
     "fh_spmm_bwd_h": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp,
                              vp]),
+    # include/flyguy_train.h
+    "ft_main": (ci, [ci, ctypes.POINTER(ctypes.c_char_p)]),
+    "ft_draw": (ci, [ctypes.c_ulonglong, ctypes.POINTER(cll), ci, ci, ci, vp]),
+    "ft_lr": (None, [cll, cf, cf, cf, cf, ctypes.c_double, ctypes.POINTER(cf)]),
+    "ft_chunk_samples": (cll, [ctypes.c_char_p, ci, ci]),
+    "ft_scan_order": (ci, [ctypes.c_char_p, ci, ctypes.c_char_p, ci]),
+    "fd_gather16": (None, [vp, vp, vp, ci, vp, ci, ci, ci, vp, vp, vp]),
+    "fd_unpack16": (None, [vp, ci, ci, ci, vp, vp, vp]),
+    "fc_layers": (ci, [vp, ctypes.POINTER(ci), ci]),
+    "fc_survey": (ci, [vp, vp, vp, ci, ci, cf, ci]),
+    "fc_survey_read": (cll, [vp, vp, vp, ctypes.POINTER(ctypes.c_double)]),
+    "fc_revive": (ci, [vp, vp, vp, ci, ci, cf, ctypes.c_ulonglong, cll, ctypes.c_char_p, ci]),
 }
 
 

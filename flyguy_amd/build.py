@@ -2,8 +2,9 @@
 
     python -m flyguy_amd.build
 
-The library is plain HIP C++ behind a C ABI (include/flyguy_core.h); it links only the HIP runtime, so ctypes
-loads it next to PyTorch in the same process and GPU context.
+The library is plain HIP C++ behind a C ABI (include/flyguy_core.h, include/flyguy_train.h); it links only the HIP
+runtime, so ctypes loads it next to PyTorch in the same process and GPU context.  The teaching trainer's executable
+(flyguy_amd/flyguy_train) is a one-line main over the library's ft_main, found next to it at run time.
 """
 from __future__ import annotations
 
@@ -16,8 +17,10 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libflyguy_core.so"
-SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "hop_api.hip", "half.hip")]
-HEADERS = [PKG / "csrc" / "common.h", PKG / "csrc" / "kernels.h", PKG / "csrc" / "device.h", ROOT / "include" / "flyguy_core.h"]
+EXE = PKG / "flyguy_train"
+SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "hop_api.hip", "half.hip", "train.hip")]
+HEADERS = [PKG / "csrc" / n for n in ("common.h", "kernels.h", "device.h", "core.h")] + \
+    [ROOT / "include" / "flyguy_core.h", ROOT / "include" / "flyguy_train.h"]
 ARCH = os.environ.get("FLYGUY_OFFLOAD_ARCH", "gfx950")
 
 
@@ -56,6 +59,13 @@ def build(verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    tmp = EXE.with_suffix(".tmp")
+    cmd = ["g++", "-O2", "-std=c++17", str(PKG / "csrc" / "flyguy_train_main.cpp"), "-o", str(tmp), f"-L{PKG}",
+           "-lflyguy_core", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath-link,/opt/rocm/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, EXE)
     return LIB
 
 

@@ -1,0 +1,131 @@
+// Internal interface of the library's core (not part of the C-ABI): the device state of one network handle and
+// the passes over it, shared by the entry points of core.hip and the teaching trainer of train.hip.
+#pragma once
+#include <algorithm>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "kernels.h"
+
+namespace fg {
+
+struct DevPlan {
+    int2* wave = nullptr;
+    int4* seg = nullptr;
+    int4* split = nullptr;
+    int *pcol = nullptr, *pidx = nullptr;      // per position: source row and weight index (-1: no edge)
+    int nwave = 0, nseg = 0, nsplit = 0, nslot = 0, rows = 0;
+    long long npos = 0;
+    Plan view() const { return Plan{wave, nwave, seg, nseg, split, nsplit, rows, nslot, npos}; }
+};
+
+struct HopD {
+    int rows = 0, src = 0, E = 0;
+    int *nid = nullptr, *drow = nullptr;
+    bool has_drive = false;
+    int2 *cw = nullptr, *tcw = nullptr;
+    DevPlan fp, bp;
+    float *h = nullptr, *ggp = nullptr, *gsp = nullptr;
+    float4* info = nullptr;          // per row {gain, softplus(theta), re-drive row}, refreshed at every pass
+    float* zk = nullptr;             // the pre-activation, kept only by survey passes (allocated on first use)
+    std::vector<int> h_nid, h_crow, h_col, h_widx;   // host copies of the index arrays (the revive surgery)
+};
+
+// Stages timed with HIP events on the library's stream when profiling is on (fc_profile): where the time of a
+// forward / backward / step goes, kernel by kernel.
+enum Stage {
+    ST_OBS = 0, ST_PACK = 1, ST_PLUG = 2, ST_HOP = 3,            // ST_HOP + k: forward of hop k+1 (k < 8)
+    ST_LOGITS = 11, ST_LOSS = 12, ST_RBWD = 13, ST_BHOP = 14,    // ST_BHOP + k: backward of hop k+1 (k < 8)
+    ST_REDUCE = 22, ST_ADAM = 23, ST_ZERO = 24, ST_COUNT = 25
+};
+
+struct Prof {
+    bool on = false;
+    std::vector<std::pair<hipEvent_t, int>> rec;   // (event, stage*2 + 0 start / 1 end) in recording order
+    std::vector<hipEvent_t> pool;
+    double ms[ST_COUNT] = {0};
+    long long n[ST_COUNT] = {0};
+    hipEvent_t get() {
+        if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+};
+
+struct Core {
+    int obs_dim = 0, n_act = 0, hops = 0, n_neurons = 0, n_w = 0, n_s = 0, fan = 0, n_dn = 0, E_in = 0;
+    std::vector<int> sizes, E;
+    int maxB = 0, Tm = 0;
+    int *in_crow = nullptr, *in_col = nullptr, *n0 = nullptr, *dn = nullptr, *dn_inv = nullptr;
+    int2* in_cw = nullptr;
+    float4* info0 = nullptr;
+    DevPlan pp;
+    std::vector<HopD> hop;
+    float* pm = nullptr;
+    long long PT = 0, off[8] = {0}, psize[7] = {0};
+    float *x = nullptr, *drive = nullptr, *h0 = nullptr, *gdrive = nullptr, *gz[2] = {nullptr, nullptr};
+    float *lg = nullptr, *dl = nullptr, *part = nullptr, *gwpart = nullptr, *ggp0 = nullptr, *gsp0 = nullptr;
+    float *ginb = nullptr, *ginw = nullptr, *gow_p = nullptr, *gob_p = nullptr, *stats_part = nullptr;
+    float *stats = nullptr, *red = nullptr, *nrm = nullptr;
+    std::vector<int> h_n0, h_dn;     // host copies: the sensory rows' neurons, the read-out rows
+    bool keep_z = false;             // forward passes store every hop layer's pre-activation (surveys)
+    int* scnt = nullptr;             // survey sums per row of every layer (sensory rows, then each hop's rows):
+    float* ssq = nullptr;            //   samples for which the row fires, sum of its squared pre-activation
+    float* sstats = nullptr;         //   and the loss sums {KL, agreements}
+    double s_samples = 0;
+    long long rows_total = 0;
+    long long adam_t = 0;
+    int B = 0;
+    hipStream_t st = nullptr;
+    std::vector<void*> allocs;
+    Prof prof;
+    float* arr(int set, int i) const { return pm + (long long)set * PT + off[i]; }
+};
+
+// RAII: events before and after the launches of one stage (no-op unless profiling)
+struct Timed {
+    Core& c;
+    int stage;
+    Timed(Core& c_, int s) : c(c_), stage(s) { mark(0); }
+    ~Timed() { mark(1); }
+    void mark(int end) {
+        if (!c.prof.on) return;
+        hipEvent_t e = c.prof.get();
+        if (e && hipEventRecord(e, c.st) == hipSuccess) c.prof.rec.push_back({e, stage * 2 + end});
+    }
+};
+
+enum { SET_P = 0, SET_EMA = 1, SET_M = 2, SET_V = 3, SET_G = 4 };
+
+template <class T>
+T* dalloc(Core& c, size_t n) {
+    void* p = nullptr;
+    const size_t bytes = std::max<size_t>(n, 1) * sizeof(T);
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        set_error("out of device memory (" + std::to_string(bytes) + " bytes)");
+        return nullptr;
+    }
+    c.allocs.push_back(p);
+    if (hipMemset(p, 0, bytes) != hipSuccess) {
+        set_error("hipMemset failed");
+        return nullptr;
+    }
+    return (T*)p;
+}
+
+Core* build(const unsigned char* bytes, long long len, int max_batch);
+void release(Core* c);
+bool check_batch(const Core* c, int B);
+bool prof_collect(Core& c);
+// forward of a batch through the weight set `set` (SET_P or SET_EMA); obs [B][obs_dim] row-major on the device;
+// logits [B][n_act]
+bool forward(Core& c, const float* obs, int B, float* logits, int set);
+// backward of the last forward (through SET_P) from dlogits [B][n_act]: gradients ADDED to the SET_G arrays
+bool backward(Core& c, const float* dlogits, int B);
+float grad_norm(Core& c);
+// Adam + running average over all seven arrays; lr for W, lr_neuron for gain / theta, lr_plug for the rest
+float step(Core& c, float lr, float lr_neuron, float lr_plug, float max_norm, float ema);
+
+}  // namespace fg

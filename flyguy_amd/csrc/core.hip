@@ -19,7 +19,7 @@
 #include <vector>
 
 #include "../../include/flyguy_core.h"
-#include "kernels.h"
+#include "core.h"
 
 namespace fg {
 
@@ -85,122 +85,6 @@ static bool make_plan(const int* rowptr, int rows, int seg_max, const int* drow,
     return true;
 }
 
-struct DevPlan {
-    int2* wave = nullptr;
-    int4* seg = nullptr;
-    int4* split = nullptr;
-    int *pcol = nullptr, *pidx = nullptr;      // per position: source row and weight index (-1: no edge)
-    int nwave = 0, nseg = 0, nsplit = 0, nslot = 0, rows = 0;
-    long long npos = 0;
-    Plan view() const { return Plan{wave, nwave, seg, nseg, split, nsplit, rows, nslot, npos}; }
-};
-
-struct HopD {
-    int rows = 0, src = 0, E = 0;
-    int *nid = nullptr, *drow = nullptr;
-    bool has_drive = false;
-    int2 *cw = nullptr, *tcw = nullptr;
-    DevPlan fp, bp;
-    float *h = nullptr, *ggp = nullptr, *gsp = nullptr;
-    float4* info = nullptr;          // per row {gain, softplus(theta), re-drive row}, refreshed at every pass
-};
-
-// Stages timed with HIP events on the library's stream when profiling is on (fc_profile): where the time of a
-// forward / backward / step goes, kernel by kernel.
-enum Stage {
-    ST_OBS = 0, ST_PACK = 1, ST_PLUG = 2, ST_HOP = 3,            // ST_HOP + k: forward of hop k+1 (k < 8)
-    ST_LOGITS = 11, ST_LOSS = 12, ST_RBWD = 13, ST_BHOP = 14,    // ST_BHOP + k: backward of hop k+1 (k < 8)
-    ST_REDUCE = 22, ST_ADAM = 23, ST_ZERO = 24, ST_COUNT = 25
-};
-
-struct Prof {
-    bool on = false;
-    std::vector<std::pair<hipEvent_t, int>> rec;   // (event, stage*2 + 0 start / 1 end) in recording order
-    std::vector<hipEvent_t> pool;
-    double ms[ST_COUNT] = {0};
-    long long n[ST_COUNT] = {0};
-    hipEvent_t get() {
-        if (!pool.empty()) { hipEvent_t e = pool.back(); pool.pop_back(); return e; }
-        hipEvent_t e = nullptr;
-        if (hipEventCreate(&e) != hipSuccess) return nullptr;
-        return e;
-    }
-};
-
-struct Core {
-    int obs_dim = 0, n_act = 0, hops = 0, n_neurons = 0, n_w = 0, n_s = 0, fan = 0, n_dn = 0, E_in = 0;
-    std::vector<int> sizes, E;
-    int maxB = 0, Tm = 0;
-    int *in_crow = nullptr, *in_col = nullptr, *n0 = nullptr, *dn = nullptr, *dn_inv = nullptr;
-    int2* in_cw = nullptr;
-    float4* info0 = nullptr;
-    DevPlan pp;
-    std::vector<HopD> hop;
-    float* pm = nullptr;
-    long long PT = 0, off[8] = {0}, psize[7] = {0};
-    float *x = nullptr, *drive = nullptr, *h0 = nullptr, *gdrive = nullptr, *gz[2] = {nullptr, nullptr};
-    float *lg = nullptr, *dl = nullptr, *part = nullptr, *gwpart = nullptr, *ggp0 = nullptr, *gsp0 = nullptr;
-    float *ginb = nullptr, *ginw = nullptr, *gow_p = nullptr, *gob_p = nullptr, *stats_part = nullptr;
-    float *stats = nullptr, *red = nullptr, *nrm = nullptr;
-    long long adam_t = 0;
-    int B = 0;
-    hipStream_t st = nullptr;
-    std::vector<void*> allocs;
-    Prof prof;
-    float* arr(int set, int i) const { return pm + (long long)set * PT + off[i]; }
-};
-
-// RAII: events before and after the launches of one stage (no-op unless profiling)
-struct Timed {
-    Core& c;
-    int stage;
-    Timed(Core& c_, int s) : c(c_), stage(s) { mark(0); }
-    ~Timed() { mark(1); }
-    void mark(int end) {
-        if (!c.prof.on) return;
-        hipEvent_t e = c.prof.get();
-        if (e && hipEventRecord(e, c.st) == hipSuccess) c.prof.rec.push_back({e, stage * 2 + end});
-    }
-};
-
-// fold the recorded events into per-stage totals (waits for them)
-static bool prof_collect(Core& c) {
-    std::vector<hipEvent_t> open(ST_COUNT, nullptr);
-    bool ok = true;
-    for (auto& r : c.prof.rec) {
-        const int stg = r.second / 2;
-        if (r.second % 2 == 0) { open[stg] = r.first; continue; }
-        if (open[stg]) {
-            float ms = 0.f;
-            if (hipEventSynchronize(r.first) != hipSuccess || hipEventElapsedTime(&ms, open[stg], r.first) != hipSuccess) ok = false;
-            c.prof.ms[stg] += ms;
-            c.prof.n[stg] += 1;
-            c.prof.pool.push_back(open[stg]);
-            open[stg] = nullptr;
-        }
-        c.prof.pool.push_back(r.first);
-    }
-    c.prof.rec.clear();
-    return ok;
-}
-
-enum { SET_P = 0, SET_EMA = 1, SET_M = 2, SET_V = 3, SET_G = 4 };
-
-template <class T>
-static T* dalloc(Core& c, size_t n) {
-    void* p = nullptr;
-    const size_t bytes = std::max<size_t>(n, 1) * sizeof(T);
-    if (hipMalloc(&p, bytes) != hipSuccess) {
-        set_error("out of device memory (" + std::to_string(bytes) + " bytes)");
-        return nullptr;
-    }
-    c.allocs.push_back(p);
-    if (hipMemset(p, 0, bytes) != hipSuccess) {
-        set_error("hipMemset failed");
-        return nullptr;
-    }
-    return (T*)p;
-}
 template <class T>
 static T* upload(Core& c, const std::vector<T>& v) {
     T* p = dalloc<T>(c, v.size());
@@ -234,12 +118,33 @@ static bool upload_plan(Core& c, const HostPlan& h, int rows, const std::vector<
     return d.wave && d.seg && d.split && d.pcol && d.pidx;
 }
 
-static void release(Core* c) {
+void release(Core* c) {
     if (!c) return;
     for (auto& r : c->prof.rec) (void)hipEventDestroy(r.first);
     for (auto e : c->prof.pool) (void)hipEventDestroy(e);
     for (void* p : c->allocs) (void)hipFree(p);
     delete c;
+}
+
+// fold the recorded events into per-stage totals (waits for them)
+bool prof_collect(Core& c) {
+    std::vector<hipEvent_t> open(ST_COUNT, nullptr);
+    bool ok = true;
+    for (auto& r : c.prof.rec) {
+        const int stg = r.second / 2;
+        if (r.second % 2 == 0) { open[stg] = r.first; continue; }
+        if (open[stg]) {
+            float ms = 0.f;
+            if (hipEventSynchronize(r.first) != hipSuccess || hipEventElapsedTime(&ms, open[stg], r.first) != hipSuccess) ok = false;
+            c.prof.ms[stg] += ms;
+            c.prof.n[stg] += 1;
+            c.prof.pool.push_back(open[stg]);
+            open[stg] = nullptr;
+        }
+        c.prof.pool.push_back(r.first);
+    }
+    c.prof.rec.clear();
+    return ok;
 }
 
 // ------------------------------------------------------------------------------------------------ NET.bin
@@ -281,7 +186,7 @@ static bool distinct(const std::vector<int>& v, long long n, bool skip_negative)
     return true;
 }
 
-static Core* build(const unsigned char* bytes, long long len, int max_batch) {
+Core* build(const unsigned char* bytes, long long len, int max_batch) {
     clear_error();
     if (!bytes || len < 36 || std::memcmp(bytes, "FLY1", 4) != 0) {
         set_error("not a FLY1 network file");
@@ -371,6 +276,7 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
         d.cw = dalloc<int2>(*c, (size_t)d.fp.npos);
         d.tcw = dalloc<int2>(*c, (size_t)d.bp.npos);
         if (!d.nid || !d.drow || !d.cw || !d.tcw) return nullptr;
+        d.h_nid = std::move(h.nid); d.h_crow = std::move(h.crow); d.h_col = std::move(h.col); d.h_widx = std::move(h.widx);
         max_slot = std::max<long long>({max_slot, d.fp.nslot, d.bp.nslot});
         max_pos = std::max<long long>(max_pos, d.bp.npos);
         max_rows = std::max<long long>(max_rows, d.rows);
@@ -379,6 +285,10 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
     for (int j = 0; j < c->n_dn; ++j) dn_inv[dn[j]] = j;
     c->in_crow = upload(*c, in_crow); c->in_col = upload(*c, in_col); c->n0 = upload(*c, n0);
     c->dn = upload(*c, dn); c->dn_inv = upload(*c, dn_inv);
+    c->rows_total = c->n_s;
+    for (auto& d : c->hop) c->rows_total += d.rows;
+    c->h_n0 = std::move(n0);
+    c->h_dn = std::move(dn);
     if (!c->in_crow || !c->in_col || !c->n0 || !c->dn || !c->dn_inv || !c->in_cw) return nullptr;
 
     // parameters: 5 sets x 7 arrays
@@ -433,7 +343,7 @@ static Core* build(const unsigned char* bytes, long long len, int max_batch) {
     return c.release();
 }
 
-static bool check_batch(const Core* c, int B) {
+bool check_batch(const Core* c, int B) {
     if (!c) { set_error("null handle"); return false; }
     if (B <= 0 || B % TW != 0 || B > c->maxB) {
         set_error("batch " + std::to_string(B) + " must be a positive multiple of 32 and at most " + std::to_string(c->maxB));
@@ -451,7 +361,7 @@ static hipError_t rowinfo(Core& c, const float* gain, const float* theta) {
     return e;
 }
 
-static bool forward(Core& c, const float* obs, int B, float* logits, int set) {
+bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     const int T = B / TW;
     hipStream_t st = c.st;
     { Timed t(c, ST_OBS); FG_CHECK(launch_obs_in(obs, c.x, c.obs_dim, B, st), false); }
@@ -475,6 +385,7 @@ static bool forward(Core& c, const float* obs, int B, float* logits, int set) {
         e.info = d.info;
         if (d.has_drive) { e.drive = c.drive; e.ldrive = tiled(c.n_s); }
         e.h = d.h; e.lh = tiled(d.rows);
+        if (c.keep_z) { e.z = d.zk; e.lz = tiled(d.rows); }
         { Timed t(c, ST_HOP + std::min(hk, 7)); FG_CHECK(launch_fwd(d.fp.view(), d.cw, hp, tiled(d.src), d.src, e, c.part, tiled(d.fp.nslot), T, st), false); }
         hp = d.h;
         ++hk;
@@ -488,7 +399,7 @@ static bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     return true;
 }
 
-static bool backward(Core& c, const float* dlogits, int B) {
+bool backward(Core& c, const float* dlogits, int B) {
     const int T = B / TW, K = c.hops;
     hipStream_t st = c.st;
     const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
@@ -569,7 +480,7 @@ static bool backward(Core& c, const float* dlogits, int B) {
     return true;
 }
 
-static float grad_norm(Core& c) {
+float grad_norm(Core& c) {
     if (launch_sumsq(c.arr(SET_G, 0), c.PT, c.red, c.nrm, c.st) != hipSuccess) { set_error("grad norm launch"); return -1.f; }
     float ss = 0.f;
     FG_CHECK(hipMemcpyAsync(&ss, c.nrm, 4, hipMemcpyDeviceToHost, c.st), -1.f);
@@ -577,7 +488,7 @@ static float grad_norm(Core& c) {
     return sqrtf(ss);
 }
 
-static float step(Core& c, float lr, float lr_neuron, float lr_plug, float max_norm, float ema) {
+float step(Core& c, float lr, float lr_neuron, float lr_plug, float max_norm, float ema) {
     float g = 0.f;
     if (max_norm > 0.f) {
         g = grad_norm(c);

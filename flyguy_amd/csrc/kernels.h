@@ -108,8 +108,10 @@ int readout_chunks(int B);
 // idx == nullptr: i itself.  The indices a launch names are distinct, so no two threads add to one entry.
 hipError_t launch_reduce(const float* part, long long ld, long long n, int nt, const int* idx, const float* theta,
                          float* G, hipStream_t st);
+// KL(teacher || student) per sample (flyguy_train.cu:104-123): dl [B][n_act]; stats {KL sum, agreements} set, or
+// added to when accumulate
 hipError_t launch_loss(const float* lg, const float* tl, float* dl, float* stats_part, float* stats, int n_act, int B,
-                       float it, hipStream_t st);
+                       float it, hipStream_t st, bool accumulate = false);
 hipError_t launch_fill(float* p, float v, long long n, hipStream_t st);
 hipError_t launch_sumsq(const float* g, long long n, float* part, float* out, hipStream_t st);
 struct AdamSeg {

@@ -476,12 +476,12 @@ __global__ __launch_bounds__(LOSS_S) void k_loss(const float* __restrict__ lg, c
         stats_part[2 * blockIdx.x + 1] = agree;
     }
 }
-__global__ void k_sum_pairs(const float* __restrict__ part, int n, float* __restrict__ out) {
+__global__ void k_sum_pairs(const float* __restrict__ part, int n, float* __restrict__ out, int acc) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
     float a = 0.f, b = 0.f;
     for (int i = 0; i < n; ++i) { a += part[2 * i]; b += part[2 * i + 1]; }
-    out[0] = a;
-    out[1] = b;
+    out[0] = acc ? out[0] + a : a;
+    out[1] = acc ? out[1] + b : b;
 }
 
 __global__ void k_fill(float* __restrict__ p, float v, long long n) {
@@ -642,13 +642,13 @@ hipError_t launch_reduce(const float* part, long long ld, long long n, int nt, c
 }
 
 hipError_t launch_loss(const float* lg, const float* tl, float* dl, float* stats_part, float* stats, int n_act, int B,
-                       float it, hipStream_t st) {
+                       float it, hipStream_t st, bool accumulate) {
     if (n_act > 128) return hipErrorInvalidValue;       // the staged logits must fit the LDS
     const unsigned nb = blocks(B, LOSS_S);
     k_loss<<<nb, LOSS_S, (size_t)2 * LOSS_S * n_act * sizeof(float), st>>>(lg, tl, dl, stats_part, n_act, B, it);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    k_sum_pairs<<<1, 64, 0, st>>>(stats_part, (int)nb, stats);
+    k_sum_pairs<<<1, 64, 0, st>>>(stats_part, (int)nb, stats, accumulate ? 1 : 0);
     return hipGetLastError();
 }
 
