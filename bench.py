@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of the fly actor's batched inference and teaching step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096] [--no-cpu]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096]
+                    [--no-cpu] [--trainer-steps 60]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -13,6 +14,9 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
            stream over the timed region), against 8 TB/s;
   cpu_baseline: the reference's own CPU forward (fly_infer.cpp, compiled into oracle/_ref) on a bounded sample of
            the same network, one core; train: the oracle's float32 restatement on a small batch.
+  trainer: samples / s of the teaching trainer's own loop (flyguy_amd/flyguy_train, run as a child process on
+           synthetic binary16 FLYD chunks of the same network: draw, gather, step, as its log reports them) at
+           B = 4096 and at the reference trainer's default B = 512.
 One JSON line on stdout.  Only one GPU: --gpus N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -89,6 +93,46 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
     return fwd, train
 
 
+def trainer_leg(s, params, batches, steps: int) -> dict:
+    """samples/s of flyguy_train's loop on synthetic chunks (3 chunks of 32,768 samples), from its last log line."""
+    import re
+    import struct
+    import subprocess
+    import tempfile
+    from pathlib import Path
+
+    import numpy as np
+    from flyguy_amd.export import net_bytes, write_params
+
+    exe = Path(__file__).resolve().parent / "flyguy_amd" / "flyguy_train"
+    out = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        tmp = Path(tmp)
+        (tmp / "net.bin").write_bytes(net_bytes(s))
+        write_params(params, tmp / "init.bin", 0)
+        data = tmp / "data"
+        data.mkdir()
+        rng = np.random.default_rng(0)
+        for i in range(3):
+            n = 32768
+            with open(data / f"chunk_{i:04d}.bin", "wb") as fh:
+                fh.write(b"FLYD" + struct.pack("<qii", n, s["obs_dim"], s["n_act"]))
+                fh.write(rng.standard_normal((n, s["obs_dim"]), dtype=np.float32).astype(np.float16).tobytes())
+                fh.write((2 * rng.standard_normal((n, s["n_act"]), dtype=np.float32)).astype(np.float16).tobytes())
+        for B in batches:
+            n_steps = steps * max(1, 4096 // B)
+            cmd = [str(exe), str(tmp / "net.bin"), str(tmp / "init.bin"), str(data), str(tmp / f"out{B}"),
+                   "--batch", str(B), "--steps", str(n_steps), "--log", str(n_steps // 2), "--eval-batches", "0",
+                   "--save-sec", "1e9", "--ring", "3"]
+            print(f"# trainer B={B}: {n_steps} steps", file=sys.stderr, flush=True)
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+            rates = [float(m.group(1)) for m in re.finditer(r"^step \d+ \| ([0-9.]+) samples/s", r.stdout, re.M)]
+            if r.returncode != 0 or not rates:
+                raise RuntimeError(f"flyguy_train failed ({r.returncode}): {r.stderr[-2000:]}")
+            out[f"B={B}"] = {"value": rates[-1], "unit": "samples/s", "steps_timed": n_steps - n_steps // 2}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,6 +142,7 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=8192)
     ap.add_argument("--cpu-train-batch", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--trainer-steps", type=int, default=60, help="teaching-trainer loop steps at B=4096 (0: skip)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 copies of 1 GiB (read 1 GiB, write 1 GiB each) so a counter run can scale "
                          "FETCH_SIZE / WRITE_SIZE by what they read for a copy of known size")
@@ -139,43 +184,44 @@ def main() -> int:
     print(f"# set-up {time.perf_counter() - t_setup:.1f} s", file=sys.stderr, flush=True)
     ab = algorithmic_bytes(s, B)
 
+    def timed(fn):
+        """K calls bracketed by synchronisations, with per-stage HIP events on the library's stream (fc_profile)"""
+        call("fc_profile", core, 1)
+        profile_read(core, reset=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(K):
+            fn()
+        torch.cuda.synchronize()
+        t = time.perf_counter() - t0
+        prof = profile_read(core, reset=True)
+        call("fc_profile", core, 0)
+        return t, prof
+
     # ---- batched forward
+    def fwd():
+        call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)
     for _ in range(W):
-        call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)
+        fwd()
     torch.cuda.synchronize()
-    call("fc_profile", core, 1)
-    profile_read(core, reset=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(K):
-        call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)
-    torch.cuda.synchronize()
-    t_fwd = time.perf_counter() - t0
-    prof_fwd = profile_read(core, reset=True)
-    call("fc_profile", core, 0)
+    t_fwd, prof_fwd = timed(fwd)
     assert torch.isfinite(logits).all()
     ms_fwd = 1e3 * t_fwd / K
     dps = B * K / t_fwd
     print(f"# forward: {ms_fwd:.3f} ms / batch of {B}, {dps:,.0f} decisions/s", file=sys.stderr, flush=True)
 
     # ---- teaching step
+    def teach():
+        call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4, 3e-5, 1e-4, 0.0, 0.999, stats.data_ptr())
     for _ in range(W):
-        call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4, 3e-5, 1e-4, 0.0, 0.999, stats.data_ptr())
+        teach()
     torch.cuda.synchronize()
-    call("fc_profile", core, 1)
-    profile_read(core, reset=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(K):
-        call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4, 3e-5, 1e-4, 0.0, 0.999, stats.data_ptr())
-    torch.cuda.synchronize()
-    t_train = time.perf_counter() - t0
-    prof_train = profile_read(core, reset=True)
-    call("fc_profile", core, 0)
+    t_train, prof_train = timed(teach)
     assert np.isfinite(float(stats[0]))
+    kl = float(stats[0]) / B
     ms_train = 1e3 * t_train / K
     sps = B * K / t_train
-    print(f"# train: {ms_train:.3f} ms / step of {B}, {sps:,.0f} samples/s, kl {float(stats[0]) / B:.4f}",
+    print(f"# train: {ms_train:.3f} ms / step of {B}, {sps:,.0f} samples/s, kl {kl:.4f}",
           file=sys.stderr, flush=True)
 
     def stage_ms(prof, name):
@@ -200,6 +246,17 @@ def main() -> int:
     cpu_f = cpu_t = None
     if not args.no_cpu:
         cpu_f, cpu_t = cpu_baselines(s, params, args.cpu_sample, args.cpu_train_batch)
+    L.fc_free(core)
+    core = None
+    trainer = None
+    if args.trainer_steps > 0:
+        trainer = trainer_leg(s, params, (4096, 512), args.trainer_steps)
+        trainer["workload"] = ("flyguy_train loop on synthetic binary16 FLYD chunks (3 x 32,768 samples, ring of 3) of "
+                               "the same network: draw, gather, teaching step, samples/s from its own log")
+        trainer["reference_published"] = {"value": 10300, "unit": "samples/s", "batch": 512,
+                                          "hardware": "RTX 4070 laptop"}
+        print(f"# trainer: {trainer['B=4096']['value']:,.0f} samples/s at B=4096, "
+              f"{trainer['B=512']['value']:,.0f} at B=512", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC, "value": round(dps, 1), "unit": "decisions/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -226,11 +283,11 @@ def main() -> int:
                                "whole_step_frac": round(ab["train"] / (t_train / K) / PEAK_HBM, 4),
                                "whole_step_algorithmic_bytes": ab["train"]},
                   "cpu_baseline": cpu_t},
+        "trainer": trainer,
         "stages_ms": {"forward": {k: round(v[0] / v[1], 4) for k, v in prof_fwd.items()},
                       "train": {k: round(v[0] / v[1], 4) for k, v in prof_train.items()}},
     }
     print(json.dumps(line), flush=True)
-    L.fc_free(core)
     if args.calibrate:
         a = torch.ones(1 << 28, device=dev)
         b = torch.empty_like(a)
