@@ -15,6 +15,7 @@ vp, ci, cll, cf = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_flo
 _SIGS = {
     "fc_create": (vp, [ctypes.c_char_p, ci]),
     "fc_create_from_memory": (vp, [ctypes.c_char_p, cll, ci]),
+    "fc_create_ex": (vp, [ctypes.c_char_p, cll, ci, ci]),
     "fc_free": (None, [vp]),
     "fc_set_stream": (None, [vp, vp]),
     "fc_sizes": (None, [vp, ctypes.POINTER(cll)]),

@@ -18,8 +18,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libflyguy_core.so"
 EXE = PKG / "flyguy_train"
-SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "hop_api.hip", "half.hip", "train.hip")]
-HEADERS = [PKG / "csrc" / n for n in ("common.h", "kernels.h", "device.h", "core.h")] + \
+SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "core16.hip", "hop_api.hip", "half.hip", "train.hip")]
+HEADERS = [PKG / "csrc" / n for n in ("common.h", "kernels.h", "device.h", "core.h", "half.h")] + \
     [ROOT / "include" / "flyguy_core.h", ROOT / "include" / "flyguy_train.h"]
 ARCH = os.environ.get("FLYGUY_OFFLOAD_ARCH", "gfx950")
 

@@ -14,6 +14,7 @@
 namespace fg {
 
 constexpr int TW = 32;          // columns (samples) per tile
+constexpr int TW16 = 64;        // samples per tile of 16-bit states (one 128-byte line)
 constexpr int LPR = TW / 4;     // lanes per row: each lane holds a float4 of the tile
 constexpr int RPW = 64 / LPR;   // rows per wave (8)
 constexpr int WG = 256;         // threads per workgroup

@@ -76,6 +76,7 @@ struct Core {
     float* sstats = nullptr;         //   and the loss sums {KL, agreements}
     double s_samples = 0;
     long long rows_total = 0;
+    int prec = 0;                    // 0: float32 states [B/32][rows][32]; 1: bfloat16 states [B/64][rows][64]
     long long adam_t = 0;
     int B = 0;
     hipStream_t st = nullptr;
@@ -115,7 +116,8 @@ T* dalloc(Core& c, size_t n) {
     return (T*)p;
 }
 
-Core* build(const unsigned char* bytes, long long len, int max_batch);
+// prec: 0 float32 states, 1 bfloat16 states (the batch then a multiple of 64)
+Core* build(const unsigned char* bytes, long long len, int max_batch, int prec = 0);
 void release(Core* c);
 bool check_batch(const Core* c, int B);
 bool prof_collect(Core& c);

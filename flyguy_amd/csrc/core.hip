@@ -186,7 +186,7 @@ static bool distinct(const std::vector<int>& v, long long n, bool skip_negative)
     return true;
 }
 
-Core* build(const unsigned char* bytes, long long len, int max_batch) {
+Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) {
     clear_error();
     if (!bytes || len < 36 || std::memcmp(bytes, "FLY1", 4) != 0) {
         set_error("not a FLY1 network file");
@@ -196,7 +196,12 @@ Core* build(const unsigned char* bytes, long long len, int max_batch) {
         set_error("max_batch must be positive");
         return nullptr;
     }
+    if (prec != 0 && prec != 1) {
+        set_error("unknown state precision");
+        return nullptr;
+    }
     std::unique_ptr<Core, void (*)(Core*)> c(new Core, release);
+    c->prec = prec;
     Reader r{bytes, len, 4};
     auto hd = r.ints(8);
     if (!r.ok) { set_error("short network file (header)"); return nullptr; }
@@ -244,7 +249,8 @@ Core* build(const unsigned char* bytes, long long len, int max_batch) {
     if (!distinct(dn, c->sizes[K], false)) { set_error("bad read-out rows"); return nullptr; }
 
     // plans
-    const int bm = (max_batch + TW - 1) / TW * TW;
+    const int tq = prec ? TW16 : TW;
+    const int bm = (max_batch + tq - 1) / tq * tq;
     c->maxB = bm;
     c->Tm = bm / TW;
     HostPlan hp;
@@ -304,16 +310,20 @@ Core* build(const unsigned char* bytes, long long len, int max_batch) {
     c->pm = dalloc<float>(*c, (size_t)(5 * o));
     if (!c->pm) return nullptr;
 
-    // states and partial sums
+    // states (float32 or bfloat16, max_batch samples per row) and partial sums
     const size_t Tm = c->Tm, S = TW;
-    c->x = dalloc<float>(*c, Tm * c->obs_dim * S);
-    c->drive = dalloc<float>(*c, Tm * c->n_s * S);
-    c->h0 = dalloc<float>(*c, Tm * c->n_s * S);
+    auto state = [&](long long rows) -> float* {
+        return prec ? reinterpret_cast<float*>(dalloc<unsigned short>(*c, (size_t)bm * rows))
+                    : dalloc<float>(*c, (size_t)bm * rows);
+    };
+    c->x = state(c->obs_dim);
+    c->drive = state(c->n_s);
+    c->h0 = state(c->n_s);
     c->gdrive = dalloc<float>(*c, Tm * c->n_s * S);
-    c->gz[0] = dalloc<float>(*c, Tm * max_rows * S);
-    c->gz[1] = dalloc<float>(*c, Tm * max_rows * S);
+    c->gz[0] = state(max_rows);
+    c->gz[1] = state(max_rows);
     for (auto& d : c->hop) {
-        d.h = dalloc<float>(*c, Tm * d.rows * S);
+        d.h = state(d.rows);
         d.ggp = dalloc<float>(*c, Tm * d.rows);
         d.gsp = dalloc<float>(*c, Tm * d.rows);
         d.info = dalloc<float4>(*c, d.rows);
@@ -345,8 +355,10 @@ Core* build(const unsigned char* bytes, long long len, int max_batch) {
 
 bool check_batch(const Core* c, int B) {
     if (!c) { set_error("null handle"); return false; }
-    if (B <= 0 || B % TW != 0 || B > c->maxB) {
-        set_error("batch " + std::to_string(B) + " must be a positive multiple of 32 and at most " + std::to_string(c->maxB));
+    const int q = c->prec ? TW16 : TW;
+    if (B <= 0 || B % q != 0 || B > c->maxB) {
+        set_error("batch " + std::to_string(B) + " must be a positive multiple of " + std::to_string(q) + " and at most " +
+                  std::to_string(c->maxB));
         return false;
     }
     return true;
@@ -361,7 +373,11 @@ static hipError_t rowinfo(Core& c, const float* gain, const float* theta) {
     return e;
 }
 
+static bool forward16(Core& c, const float* obs, int B, float* logits, int set);
+static bool backward16(Core& c, const float* dlogits, int B);
+
 bool forward(Core& c, const float* obs, int B, float* logits, int set) {
+    if (c.prec) return forward16(c, obs, B, logits, set);
     const int T = B / TW;
     hipStream_t st = c.st;
     { Timed t(c, ST_OBS); FG_CHECK(launch_obs_in(obs, c.x, c.obs_dim, B, st), false); }
@@ -400,6 +416,7 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
 }
 
 bool backward(Core& c, const float* dlogits, int B) {
+    if (c.prec) return backward16(c, dlogits, B);
     const int T = B / TW, K = c.hops;
     hipStream_t st = c.st;
     const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
@@ -480,6 +497,131 @@ bool backward(Core& c, const float* dlogits, int B) {
     return true;
 }
 
+// ---- the same passes over bfloat16 states (core16.hip): tiles of 64 samples
+typedef unsigned short u16;
+static u16* s16(float* p) { return reinterpret_cast<u16*>(p); }
+
+static bool forward16(Core& c, const float* obs, int B, float* logits, int set) {
+    const int T = B / TW16;
+    hipStream_t st = c.st;
+    { Timed t(c, ST_OBS); FG_CHECK(launch_obs_in16(obs, s16(c.x), c.obs_dim, B, st), false); }
+    const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
+    {
+        Timed t(c, ST_PACK);
+        FG_CHECK(launch_pack(c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos, st), false);
+        for (auto& d : c.hop) FG_CHECK(launch_pack(d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos, st), false);
+        FG_CHECK(rowinfo(c, gain, theta), false);
+    }
+    FwdEpi16 e0;
+    e0.bias = c.arr(set, 4);
+    e0.info = c.info0;
+    e0.z = s16(c.drive);
+    e0.h = s16(c.h0);
+    e0.rows = c.n_s;
+    { Timed t(c, ST_PLUG); FG_CHECK(launch_fwd16c(c.pp.view(), c.in_cw, s16(c.x), c.obs_dim, e0, c.part, T, st), false); }
+    const u16* hp = s16(c.h0);
+    int hk = 0;
+    for (auto& d : c.hop) {
+        FwdEpi16 e;
+        e.info = d.info;
+        if (d.has_drive) { e.drive = s16(c.drive); e.n_s = c.n_s; }
+        e.h = s16(d.h);
+        e.rows = d.rows;
+        { Timed t(c, ST_HOP + std::min(hk, 7)); FG_CHECK(launch_fwd16c(d.fp.view(), d.cw, hp, d.src, e, c.part, T, st), false); }
+        hp = s16(d.h);
+        ++hk;
+    }
+    {
+        Timed t(c, ST_LOGITS);
+        FG_CHECK(launch_logits16(hp, c.sizes[c.hops], c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, logits, B, st),
+                 false);
+    }
+    c.B = B;
+    return true;
+}
+
+static bool backward16(Core& c, const float* dlogits, int B) {
+    const int T = B / TW16, K = c.hops;
+    hipStream_t st = c.st;
+    const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
+    float* G[7];
+    for (int i = 0; i < 7; ++i) G[i] = c.arr(SET_G, i);
+    { Timed t(c, ST_ZERO); FG_CHECK(launch_fill(c.gdrive, 0.f, (long long)B * c.n_s, st), false); }
+    {
+        Timed t(c, ST_PACK);
+        for (auto& d : c.hop) FG_CHECK(launch_pack(d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos, st), false);
+        FG_CHECK(rowinfo(c, gain, theta), false);
+    }
+    HopD& top = c.hop[K - 1];
+    BwdEpi16 et;
+    et.mode = 1;
+    et.h = s16(top.h);
+    et.rows = top.rows;
+    et.info = top.info;
+    et.drow = top.has_drive ? top.drow : nullptr;
+    et.gz_out = s16(c.gz[0]);
+    et.gdrive = c.gdrive;
+    et.n_s = c.n_s;
+    et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
+    {
+        Timed t(c, ST_RBWD);
+        FG_CHECK(launch_readout_bwd_h16(dlogits, c.arr(SET_P, 5), c.dn_inv, c.n_dn, c.n_act, top.rows, et, B, st), false);
+        FG_CHECK(launch_readout_bwd_w16(dlogits, s16(top.h), top.rows, c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st), false);
+    }
+    const int nch = readout_chunks(B);
+    {
+        Timed t(c, ST_REDUCE);
+        FG_CHECK(launch_reduce(c.gow_p, (long long)c.n_act * c.n_dn, (long long)c.n_act * c.n_dn, nch, nullptr, nullptr, G[5], st), false);
+        FG_CHECK(launch_reduce(c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], st), false);
+        FG_CHECK(launch_reduce(top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1], st), false);
+        FG_CHECK(launch_reduce(top.gsp, top.rows, top.rows, T, top.nid, theta, G[2], st), false);
+    }
+    int cur = 0;
+    for (int k = K; k >= 1; --k) {
+        HopD& d = c.hop[k - 1];
+        BwdEpi16 e;
+        e.gdrive = c.gdrive;
+        e.n_s = c.n_s;
+        int rows_below;
+        float *ggp, *gsp;
+        const int* nid_below;
+        if (k >= 2) {
+            HopD& b = c.hop[k - 2];
+            e.mode = 1;
+            e.h = s16(b.h);
+            e.rows = b.rows;
+            e.info = b.info;
+            e.gz_out = s16(c.gz[cur ^ 1]);
+            rows_below = b.rows; ggp = b.ggp; gsp = b.gsp; nid_below = b.nid;
+        } else {
+            e.mode = 2;
+            e.h = s16(c.h0);
+            e.z = s16(c.drive);
+            e.rows = c.n_s;
+            e.info = c.info0;
+            e.in_crow = c.in_crow; e.in_col = c.in_col; e.x = s16(c.x); e.x_rows = c.obs_dim;
+            e.ginb_part = c.ginb; e.gb_ld = c.n_s;
+            e.ginw_part = c.ginw; e.gw_ld = c.E_in;
+            rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
+        }
+        e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
+        {
+            Timed t(c, ST_BHOP + std::min(k - 1, 7));
+            FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, c.gwpart, d.bp.npos, e, c.part, T, st), false);
+        }
+        Timed t(c, ST_REDUCE);
+        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, T, d.bp.pidx, nullptr, G[0], st), false);
+        FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
+        FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
+        if (k == 1) {
+            FG_CHECK(launch_reduce(c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], st), false);
+            FG_CHECK(launch_reduce(c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], st), false);
+        }
+        cur ^= 1;
+    }
+    return true;
+}
+
 float grad_norm(Core& c) {
     if (launch_sumsq(c.arr(SET_G, 0), c.PT, c.red, c.nrm, c.st) != hipSuccess) { set_error("grad norm launch"); return -1.f; }
     float ss = 0.f;
@@ -520,6 +662,14 @@ void fc_clear_error(void) { fg::clear_error(); }
 
 void* fc_create_from_memory(const void* net_bytes, long long len, int max_batch) {
     return build((const unsigned char*)net_bytes, len, max_batch);
+}
+
+void* fc_create_ex(const void* net_bytes, long long len, int max_batch, int flags) {
+    if (flags & ~FC_STATES_BF16) {
+        set_error("fc_create_ex: unknown flags");
+        return nullptr;
+    }
+    return build((const unsigned char*)net_bytes, len, max_batch, (flags & FC_STATES_BF16) ? 1 : 0);
 }
 
 void* fc_create(const char* net_path, int max_batch) {
@@ -630,6 +780,14 @@ void fc_export_state(void* h, int layer, int what, float* dst, int B) {
     }
     const float* src;
     int rows;
+    if (c->prec) {
+        if (what == 2) { src = c->x; rows = c->obs_dim; }
+        else if (layer == 0) { src = what == 0 ? c->h0 : c->drive; rows = c->n_s; }
+        else if (what == 1) { set_error("fc_export_state: a hop layer's pre-activation is not kept (only h)"); return; }
+        else { src = c->hop[layer - 1].h; rows = c->hop[layer - 1].rows; }
+        FG_CHECK(launch_export16(reinterpret_cast<const unsigned short*>(src), rows, dst, B, c->st), );
+        return;
+    }
     if (what == 2) { src = c->x; rows = c->obs_dim; }
     else if (layer == 0) { src = what == 0 ? c->h0 : c->drive; rows = c->n_s; }
     else {

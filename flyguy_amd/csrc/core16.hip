@@ -1,0 +1,540 @@
+// The library core with bfloat16 states: the observations x, the sensory layer's drive, every layer's output h and
+// the gradients gz the backward gathers are stored as bfloat16 (round to nearest even).  Sums, split-row partials,
+// the drive's gradient, the per-tile gradient partials, the weights and Adam stay float32.
+//
+// A 16-bit state tensor is [T = B/64][rows][64]: one 128-byte line per row holds 64 samples, so a gathered source
+// line serves twice the samples it serves in the float32 layout ([B/32][rows][32]).  Each lane of an 8-lane group
+// holds 8 samples.  Row plans, (source, weight) pairs, the gather loop and the per-edge weight gradient's
+// reduce-scatter are those of the float32 kernels (kernels.hip); the epilogues do the same neuron arithmetic in float32
+// on the widened values.  Quantities derived from a state use its stored (rounded) value: a hop layer's gain gradient
+// uses z = (h + softplus(theta)) / gain of the stored h, the sensory layer's the stored drive, and the drive's
+// gradient collects the hops' gz before their rounding.  Float32 tensors beside them (partials, the drive's gradient)
+// use the same tiling, [T][rows][64] floats.
+#include "half.h"
+
+namespace fg {
+
+typedef unsigned short bf16_t;
+
+__device__ __forceinline__ void ld8(const bf16_t* base, int rows, int tile, int row, int sub, float (&f)[8]) {
+    unpack8<BF16>(*reinterpret_cast<const u32x4*>(base + ((size_t)tile * rows + row) * TW16 + sub * 8), f);
+}
+// two floats -> two bfloat16 in one word (low half first), rounded to nearest even by the hardware conversion
+__device__ __forceinline__ unsigned pack2(float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    const bf2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ void st8(bf16_t* base, int rows, int tile, int row, int sub, const float (&f)[8]) {
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = pack2(f[2 * k], f[2 * k + 1]);
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(base + ((size_t)tile * rows + row) * TW16 + sub * 8));
+}
+__device__ __forceinline__ float* f8p(float* base, int rows, int tile, int row, int sub) {
+    return base + ((size_t)tile * rows + row) * TW16 + sub * 8;
+}
+__device__ __forceinline__ void ldf8(const float* p, float (&f)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+// ------------------------------------------------------------------------------------------------ forward
+struct FwdIn16 {
+    float dv[8];
+    float g, sp;
+};
+__device__ __forceinline__ void fwd_inputs16(const FwdEpi16& e, int t, int d, int tile, int sub, FwdIn16& in) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) in.dv[k] = 0.f;
+    in.g = in.sp = 0.f;
+    if (e.drive && d >= 0) ld8(e.drive, e.n_s, tile, d, sub, in.dv);
+    if (e.info) {
+        const float4 r = e.info[t];
+        in.g = r.x;
+        in.sp = r.y;
+    }
+}
+__device__ __forceinline__ void fwd_finish16(const FwdEpi16& e, int t, int tile, int sub, float (&acc)[8], const FwdIn16& in) {
+    if (e.drive)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] += in.dv[k];
+    if (e.z) st8(e.z, e.rows, tile, t, sub, acc);
+    if (e.info) {
+        float hv[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) hv[k] = fmaxf(fmaf(in.g, acc[k], -in.sp), 0.f);
+        st8(e.h, e.rows, tile, t, sub, hv);
+    }
+}
+
+// the plug or one hop over its row plan (as k_fwd); split rows leave float32 partials [T][nslot][64]
+__global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ cw, const bf16_t* __restrict__ src,
+                                               int src_rows, FwdEpi16 epi, float* __restrict__ part, int T, int RB) {
+    __shared__ __align__(16) int2 slots[WG / LPR][LPR];
+    int rb;
+    const int tile = tile_of(blockIdx.x, RB, T, rb);
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
+    int2 wv;
+    const bool wok = load_wave(p, w, wv);
+    const int2* q = cw + wv.x + lane;
+    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    int4 sg;
+    const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(src + (size_t)tile * src_rows * TW16), (short)0, src_rows * 128, 0x00020000);
+    const bool whole = live && sg.y < 0;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    FwdIn16 in{};
+    for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
+        int c[8];
+        float wt[8];
+        stage8(slots[grp], sub, nxt, c, wt);
+        u32x4 raw[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) raw[s] = s < left ? gather16(rs, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
+        __builtin_amdgcn_sched_barrier(0);
+        if (left > 8) nxt = q[64 * (j + 1)];
+        if (j == 0 && whole) {                 // the row's own inputs after the first gathers; the bias starts the sum
+            fwd_inputs16(epi, sg.x, sg.z, tile, sub, in);
+            if (epi.bias) {
+                const float b = epi.bias[sg.x];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[k] = b;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            float f[8];
+            unpack8<BF16>(raw[s], f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[k] = fmaf(wt[s], f[k], acc[k]);
+        }
+    }
+    if (whole && !(wok && wv.y > 0)) {          // a wave without edges
+        fwd_inputs16(epi, sg.x, sg.z, tile, sub, in);
+        if (epi.bias) {
+            const float b = epi.bias[sg.x];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[k] = b;
+        }
+    }
+    if (!live) return;
+    if (sg.y >= 0) {
+        store8(part + ((size_t)tile * p.nslot + sg.y) * TW16 + sub * 8, acc);
+        return;
+    }
+    fwd_finish16(epi, sg.x, tile, sub, acc, in);
+}
+
+__global__ __launch_bounds__(WG) void k_cfwd16_combine(Plan p, const float* __restrict__ part, FwdEpi16 epi, int T) {
+    long long q = ((long long)blockIdx.x * WG + threadIdx.x);
+    const int sub = (int)(q & 7);
+    q >>= 3;
+    const int tile = (int)(q % T);
+    const long long i = q / T;
+    int4 s;
+    if (!load_split(p, i, s)) return;
+    const float b = epi.bias ? epi.bias[s.x] : 0.f;
+    float acc[8] = {b, b, b, b, b, b, b, b};
+    FwdIn16 in{};
+    fwd_inputs16(epi, s.x, s.w, tile, sub, in);
+    for (int k = 0; k < s.z; ++k) {
+        float v[8];
+        ldf8(part + ((size_t)tile * p.nslot + s.y + k) * TW16 + sub * 8, v);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) acc[m] += v[m];
+    }
+    fwd_finish16(epi, s.x, tile, sub, acc, in);
+}
+
+// ------------------------------------------------------------------------------------------------ backward
+struct BwdIn16 {
+    float h[8], z[8], gd[8];
+    float gn, sp;
+    int d;
+};
+// MODE 1: a hop layer (d: the row's re-drive row); 2: the sensory layer
+template <int MODE>
+__device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, int tile, int sub, BwdIn16& in) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) in.z[k] = in.gd[k] = 0.f;
+    in.d = MODE == 2 ? j : d;
+    if (in.d >= 0) ldf8(f8p(e.gdrive, e.n_s, tile, in.d, sub), in.gd);
+    ld8(e.h, e.rows, tile, j, sub, in.h);
+    if constexpr (MODE == 2) ld8(e.z, e.rows, tile, j, sub, in.z);
+    const float4 r = e.info[j];
+    in.gn = r.x;
+    in.sp = r.y;
+}
+
+template <int MODE>
+__device__ __forceinline__ void bwd_finish16(const BwdEpi16& e, int j, int tile, int sub, const float (&gh)[8],
+                                             const BwdIn16& in) {
+    float g[8], gzv[8];
+    float sg = 0.f, sgh = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        g[k] = in.h[k] > 0.f ? gh[k] : 0.f;
+        gzv[k] = g[k] * in.gn;
+        sg += g[k];
+        sgh = fmaf(g[k], MODE == 1 ? in.h[k] : in.z[k], sgh);
+    }
+    const float ps = gsum8(sg);
+    float pg;
+    if constexpr (MODE == 1) pg = in.gn != 0.f ? (gsum8(sgh) + in.sp * ps) / in.gn : 0.f;   // (see k_bwd)
+    else pg = gsum8(sgh);
+    if (sub == 0) {
+        e.ggain_part[(size_t)tile * e.gp_ld + j] = pg;
+        e.gsum_part[(size_t)tile * e.gp_ld + j] = ps;
+    }
+    if constexpr (MODE == 1) {
+        st8(e.gz_out, e.rows, tile, j, sub, gzv);
+        if (in.d >= 0) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = in.gd[k] + gzv[k];
+            store8(f8p(e.gdrive, e.n_s, tile, in.d, sub), v);
+        }
+        return;
+    }
+    // the sensory layer: the drive's gradient is complete -> the plug's bias and per-connection gradients
+    float gd[8];
+    float sb = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        gd[k] = in.gd[k] + gzv[k];
+        sb += gd[k];
+    }
+    const float pb = gsum8(sb);
+    if (sub == 0) e.ginb_part[(size_t)tile * e.gb_ld + j] = pb;
+    float* gwo = e.ginw_part + (size_t)tile * e.gw_ld;
+    const int f0 = e.in_crow[j], f1 = e.in_crow[j + 1];
+    for (int f = f0; f < f1; f += 8) {
+        const int mc = f + sub < f1 ? e.in_col[f + sub] : NO_ROW;
+        int c[8];
+        c[0] = bcast8<0>(mc); c[1] = bcast8<1>(mc); c[2] = bcast8<2>(mc); c[3] = bcast8<3>(mc);
+        c[4] = bcast8<4>(mc); c[5] = bcast8<5>(mc); c[6] = bcast8<6>(mc); c[7] = bcast8<7>(mc);
+        float dd[8];
+#pragma unroll
+        for (int s2 = 0; s2 < 8; ++s2) {
+            const bool ok = (unsigned)c[s2] < (unsigned)e.x_rows;
+            float xv[8];
+            ld8(e.x, e.x_rows, tile, ok ? c[s2] : 0, sub, xv);
+            float dp = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) dp = fmaf(gd[k], xv[k], dp);
+            dd[s2] = ok ? dp : 0.f;
+        }
+        const float pw = rs8(dd, sub);
+        if (f + sub < f1) gwo[f + sub] = pw;
+    }
+}
+
+// over the transposed plan (rows = the layer below, j): gh_j = sum W gz (gathered), the per-edge weight gradient
+// partial sum over the tile of gz * h_j, then the layer's neuron backward
+template <int MODE>
+__global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ cw, const bf16_t* __restrict__ gz,
+                                               int gz_rows, float* __restrict__ gwpart, long long gw_ld, BwdEpi16 epi,
+                                               float* __restrict__ part, int T, int RB) {
+    __shared__ __align__(16) int2 slots[WG / LPR][LPR];
+    int rb;
+    const int tile = tile_of(blockIdx.x, RB, T, rb);
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
+    int2 wv;
+    const bool wok = load_wave(p, w, wv);
+    const int2* q = cw + wv.x + lane;
+    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    int4 sg;
+    const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(gz + (size_t)tile * gz_rows * TW16), (short)0, gz_rows * 128, 0x00020000);
+    float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
+    const bool whole = live && sg.y < 0;
+    float hj[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    BwdIn16 in{};
+    for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
+        int c[8];
+        float wt[8];
+        stage8(slots[grp], sub, nxt, c, wt);
+        u32x4 raw[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) raw[s] = s < left ? gather16(rs, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
+        __builtin_amdgcn_sched_barrier(0);
+        if (left > 8) nxt = q[64 * (j + 1)];
+        if (j == 0) {                           // the row's own inputs, after the first gathers
+            if (whole) {
+                bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) hj[k] = in.h[k];
+            } else if (live) {
+                ld8(epi.h, epi.rows, tile, sg.x, sub, hj);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float d[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            float f[8];
+            unpack8<BF16>(raw[s], f);
+            float dp = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                acc[k] = fmaf(wt[s], f[k], acc[k]);
+                dp = fmaf(hj[k], f[k], dp);
+            }
+            d[s] = dp;
+        }
+        if (gwp) gwp[64 * j] = rs8(d, sub);
+    }
+    if (whole && !(wok && wv.y > 0)) bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in);
+    if (!live) return;
+    if (sg.y >= 0) {
+        store8(part + ((size_t)tile * p.nslot + sg.y) * TW16 + sub * 8, acc);
+        return;
+    }
+    bwd_finish16<MODE>(epi, sg.x, tile, sub, acc, in);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(WG) void k_cbwd16_combine(Plan p, const float* __restrict__ part, BwdEpi16 epi, int T) {
+    long long q = ((long long)blockIdx.x * WG + threadIdx.x);
+    const int sub = (int)(q & 7);
+    q >>= 3;
+    const int tile = (int)(q % T);
+    const long long i = q / T;
+    int4 s;
+    if (!load_split(p, i, s)) return;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    BwdIn16 in{};
+    bwd_inputs16<MODE>(epi, s.x, s.w, tile, sub, in);
+    for (int k = 0; k < s.z; ++k) {
+        float v[8];
+        ldf8(part + ((size_t)tile * p.nslot + s.y + k) * TW16 + sub * 8, v);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) acc[m] += v[m];
+    }
+    bwd_finish16<MODE>(epi, s.x, tile, sub, acc, in);
+}
+
+// ------------------------------------------------------------------------------------------------ x, read-out
+// obs [B][obs_dim] float32 -> x [T][obs_dim][64] bfloat16; one workgroup per (tile, 64 features)
+__global__ __launch_bounds__(WG) void k_obs_in16(const float* __restrict__ obs, bf16_t* __restrict__ x, int obs_dim) {
+    __shared__ float s[TW16][65];
+    const int tile = blockIdx.y, f0 = blockIdx.x * 64;
+    for (int i = threadIdx.x; i < TW16 * 64; i += WG) {
+        const int c = i / 64, f = i % 64;
+        s[c][f] = (f0 + f < obs_dim) ? obs[(size_t)(tile * TW16 + c) * obs_dim + f0 + f] : 0.f;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < TW16 * 64; i += WG) {
+        const int f = i / TW16, c = i % TW16;
+        if (f0 + f < obs_dim) x[((size_t)tile * obs_dim + f0 + f) * TW16 + c] = __builtin_bit_cast(bf16_t, (__bf16)s[c][f]);
+    }
+}
+
+// logits[b][a] = ob[a] + sum_j ow[a][j] * hK[dn[j]][b] in j order (as k_logits); one workgroup per (tile, 32 actions)
+constexpr int LG_J16 = 32;
+__global__ __launch_bounds__(WG) void k_logits16(const bf16_t* __restrict__ hK, int rows, const int* __restrict__ dn,
+                                                 int n_dn, const float* __restrict__ ow, const float* __restrict__ ob,
+                                                 int n_act, float* __restrict__ logits) {
+    __shared__ float hs[LG_J16][TW16];
+    __shared__ float ws[RPG][LG_J16 + 1];
+    const int tile = blockIdx.x, a0 = blockIdx.y * RPG;
+    const int g = threadIdx.x >> 3, sub = threadIdx.x & 7, a = a0 + g;
+    const float b0 = a < n_act ? ob[a] : 0.f;
+    float acc[8] = {b0, b0, b0, b0, b0, b0, b0, b0};
+    for (int j0 = 0; j0 < n_dn; j0 += LG_J16) {
+        const int nj = min(LG_J16, n_dn - j0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < LG_J16 * LPR; i += WG) {
+            const int jj = i / LPR, qq = i % LPR;
+            float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (jj < nj) ld8(hK, rows, tile, dn[j0 + jj], qq, f);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) hs[jj][qq * 8 + k] = f[k];
+        }
+        for (int i = threadIdx.x; i < RPG * LG_J16; i += WG) {
+            const int aa = i / LG_J16, jj = i % LG_J16;
+            ws[aa][jj] = (jj < nj && a0 + aa < n_act) ? ow[(size_t)(a0 + aa) * n_dn + j0 + jj] : 0.f;
+        }
+        __syncthreads();
+        for (int jj = 0; jj < nj; ++jj) {
+            const float wv = ws[g][jj];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[k] = fmaf(wv, hs[jj][sub * 8 + k], acc[k]);
+        }
+    }
+    if (a >= n_act) return;
+    float* o = logits + (size_t)(tile * TW16 + sub * 8) * n_act + a;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[(size_t)k * n_act] = acc[k];
+}
+
+// gh of the top layer from the logits' gradient, then its neuron backward (as k_readout_bwd_h)
+__global__ __launch_bounds__(WG) void k_rbwd_h16(const float* __restrict__ dl, const float* __restrict__ ow,
+                                                 const int* __restrict__ dn_inv, int n_dn, int n_act, int rows,
+                                                 BwdEpi16 epi) {
+    extern __shared__ float sm[];
+    float* dlT = sm;                         // [n_act][64]
+    float* owc = sm + (size_t)n_act * TW16;  // [32][n_act]
+    const int tile = blockIdx.y, r0 = blockIdx.x * RPG;
+    for (int i = threadIdx.x; i < n_act * TW16; i += WG) {
+        const int c = i / n_act, a = i % n_act;
+        dlT[a * TW16 + c] = dl[(size_t)(tile * TW16 + c) * n_act + a];
+    }
+    for (int i = threadIdx.x; i < RPG * n_act; i += WG) {
+        const int r = i / n_act, a = i % n_act, t = r0 + r;
+        const int j = t < rows ? dn_inv[t] : -1;
+        owc[r * n_act + a] = j >= 0 ? ow[(size_t)a * n_dn + j] : 0.f;
+    }
+    __syncthreads();
+    const int r = threadIdx.x >> 3, sub = threadIdx.x & 7, t = r0 + r;
+    if (t >= rows) return;                   // whole 8-lane groups
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (dn_inv[t] >= 0)
+        for (int a = 0; a < n_act; ++a) {
+            const float wv = owc[r * n_act + a];
+            const float* d = dlT + a * TW16 + sub * 8;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[k] = fmaf(wv, d[k], acc[k]);
+        }
+    BwdIn16 in{};
+    bwd_inputs16<1>(epi, t, epi.drow ? epi.drow[t] : -1, tile, sub, in);
+    bwd_finish16<1>(epi, t, tile, sub, acc, in);
+}
+
+// per chunk of 8 tiles (512 samples): gow[a][j] partial = sum_b dl[b][a] * hK[dn[j]][b], gob[a] partial = sum_b dl[b][a]
+constexpr int RO_CHUNK16 = 8;
+__global__ __launch_bounds__(WG) void k_rbwd_w16(const float* __restrict__ dl, const bf16_t* __restrict__ hK, int rows,
+                                                 const int* __restrict__ dn, int n_dn, int n_act, int T,
+                                                 float* __restrict__ gow_part, float* __restrict__ gob_part) {
+    __shared__ float hT[32][TW16 + 1];
+    __shared__ float ds[TW16][97];
+    const int j0 = blockIdx.x * 32, chunk = blockIdx.y;
+    const int jj = threadIdx.x & 31, ag = threadIdx.x >> 5;
+    const int t0 = chunk * RO_CHUNK16, t1 = min(T, t0 + RO_CHUNK16);
+    for (int a0 = 0; a0 < n_act; a0 += 96) {
+        float acc[12];
+        float accb = 0.f;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) acc[i] = 0.f;
+        for (int tile = t0; tile < t1; ++tile) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < 32 * TW16; i += WG) {
+                const int j = i / TW16, c = i % TW16;
+                hT[j][c] = (j0 + j < n_dn)
+                               ? __uint_as_float((unsigned)hK[((size_t)tile * rows + dn[j0 + j]) * TW16 + c] << 16)
+                               : 0.f;
+            }
+            for (int i = threadIdx.x; i < TW16 * 96; i += WG) {
+                const int c = i / 96, a = i % 96;
+                ds[c][a] = (a0 + a < n_act) ? dl[(size_t)(tile * TW16 + c) * n_act + a0 + a] : 0.f;
+            }
+            __syncthreads();
+            for (int c = 0; c < TW16; ++c) {
+                const float hv = hT[jj][c];
+#pragma unroll
+                for (int i = 0; i < 12; ++i) acc[i] = fmaf(ds[c][ag + 8 * i], hv, acc[i]);
+            }
+            if (blockIdx.x == 0 && threadIdx.x < 96)
+                for (int c = 0; c < TW16; ++c) accb += ds[c][threadIdx.x];
+        }
+        const size_t base = (size_t)chunk * n_act * n_dn;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            const int a = a0 + ag + 8 * i;
+            if (a < n_act && j0 + jj < n_dn) gow_part[base + (size_t)a * n_dn + j0 + jj] = acc[i];
+        }
+        if (blockIdx.x == 0 && threadIdx.x < 96 && a0 + threadIdx.x < n_act)
+            gob_part[(size_t)chunk * n_act + a0 + threadIdx.x] = accb;
+    }
+}
+
+// a 16-bit state -> [rows][B] float32 (tests and diagnostics)
+__global__ void k_export16(const bf16_t* __restrict__ src, int rows, float* __restrict__ dst, int B) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)rows * B) return;
+    const int r = (int)(i / B), b = (int)(i % B);
+    dst[i] = __uint_as_float((unsigned)src[((size_t)(b / TW16) * rows + r) * TW16 + (b % TW16)] << 16);
+}
+
+// ------------------------------------------------------------------------------------------------ launchers
+static inline unsigned nblocks(long long n, int per = WG) { return (unsigned)((n + per - 1) / per); }
+
+hipError_t launch_obs_in16(const float* obs, unsigned short* x, int obs_dim, int B, hipStream_t st) {
+    k_obs_in16<<<dim3((unsigned)((obs_dim + 63) / 64), (unsigned)(B / TW16)), WG, 0, st>>>(obs, x, obs_dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* src, int src_rows, const FwdEpi16& epi,
+                         float* part, int T, hipStream_t st) {
+    if (p.nwave > 0) {
+        const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
+        k_cfwd16<<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, src_rows, epi, part, T, RB);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (p.nsplit > 0) {
+        k_cfwd16_combine<<<nblocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, epi, T);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+template <int MODE>
+static hipError_t launch_bwd16c_as(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
+                                   long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st) {
+    if (p.nwave > 0) {
+        const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
+        k_cbwd16<MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, RB);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (p.nsplit > 0) {
+        k_cbwd16_combine<MODE><<<nblocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, epi, T);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
+                         long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st) {
+    if (epi.mode == 1) return launch_bwd16c_as<1>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, st);
+    if (epi.mode == 2) return launch_bwd16c_as<2>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_logits16(const unsigned short* hK, int rows, const int* dn, int n_dn, const float* ow, const float* ob,
+                           int n_act, float* logits, int B, hipStream_t st) {
+    k_logits16<<<dim3((unsigned)(B / TW16), (unsigned)((n_act + RPG - 1) / RPG)), WG, 0, st>>>(hK, rows, dn, n_dn, ow, ob,
+                                                                                             n_act, logits);
+    return hipGetLastError();
+}
+
+hipError_t launch_readout_bwd_h16(const float* dl, const float* ow, const int* dn_inv, int n_dn, int n_act, int rows,
+                                  const BwdEpi16& epi, int B, hipStream_t st) {
+    dim3 grid((unsigned)((rows + RPG - 1) / RPG), (unsigned)(B / TW16));
+    const size_t sm = (size_t)n_act * (TW16 + RPG) * sizeof(float);
+    k_rbwd_h16<<<grid, WG, sm, st>>>(dl, ow, dn_inv, n_dn, n_act, rows, epi);
+    return hipGetLastError();
+}
+
+hipError_t launch_readout_bwd_w16(const float* dl, const unsigned short* hK, int rows, const int* dn, int n_dn,
+                                  int n_act, float* gow_part, float* gob_part, int B, hipStream_t st) {
+    const int T = B / TW16;
+    dim3 grid((unsigned)((n_dn + 31) / 32), (unsigned)((T + RO_CHUNK16 - 1) / RO_CHUNK16));
+    k_rbwd_w16<<<grid, WG, 0, st>>>(dl, hK, rows, dn, n_dn, n_act, T, gow_part, gob_part);
+    return hipGetLastError();
+}
+
+hipError_t launch_export16(const unsigned short* src, int rows, float* dst, int B, hipStream_t st) {
+    k_export16<<<nblocks((long long)rows * B), WG, 0, st>>>(src, rows, dst, B);
+    return hipGetLastError();
+}
+
+}  // namespace fg

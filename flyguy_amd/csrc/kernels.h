@@ -108,6 +108,50 @@ int readout_chunks(int B);
 // idx == nullptr: i itself.  The indices a launch names are distinct, so no two threads add to one entry.
 hipError_t launch_reduce(const float* part, long long ld, long long n, int nt, const int* idx, const float* theta,
                          float* G, hipStream_t st);
+// The core with bfloat16 states (core16.hip): the epilogues of FwdEpi / BwdEpi on [T = B/64][rows][64] tiles, with
+// float32 tensors (partials, the drive's gradient) in the same tiling.
+struct FwdEpi16 {
+    const float* bias = nullptr;
+    const float4* info = nullptr;
+    const unsigned short* drive = nullptr;   // re-drive source: the sensory layer's drive (nullptr: none here)
+    int n_s = 0;                             // rows of drive
+    unsigned short* z = nullptr;             // the sensory layer's pre-activation (its drive)
+    unsigned short* h = nullptr;
+    int rows = 0;                            // rows of z and h
+};
+struct BwdEpi16 {
+    int mode = 1;                            // 1: a hop layer; 2: the sensory layer (+ plug)
+    const unsigned short* h = nullptr;       // the layer's output (also the per-edge gradient's source operand)
+    const unsigned short* z = nullptr;       // the sensory layer's drive
+    int rows = 0;
+    const float4* info = nullptr;
+    const int* drow = nullptr;               // per row: re-drive row (read-out kernel only)
+    unsigned short* gz_out = nullptr;        // mode 1: the layer's gz, gathered by the next backward
+    float* gdrive = nullptr;                 // float32 [T][n_s][64]
+    int n_s = 0;
+    float *ggain_part = nullptr, *gsum_part = nullptr;
+    long long gp_ld = 0;
+    const int *in_crow = nullptr, *in_col = nullptr;
+    const unsigned short* x = nullptr;
+    int x_rows = 0;
+    float* ginb_part = nullptr;
+    long long gb_ld = 0;
+    float* ginw_part = nullptr;
+    long long gw_ld = 0;
+};
+hipError_t launch_obs_in16(const float* obs, unsigned short* x, int obs_dim, int B, hipStream_t st);
+hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* src, int src_rows, const FwdEpi16& epi,
+                         float* part, int T, hipStream_t st);
+hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
+                         long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st);
+hipError_t launch_logits16(const unsigned short* hK, int rows, const int* dn, int n_dn, const float* ow, const float* ob,
+                           int n_act, float* logits, int B, hipStream_t st);
+hipError_t launch_readout_bwd_h16(const float* dl, const float* ow, const int* dn_inv, int n_dn, int n_act, int rows,
+                                  const BwdEpi16& epi, int B, hipStream_t st);
+hipError_t launch_readout_bwd_w16(const float* dl, const unsigned short* hK, int rows, const int* dn, int n_dn,
+                                  int n_act, float* gow_part, float* gob_part, int B, hipStream_t st);
+hipError_t launch_export16(const unsigned short* src, int rows, float* dst, int B, hipStream_t st);
+
 // KL(teacher || student) per sample (flyguy_train.cu:104-123): dl [B][n_act]; stats {KL sum, agreements} set, or
 // added to when accumulate
 hipError_t launch_loss(const float* lg, const float* tl, float* dl, float* stats_part, float* stats, int n_act, int B,

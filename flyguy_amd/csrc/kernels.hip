@@ -163,8 +163,9 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     float pg;
     if constexpr (MODE == 1) {
         // sum over the tile of g * z without z: where h > 0, z = (h + softplus(theta)) / gain, and elsewhere g = 0,
-        // so the sum is (sum g h + softplus(theta) sum g) / gain
-        pg = (gsum8(dot4(g, hv)) + in.sp * ps) / gn;
+        // so the sum is (sum g h + softplus(theta) sum g) / gain.  A neuron of gain 0 never fires (h = relu(-sp)):
+        // its g and so its sum are 0
+        pg = gn != 0.f ? (gsum8(dot4(g, hv)) + in.sp * ps) / gn : 0.f;
     } else {
         pg = gsum8(dot4(g, in.z));              // the sensory layer keeps its pre-activation (the drive)
     }

@@ -121,6 +121,10 @@ static bool put_dev(Core& c, float* d, const std::vector<float>& v) {
 
 // ================================================================================================ survey
 static bool ensure_survey(Core& c) {
+    if (c.prec) {
+        set_error("surveys need a float32 core");
+        return false;
+    }
     if (c.scnt) return true;
     c.scnt = dalloc<int>(c, (size_t)c.rows_total);
     c.ssq = dalloc<float>(c, (size_t)c.rows_total);

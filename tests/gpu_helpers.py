@@ -25,12 +25,12 @@ def say(*a):
 class Core:
     """One library handle (fc_create_from_memory) with the seven weight arrays set from numpy."""
 
-    def __init__(self, s: dict, params: list[np.ndarray], max_batch: int):
+    def __init__(self, s: dict, params: list[np.ndarray], max_batch: int, flags: int = 0):
         raw = net_bytes(s)
         self.s = s
-        self.h = lib().fc_create_from_memory(raw, len(raw), max_batch)
+        self.h = lib().fc_create_ex(raw, len(raw), max_batch, flags)
         if not self.h:
-            call("fc_create_from_memory")
+            call("fc_create_ex")
         self.sizes = param_sizes(s)
         self.set(0, params)
         self.set(1, params)

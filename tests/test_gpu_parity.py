@@ -77,6 +77,19 @@ def test_toy_forward_backward(gpu_lib, name, hops, fan):
     check_backward(core, o64, s, got)
 
 
+def test_zero_gain_neurons(gpu_lib):
+    """Neurons of gain 0 never fire; their gain gradient is 0 (the reference sums g * z = 0), not 0 / 0."""
+    say("toy a, 3 hops, fan 5, a tenth of the neurons at gain 0")
+    s, params = toy_net("a", 3, 5, seed=5)
+    rng = np.random.default_rng(5)
+    ids = np.unique(np.concatenate([np.asarray(h["nid"]) for h in s["hop"]] + [np.asarray(s["n0"])]))
+    params[1][rng.choice(ids, max(3, len(ids) // 10), replace=False)] = 0.0
+    obs = rng.standard_normal((64, 517)).astype(np.float32)
+    core, o64, got, _ = check_forward(s, params, obs)
+    check_backward(core, o64, s, got)
+    assert all(np.isfinite(g).all() for g in core.get(4))
+
+
 @pytest.mark.parametrize("B", [32, 96, 256])
 def test_scaled_synthetic(gpu_lib, B):
     """The 3-hop shape at 1/16 size: heavy rows split over several waves, re-drive rows, B not a multiple of 256."""
