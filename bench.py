@@ -2,7 +2,7 @@
 """Benchmark of the fly actor's batched inference and teaching step on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096]
-                    [--no-cpu] [--trainer-steps 60]
+                    [--no-cpu] [--trainer-steps 60] [--config5-steps 10]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -14,6 +14,8 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
            stream over the timed region), against 8 TB/s;
   cpu_baseline: the reference's own CPU forward (fly_infer.cpp, compiled into oracle/_ref) on a bounded sample of
            the same network, one core; train: the oracle's float32 restatement on a small batch.
+  config5: the bfloat16-state core at B = 16384 (forward and teaching step) on the same network and on its
+           Erdos-Renyi control;
   trainer: samples / s of the teaching trainer's own loop (flyguy_amd/flyguy_train, run as a child process on
            synthetic binary16 FLYD chunks of the same network: draw, gather, step, as its log reports them) at
            B = 4096 and at the reference trainer's default B = 512.
@@ -133,6 +135,64 @@ def trainer_leg(s, params, batches, steps: int) -> dict:
     return out
 
 
+def config5_leg(steps: int, warmup: int, B: int = 16384) -> dict:
+    """The bfloat16-state core (fc_create_ex, FC_STATES_BF16) at B = 16384 on the synthetic network and on its
+    Erdos-Renyi control (uniform in-degrees, same counts): forward decisions/s and teaching-step samples/s."""
+    import numpy as np
+    import torch
+    from flyguy_amd._lib import call, lib, profile_read
+    from flyguy_amd.export import net_bytes
+    from flyguy_amd.synth import synth_3hop
+
+    out = {}
+    dev = torch.device("cuda:0")
+    for kind in ("lognormal", "er"):
+        s, params = synth_3hop(kind=kind)
+        raw = net_bytes(s)
+        core = lib().fc_create_ex(raw, len(raw), B, 1)
+        if not core:
+            call("fc_create_ex")
+        tens = [torch.as_tensor(p).to(dev).contiguous() for p in params]
+        ptrs = (ctypes.c_void_p * 7)(*[t.data_ptr() for t in tens])
+        call("fc_copy", core, 0, 1, ptrs)
+        call("fc_copy", core, 1, 1, ptrs)
+        g = torch.Generator(device=dev).manual_seed(0)
+        obs = torch.randn(B, s["obs_dim"], device=dev, generator=g)
+        teacher = torch.randn(B, s["n_act"], device=dev, generator=g) * 2.0
+        logits = torch.empty(B, s["n_act"], device=dev)
+        stats = torch.zeros(2, device=dev)
+        ab = algorithmic_bytes(s, B, 2)
+        res = {}
+        for what, fn in (("forward", lambda: call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)),
+                         ("train", lambda: call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4,
+                                                3e-5, 1e-4, 0.0, 0.999, stats.data_ptr()))):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            call("fc_profile", core, 1)
+            profile_read(core, reset=True)
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            t = (time.perf_counter() - t0) / steps
+            prof = profile_read(core, reset=True)
+            call("fc_profile", core, 0)
+            byts = ab["infer" if what == "forward" else "train"]
+            res[what] = {"value": round(B / t, 1), "unit": "decisions/s" if what == "forward" else "samples/s",
+                         "ms_per_step": round(1e3 * t, 4), "whole_batch_frac": round(byts / t / PEAK_HBM, 4),
+                         "algorithmic_bytes": byts,
+                         "stages_ms": {k: round(v[0] / v[1], 4) for k, v in prof.items()}}
+        assert torch.isfinite(logits).all() and np.isfinite(float(stats[0]))
+        out[kind] = res
+        print(f"# bf16 B={B} {kind}: forward {res['forward']['ms_per_step']:.3f} ms ({res['forward']['value']:,.0f}/s), "
+              f"train {res['train']['ms_per_step']:.3f} ms ({res['train']['value']:,.0f}/s)", file=sys.stderr, flush=True)
+        lib().fc_free(core)
+        del tens, obs, teacher, logits
+        torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -143,6 +203,7 @@ def main() -> int:
     ap.add_argument("--cpu-train-batch", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--trainer-steps", type=int, default=60, help="teaching-trainer loop steps at B=4096 (0: skip)")
+    ap.add_argument("--config5-steps", type=int, default=10, help="timed bfloat16 B=16384 batches and steps (0: skip)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 copies of 1 GiB (read 1 GiB, write 1 GiB each) so a counter run can scale "
                          "FETCH_SIZE / WRITE_SIZE by what they read for a copy of known size")
@@ -248,6 +309,11 @@ def main() -> int:
         cpu_f, cpu_t = cpu_baselines(s, params, args.cpu_sample, args.cpu_train_batch)
     L.fc_free(core)
     core = None
+    config5 = None
+    if args.config5_steps > 0:
+        config5 = config5_leg(args.config5_steps, W)
+        config5["workload"] = ("bfloat16 states (x, drive, every layer's h, gathered gz), float32 sums, gradients and "
+                               "Adam; B=16384; the synthetic network (lognormal in-degree) and its Erdos-Renyi control")
     trainer = None
     if args.trainer_steps > 0:
         trainer = trainer_leg(s, params, (4096, 512), args.trainer_steps)
@@ -284,6 +350,7 @@ def main() -> int:
                                "whole_step_algorithmic_bytes": ab["train"]},
                   "cpu_baseline": cpu_t},
         "trainer": trainer,
+        "config5": config5,
         "stages_ms": {"forward": {k: round(v[0] / v[1], 4) for k, v in prof_fwd.items()},
                       "train": {k: round(v[0] / v[1], 4) for k, v in prof_train.items()}},
     }
