@@ -2,7 +2,7 @@
 """Benchmark of the fly actor's batched inference and teaching step on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096]
-                    [--no-cpu] [--trainer-steps 60] [--config5-steps 10]
+                    [--no-cpu] [--trainer-steps 60] [--config5-steps 10] [--config4-steps 0]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -193,6 +193,53 @@ def config5_leg(steps: int, warmup: int, B: int = 16384) -> dict:
     return out
 
 
+def config4_leg(steps: int, warmup: int, B: int = 1024) -> dict:
+    """The whole-connectome case (synthetic graph of 166,700 neurons and 15,283,167 connections, indexed by FlyActor)
+    at B = 1024, float32: forward decisions/s and teaching-step samples/s."""
+    import torch
+    from flyguy_amd._lib import call, lib
+    from flyguy_amd.export import net_bytes, params_from_torch, structure
+    from flyguy_amd.fly import FlyActor
+    from flyguy_amd.synth import whole_connectome
+
+    torch.manual_seed(0)
+    f = FlyActor(whole_connectome(), 517, 90, hops=3, fan=16)
+    s = structure(f)
+    params = params_from_torch(f, s)
+    raw = net_bytes(s)
+    core = lib().fc_create_from_memory(raw, len(raw), B)
+    if not core:
+        call("fc_create_from_memory")
+    dev = torch.device("cuda:0")
+    tens = [torch.as_tensor(p).to(dev).contiguous() for p in params]
+    ptrs = (ctypes.c_void_p * 7)(*[t.data_ptr() for t in tens])
+    call("fc_copy", core, 0, 1, ptrs)
+    call("fc_copy", core, 1, 1, ptrs)
+    g = torch.Generator(device=dev).manual_seed(0)
+    obs = torch.randn(B, s["obs_dim"], device=dev, generator=g)
+    teacher = torch.randn(B, s["n_act"], device=dev, generator=g) * 2.0
+    logits = torch.empty(B, s["n_act"], device=dev)
+    stats = torch.zeros(2, device=dev)
+    res = {"hop_connections": [len(h["col"]) for h in s["hop"]], "strengths": s["n_w"], "batch": B}
+    for what, fn in (("forward", lambda: call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)),
+                     ("train", lambda: call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4,
+                                            3e-5, 1e-4, 0.0, 0.999, stats.data_ptr()))):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        t = (time.perf_counter() - t0) / steps
+        res[what] = {"value": round(B / t, 1), "unit": "decisions/s" if what == "forward" else "samples/s",
+                     "ms_per_step": round(1e3 * t, 4)}
+    print(f"# whole connectome B={B}: forward {res['forward']['ms_per_step']:.3f} ms, train "
+          f"{res['train']['ms_per_step']:.3f} ms", file=sys.stderr, flush=True)
+    lib().fc_free(core)
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -204,6 +251,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--trainer-steps", type=int, default=60, help="teaching-trainer loop steps at B=4096 (0: skip)")
     ap.add_argument("--config5-steps", type=int, default=10, help="timed bfloat16 B=16384 batches and steps (0: skip)")
+    ap.add_argument("--config4-steps", type=int, default=0,
+                    help="timed whole-connectome B=1024 batches and steps (0: skip; its index build takes ~20 s)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 copies of 1 GiB (read 1 GiB, write 1 GiB each) so a counter run can scale "
                          "FETCH_SIZE / WRITE_SIZE by what they read for a copy of known size")
@@ -314,6 +363,7 @@ def main() -> int:
         config5 = config5_leg(args.config5_steps, W)
         config5["workload"] = ("bfloat16 states (x, drive, every layer's h, gathered gz), float32 sums, gradients and "
                                "Adam; B=16384; the synthetic network (lognormal in-degree) and its Erdos-Renyi control")
+    config4 = config4_leg(args.config4_steps, W) if args.config4_steps > 0 else None
     trainer = None
     if args.trainer_steps > 0:
         trainer = trainer_leg(s, params, (4096, 512), args.trainer_steps)
@@ -351,6 +401,7 @@ def main() -> int:
                   "cpu_baseline": cpu_t},
         "trainer": trainer,
         "config5": config5,
+        "config4": config4,
         "stages_ms": {"forward": {k: round(v[0] / v[1], 4) for k, v in prof_fwd.items()},
                       "train": {k: round(v[0] / v[1], 4) for k, v in prof_train.items()}},
     }

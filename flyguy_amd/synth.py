@@ -53,6 +53,21 @@ def _unique_sources(rng, d: np.ndarray, n_src: int) -> tuple[np.ndarray, np.ndar
         col[dup] = rng.integers(0, n_src, len(dup), dtype=np.int64)
 
 
+def _unique_sources_large(rng, d: np.ndarray, n_src: int) -> tuple[np.ndarray, np.ndarray]:
+    """_unique_sources for large graphs: one sort of (row, source) keys, then only the rows that still hold a repeated
+    source are redrawn and re-sorted."""
+    row = np.repeat(np.arange(len(d), dtype=np.int64), d)
+    key = row * n_src + rng.integers(0, n_src, len(row), dtype=np.int64)
+    key.sort()
+    while True:
+        dup = np.flatnonzero(key[1:] == key[:-1]) + 1
+        if len(dup) == 0:
+            return row, key - row * n_src
+        key[dup] = row[dup] * n_src + rng.integers(0, n_src, len(dup), dtype=np.int64)
+        sel = np.flatnonzero(np.isin(row, np.unique(row[dup])))      # whole rows, contiguous and in row order
+        key[sel] = np.sort(key[sel])
+
+
 def synth_3hop(sizes=SHAPE_3HOP["sizes"], edges=SHAPE_3HOP["edges"], redrive=SHAPE_3HOP["redrive"],
                obs_dim: int = 517, n_act: int = 90, fan: int = 16, sigma: float = 1.5, kind: str = "lognormal",
                seed: int = 1000) -> tuple[dict, list[np.ndarray]]:
@@ -106,6 +121,31 @@ def synth_3hop(sizes=SHAPE_3HOP["sizes"], edges=SHAPE_3HOP["edges"], redrive=SHA
               (rng.standard_normal(n_act * sizes[K]) / np.sqrt(sizes[K])).astype(np.float32),
               np.zeros(n_act, np.float32)]
     return s, params
+
+
+WHOLE = dict(neurons=166_700, connections=15_283_167, sensory=16_894, descending=1_332)
+TRANSMITTERS = ("acetylcholine", "gaba", "glutamate", "dopamine", "serotonin", "octopamine", "histamine")
+
+
+def whole_connectome(neurons: int = WHOLE["neurons"], connections: int = WHOLE["connections"],
+                     sensory: int = WHOLE["sensory"], descending: int = WHOLE["descending"], sigma: float = 1.8,
+                     seed: int = 4) -> dict:
+    """A synthetic graph file of the whole-connectome shape (the arrays FlyActor reads: body, pre, post, syn, nt,
+    sensory, descending): in-degrees LogNormal(0, sigma) scaled to the connection count, sources uniform without
+    repetition, connections in random order, synapse counts 1..20, transmitters drawn per neuron (a third
+    inhibitory), disjoint random sensory and descending sets.  FlyActor then keeps, per hop, the connections that
+    can carry the signal (its pruning, fly.py:91-121)."""
+    rng = np.random.default_rng(seed)
+    d = _degrees(rng, neurons, connections, neurons, sigma, "lognormal")
+    post, pre = _unique_sources_large(rng, d, neurons)
+    perm = rng.permutation(connections)
+    ids = rng.permutation(neurons)
+    return {"body": np.arange(neurons, dtype=np.int64), "pre": pre[perm].astype(np.int32),
+            "post": post[perm].astype(np.int32), "syn": rng.integers(1, 21, connections).astype(np.int32),
+            "nt": np.asarray(TRANSMITTERS)[rng.choice(len(TRANSMITTERS), neurons,
+                                                      p=[0.5, 0.15, 0.12, 0.06, 0.06, 0.05, 0.06])],
+            "sensory": np.sort(ids[:sensory]).astype(np.int32),
+            "descending": np.sort(ids[sensory:sensory + descending]).astype(np.int32)}
 
 
 def scaled_3hop(div: int, **kw) -> tuple[dict, list[np.ndarray]]:

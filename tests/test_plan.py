@@ -79,3 +79,18 @@ def test_plan_synthetic_graph():
 
 def test_seg_cap():
     assert seg_cap(0) == 16 and seg_cap(1_200_000) == 147 and seg_cap(1_500_000) == 184 and seg_cap(10 ** 9) == 256
+
+
+def test_whole_connectome_generator_small():
+    """The whole-connectome generator at a small size: the counts asked for, no repeated (pre, post) pair, disjoint
+    sensory and descending sets, and a graph FlyActor indexes."""
+    from flyguy_amd.fly import FlyActor
+    from flyguy_amd.synth import whole_connectome
+    g = whole_connectome(neurons=3000, connections=90_000, sensory=400, descending=60, seed=1)
+    assert len(g["pre"]) == 90_000 and len(g["body"]) == 3000
+    key = g["pre"].astype(np.int64) * 3000 + g["post"]
+    assert len(np.unique(key)) == len(key)
+    assert not set(g["sensory"].tolist()) & set(g["descending"].tolist())
+    assert not np.all(np.diff(g["post"]) >= 0)                      # connections in random order
+    f = FlyActor(g, 517, 90, hops=3, fan=16)
+    assert f.sizes[0] == 400 and 0 < f.sizes[3] <= 60
