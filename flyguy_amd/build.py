@@ -18,9 +18,10 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libflyguy_core.so"
 EXE = PKG / "flyguy_train"
+CPU_LIB = PKG / "libfly_infer.so"          # decisions on the host CPU (include/fly_infer.h): no HIP
 SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "core16.hip", "hop_api.hip", "half.hip", "train.hip")]
 HEADERS = [PKG / "csrc" / n for n in ("common.h", "kernels.h", "device.h", "core.h", "half.h")] + \
-    [ROOT / "include" / "flyguy_core.h", ROOT / "include" / "flyguy_train.h"]
+    [ROOT / "include" / "flyguy_core.h", ROOT / "include" / "flyguy_train.h", ROOT / "include" / "fly_infer.h"]
 ARCH = os.environ.get("FLYGUY_OFFLOAD_ARCH", "gfx950")
 
 
@@ -66,6 +67,14 @@ def build(verbose: bool = False) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, EXE)
+    tmp = CPU_LIB.with_suffix(".so.tmp")
+    # float32 sums as written: no multiply-add contraction
+    cmd = ["g++", "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall", "-ffp-contract=off", str(PKG / "csrc" / "infer_cpu.cpp"),
+           "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, CPU_LIB)
     return LIB
 
 

@@ -21,6 +21,7 @@ NativeFlyActor (flyguy_amd.fly_native) runs the whole network, its backward and 
 from __future__ import annotations
 
 from collections.abc import Mapping
+import struct
 from pathlib import Path
 
 import numpy as np
@@ -220,9 +221,77 @@ class FlyActor(nn.Module):
             h = torch.relu(self.gain[rows][:, None] * z - thr[rows][:, None])
         return self.out(h[self.dn_rows].t())
 
+    def _native(self):
+        """The CPU decision library (flyguy_amd/libfly_infer.so, include/fly_infer.h: a hop pushes only the neurons
+        that fire), set up from the current weights (fly.py:186-241).  None when it is not built or FLYGUY_NATIVE=0:
+        then the sparse products below play."""
+        ver = (self.w._version, self.in_w._version, self.gain._version, self.theta._version, self.in_b._version,
+               self.out.weight._version, self.out.bias._version, self.w.dtype)
+        nat = getattr(self, "_nat", None)
+        if nat is not None and nat["ver"] == ver:
+            return nat if nat["h"] else None
+        import ctypes
+        import os
+        if nat is not None and nat["h"]:
+            nat["lib"].fly_free(nat["h"])
+        nat = {"ver": ver, "h": None}
+        self._nat = nat
+        path = Path(__file__).resolve().parent / "libfly_infer.so"
+        if os.environ.get("FLYGUY_NATIVE", "1") == "0" or not path.exists() or self.w.dtype != torch.float32:
+            return None
+        lib = ctypes.CDLL(str(path))
+        vp, ci = ctypes.c_void_p, ctypes.c_int
+        lib.fly_create.restype, lib.fly_create.argtypes = vp, [ci, ci, ci]
+        lib.fly_set_plug.restype, lib.fly_set_plug.argtypes = None, [vp, ci, ci] + [vp] * 6
+        lib.fly_set_hop.restype, lib.fly_set_hop.argtypes = None, [vp, ci, ci, ci, ci] + [vp] * 6
+        lib.fly_set_out.restype, lib.fly_set_out.argtypes = None, [vp, ci, vp, vp, vp]
+        lib.fly_forward.restype, lib.fly_forward.argtypes = None, [vp, vp, ci, vp, vp]
+        lib.fly_free.restype, lib.fly_free.argtypes = None, [vp]
+        keep = []                      # the arrays handed over (the library copies them; kept until set-up ends)
+
+        def arr(t, dt):
+            a = np.ascontiguousarray(t.detach().cpu().numpy() if torch.is_tensor(t) else t, dtype=dt)
+            keep.append(a)
+            return a.ctypes.data_as(vp)
+        with torch.no_grad():
+            thr = nn.functional.softplus(self.theta)
+            h = lib.fly_create(self.obs_dim, self.out.out_features, self.hops)
+            lib.fly_set_plug(h, self.sizes[0], int(self.in_ci.numel()), arr(self.in_crow, np.int32),
+                             arr(self.in_ci, np.int32), arr(self.in_w, np.float32), arr(self.in_b, np.float32),
+                             arr(self.gain[self.n0], np.float32), arr(thr[self.n0], np.float32))
+            for k in range(1, self.hops + 1):
+                rows = getattr(self, f"n{k}")
+                drow = np.full(len(rows), -1, np.int32)
+                drow[getattr(self, f"s{k}").cpu().numpy()] = getattr(self, f"d{k}").cpu().numpy()
+                w_by_src = self.w[getattr(self, f"e{k}")[getattr(self, f"tperm{k}")]]
+                lib.fly_set_hop(h, k - 1, len(rows), self.sizes[k - 1], int(w_by_src.numel()),
+                                arr(getattr(self, f"tcrow{k}"), np.int32), arr(getattr(self, f"tci{k}"), np.int32),
+                                arr(w_by_src, np.float32), arr(self.gain[rows], np.float32), arr(thr[rows], np.float32),
+                                arr(drow, np.int32))
+            lib.fly_set_out(h, len(self.dn_rows), arr(self.dn_rows, np.int32), arr(self.out.weight, np.float32),
+                            arr(self.out.bias, np.float32))
+        nat.update(h=h, lib=lib, shade=np.zeros(int(sum(self.sizes)), np.uint8))
+        return nat
+
+    def _forward_native(self, obs: torch.Tensor, nat: dict) -> torch.Tensor:
+        import ctypes
+        x = np.ascontiguousarray(obs.detach().numpy(), dtype=np.float32)
+        out = np.empty((x.shape[0], self.out.out_features), np.float32)
+        tap = getattr(self, "tap", None)             # the visualizer: every neuron's firing for the first car
+        vp = ctypes.c_void_p
+        nat["lib"].fly_forward(nat["h"], x.ctypes.data_as(vp), x.shape[0], out.ctypes.data_as(vp),
+                               nat["shade"].ctypes.data_as(vp) if tap is not None else None)
+        if tap is not None:
+            tap(nat["shade"])
+        return torch.from_numpy(out)
+
     @torch.no_grad()
     def _forward_cpu(self, obs: torch.Tensor) -> torch.Tensor:
-        """Playing on the CPU: sparse CSR products built once from the current weights (fly.py:252-284)."""
+        """Playing on the CPU (fly.py:252-284): the CPU decision library when it is built, else sparse CSR products
+        built once from the current weights."""
+        nat = self._native()
+        if nat is not None:
+            return self._forward_native(obs, nat)
         ver = (self.w._version, self.in_w._version, self.gain._version, self.theta._version, self.in_b._version)
         c = getattr(self, "_cpu", None)
         if c is None or c["ver"] != ver:
@@ -240,11 +309,17 @@ class FlyActor(nn.Module):
             self._cpu = c
         drive = torch.sparse.mm(c["a_in"], obs.t().contiguous()) + self.in_b[:, None]
         h = torch.relu(c["g0"] * drive - c["t0"])
+        tap = getattr(self, "tap", None)             # the visualizer: every layer's firing for the first car
+        acts = [h[:, 0]] if tap is not None else None
         for a, g, t, s_, d_ in c["hop"]:
             z = torch.sparse.mm(a, h)
             if len(s_):
                 z[s_] += drive[d_]
             h = torch.relu(g * z - t)
+            if acts is not None:
+                acts.append(h[:, 0])
+        if tap is not None:
+            tap(acts)
         return self.out(h[self.dn_rows].t())
 
     def forward(self, obs: torch.Tensor, extra: torch.Tensor | None = None) -> torch.Tensor:
@@ -265,3 +340,67 @@ class FlyActor(nn.Module):
                 z = z.index_add(1, s_, drive[:, getattr(self, f"d{k}")])
             h = torch.relu(self.gain[rows] * z - thr[rows])
         return self.out(h[:, self.dn_rows])
+
+
+class VizTap:
+    """The visualizer's window into a playing actor (fly.py:308-368): after every decision the firing of every neuron
+    in play, layer by layer, goes into a small shared file, one byte a neuron, with the chosen action; a reader
+    (the visualizer's server) maps the file, nothing waits for it.  Set `actor.tap = VizTap(actor.sizes)`.
+
+    File (little endian): "FLYV", version 1 (u32), seq (u32, odd while being written) at 8, tick (u32) at 12, time
+    (f64) at 16, action (i32) at 24, 8 controls (f32) at 28, layer count and 4 layer sizes (u32) at 60, 90 action
+    probabilities (f32) at 80, match clock (f32), frame (u32), overtime (i32) at 440; the firing bytes from 512,
+    the layers one after another (sensory first), 255 * tanh(1.5 * firing)."""
+
+    HEADER = 512
+
+    def __init__(self, sizes, path=None):
+        import mmap
+        import tempfile
+        self.sizes = [int(v) for v in sizes]
+        self.path = Path(path) if path else Path(tempfile.gettempdir()) / "flyguy_viz.bin"
+        total = self.HEADER + sum(self.sizes)
+        if not (self.path.exists() and self.path.stat().st_size == total):   # a file of the right size is reused
+            with open(self.path, "wb") as fh:
+                fh.write(bytes(total))
+        self.fh = open(self.path, "r+b")
+        self.mm = mmap.mmap(self.fh.fileno(), total)
+        self.mm[0:8] = b"FLYV" + struct.pack("<I", 1)
+        self.mm[60:80] = struct.pack("<5I", len(self.sizes), *(self.sizes + [0] * 4)[:4])
+        self.seq = 0
+        self.tick = 0
+        self.acts = None
+
+    def __call__(self, acts) -> None:
+        """From the actor's forward pass: the first car's firing (a uint8 array from the CPU library, or one tensor
+        per layer from the sparse products)."""
+        self.acts = acts
+
+    def publish(self, action: int, controls, probs, clock: float = -1.0, frame: int = 0, overtime: bool = False) -> None:
+        import time
+        if self.acts is None:
+            return
+        self.mm[440:452] = struct.pack("<fIi", float(clock), int(frame) & 0xFFFFFFFF, int(bool(overtime)))
+        self.seq += 1
+        self.mm[8:12] = struct.pack("<I", self.seq)
+        at = self.HEADER
+        if isinstance(self.acts, np.ndarray):
+            b = self.acts.astype(np.uint8).tobytes()
+            self.mm[at:at + len(b)] = b
+        else:
+            for a in self.acts:
+                b = (torch.tanh(a.float() * 1.5) * 255.0).to(torch.uint8).cpu().numpy().tobytes()
+                self.mm[at:at + len(b)] = b
+                at += len(b)
+        self.tick += 1
+        self.mm[12:28] = struct.pack("<Idi", self.tick, time.time(), int(action))
+        self.mm[28:60] = np.asarray(controls, np.float32)[:8].tobytes()
+        p = np.asarray(probs, np.float32)[:90]
+        self.mm[80:80 + 4 * len(p)] = p.tobytes()
+        self.seq += 1
+        self.mm[8:12] = struct.pack("<I", self.seq)
+        self.acts = None
+
+    def close(self) -> None:
+        self.mm.close()
+        self.fh.close()

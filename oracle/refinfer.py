@@ -28,8 +28,8 @@ def _softplus(x: np.ndarray) -> np.ndarray:
 class RefInfer:
     """The reference's CPU forward on a library structure dict + the seven weight arrays."""
 
-    def __init__(self, s: dict, params: list[np.ndarray]):
-        L = ctypes.CDLL(str(LIB))
+    def __init__(self, s: dict, params: list[np.ndarray], lib_path: Path | None = None):
+        L = ctypes.CDLL(str(lib_path or LIB))
         L.fly_create.restype, L.fly_create.argtypes = vp, [ci, ci, ci]
         L.fly_set_plug.restype, L.fly_set_plug.argtypes = None, [vp, ci, ci] + [vp] * 6
         L.fly_set_hop.restype, L.fly_set_hop.argtypes = None, [vp, ci, ci, ci, ci] + [vp] * 6
@@ -64,8 +64,9 @@ class RefInfer:
         if getattr(self, "h", None):
             self.L.fly_free(self.h)
 
-    def forward(self, obs: np.ndarray) -> np.ndarray:
+    def forward(self, obs: np.ndarray, tap: np.ndarray | None = None) -> np.ndarray:
+        """logits [B][n_act]; tap (uint8, one per neuron state): the first sample's firing bytes."""
         x = np.ascontiguousarray(obs, dtype=np.float32)
         out = np.zeros((x.shape[0], self.n_act), np.float32)
-        self.L.fly_forward(self.h, x.ctypes.data, x.shape[0], out.ctypes.data, None)
+        self.L.fly_forward(self.h, x.ctypes.data, x.shape[0], out.ctypes.data, None if tap is None else tap.ctypes.data)
         return out

@@ -1,0 +1,95 @@
+"""Decisions on the host CPU (flyguy_amd/libfly_infer.so, include/fly_infer.h) and the visualizer tap.
+
+The library against the reference's own compiled CPU forward (oracle/_ref, built from fly_infer.cpp where the
+reference checkout is present): logits and firing bytes bit-identical (same float32 sums in the same order).  The
+actor's CPU play through it against the float64 oracle (<= 1e-5 of the largest logit) and against the sparse-product
+path it replaces.  The VizTap file's fields."""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import CASES, lively, toy
+from flyguy_amd.export import net_bytes, params_from_torch, structure
+from flyguy_amd.fly import FlyActor, VizTap
+from oracle import refinfer
+from oracle.oracle import Oracle
+
+OURS = FlyActor.__module__ and __import__("pathlib").Path(__import__("flyguy_amd").__file__).parent / "libfly_infer.so"
+
+
+def _actor(name, hops, fan, seed=0):
+    torch.manual_seed(seed)
+    return lively(FlyActor(toy(name), 517, 90, hops=hops, fan=fan), seed)
+
+
+@pytest.mark.skipif(not refinfer.available(), reason="the reference's CPU forward is not built here")
+@pytest.mark.parametrize("name,hops,fan", CASES)
+def test_bit_identical_to_the_reference_cpu_forward(name, hops, fan):
+    f = _actor(name, hops, fan)
+    s = structure(f)
+    P = params_from_torch(f, s)
+    obs = np.random.default_rng(1).standard_normal((16, 517)).astype(np.float32)
+    n = sum(s["sizes"])
+    tap_ref, tap_ours = np.zeros(n, np.uint8), np.zeros(n, np.uint8)
+    ref = refinfer.RefInfer(s, P).forward(obs, tap_ref)
+    ours = refinfer.RefInfer(s, P, lib_path=OURS).forward(obs, tap_ours)
+    assert np.array_equal(ours.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(tap_ours, tap_ref) and tap_ours.any()
+
+
+@pytest.mark.parametrize("name,hops,fan", [("a", 3, 5), ("b", 3, 16), ("c", 4, 6)])
+def test_actor_cpu_play(monkeypatch, name, hops, fan):
+    f = _actor(name, hops, fan)
+    s = structure(f)
+    obs = np.random.default_rng(2).standard_normal((8, 517)).astype(np.float32)
+    want = Oracle(net_bytes(s), params_from_torch(f, s), "f64").forward(obs)
+    with torch.no_grad():
+        got = f(torch.as_tensor(obs)).numpy()
+        assert f._nat["h"]                                      # the library played
+        monkeypatch.setenv("FLYGUY_NATIVE", "0")
+        f.w.mul_(1.0)                                           # (a new weight version: set-up again, now without it)
+        sparse = f(torch.as_tensor(obs)).numpy()
+        assert not f._nat["h"]
+    scale = max(1.0, np.abs(want).max())
+    assert np.abs(got - want).max() <= 1e-5 * scale
+    assert np.abs(sparse - want).max() <= 1e-5 * scale
+    # weights changed after set-up are picked up
+    monkeypatch.setenv("FLYGUY_NATIVE", "1")
+    with torch.no_grad():
+        f.out.bias.add_(1.0)
+        moved = f(torch.as_tensor(obs)).numpy()
+    assert np.allclose(moved, got + 1.0, atol=1e-5 * scale)
+
+
+def test_viz_tap(tmp_path, monkeypatch):
+    f = _actor("a", 3, 5)
+    path = tmp_path / "viz.bin"
+    tap = VizTap(f.sizes, path)
+    f.tap = tap
+    obs = torch.as_tensor(np.random.default_rng(3).standard_normal((4, 517)).astype(np.float32))
+    with torch.no_grad():
+        f(obs)                                                 # through the CPU library: bytes as they come out
+    first = np.asarray(tap.acts).copy()
+    tap.publish(7, np.arange(8, dtype=np.float32), np.full(90, 1 / 90, np.float32), clock=12.5, frame=99)
+    raw = path.read_bytes()
+    assert raw[:4] == b"FLYV" and struct.unpack("<I", raw[4:8])[0] == 1
+    seq, tick = struct.unpack("<II", raw[8:16])
+    assert seq == 2 and tick == 1 and struct.unpack("<i", raw[24:28])[0] == 7
+    assert np.array_equal(np.frombuffer(raw[28:60], np.float32), np.arange(8, dtype=np.float32))
+    assert struct.unpack("<5I", raw[60:80]) == (len(f.sizes), *(list(f.sizes) + [0] * 4)[:4])
+    assert struct.unpack("<fIi", raw[440:452]) == (12.5, 99, 0)
+    body = np.frombuffer(raw[512:], np.uint8)
+    assert len(body) == sum(f.sizes) and np.array_equal(body, first) and body.any()
+    # the sparse-product path hands over one tensor per layer; its bytes agree with the library's within one step
+    monkeypatch.setenv("FLYGUY_NATIVE", "0")
+    with torch.no_grad():
+        f.w.mul_(1.0)
+        f(obs)
+    tap.publish(3, np.zeros(8), np.zeros(90))
+    body2 = np.frombuffer(path.read_bytes()[512:], np.uint8)
+    assert np.abs(body2.astype(int) - first.astype(int)).max() <= 1
+    tap.close()
