@@ -345,9 +345,10 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     c->stats = dalloc<float>(*c, 4);
     c->red = dalloc<float>(*c, 1024);
     c->nrm = dalloc<float>(*c, 1);
+    c->owT = dalloc<float>(*c, (size_t)c->n_dn * readout_pad(c->n_act));
     if (!c->x || !c->drive || !c->h0 || !c->gdrive || !c->gz[0] || !c->gz[1] || !c->lg || !c->dl || !c->part ||
         !c->gwpart || !c->ggp0 || !c->gsp0 || !c->ginb || !c->ginw || !c->gow_p || !c->gob_p || !c->stats_part ||
-        !c->stats || !c->red || !c->nrm)
+        !c->stats || !c->red || !c->nrm || !c->owT)
         return nullptr;
     if (hipDeviceSynchronize() != hipSuccess) { set_error("device error after set-up"); return nullptr; }
     return c.release();
@@ -408,8 +409,8 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     }
     {
         Timed t(c, ST_LOGITS);
-        FG_CHECK(launch_logits(hp, tiled(c.sizes[c.hops]), c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, logits, B, st),
-                 false);
+        FG_CHECK(launch_logits_mfma(hp, false, c.sizes[c.hops], c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, c.owT,
+                                    logits, B, st), false);
     }
     c.B = B;
     return true;
@@ -533,8 +534,8 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     }
     {
         Timed t(c, ST_LOGITS);
-        FG_CHECK(launch_logits16(hp, c.sizes[c.hops], c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, logits, B, st),
-                 false);
+        FG_CHECK(launch_logits_mfma(hp, true, c.sizes[c.hops], c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, c.owT,
+                                    logits, B, st), false);
     }
     c.B = B;
     return true;

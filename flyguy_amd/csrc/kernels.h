@@ -97,6 +97,11 @@ hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, i
 hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
                       float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st);
 hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStream_t st);
+// the read-out on the matrix cores (readout.hip): owT, n_dn x readout_pad(n_act) floats of scratch for the
+// transposed weights; hK float32 tiles of 32 or (bf16_states) bfloat16 tiles of 64
+int readout_pad(int n_act);
+hipError_t launch_logits_mfma(const void* hK, bool bf16_states, int rows, const int* dn, int n_dn, const float* ow,
+                              const float* ob, int n_act, float* owT, float* logits, int B, hipStream_t st);
 hipError_t launch_logits(const float* hK, Lay lh, const int* dn, int n_dn, const float* ow, const float* ob, int n_act,
                          float* logits, int B, hipStream_t st);
 hipError_t launch_readout_bwd_h(const float* dl, const float* ow, const int* dn_inv, int n_dn, int n_act, int rows,

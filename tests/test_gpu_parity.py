@@ -3,8 +3,11 @@
 Tolerances (from the target: fp32 logits within 1e-5 relative, weight gradients within 1e-4 relative, argmax
 identical), relative to the largest entry as flyguy/native/core_check.py:59 measures:
   logits and every internal state vs the float64 oracle   <= 1e-5
-  logits vs the float32 oracle (the reference's arithmetic) <= 1e-6  (rows split over several waves are summed
-                                                                      in pieces; softplus may differ by an ulp)
+  logits vs the float32 oracle (the reference's arithmetic) <= 4e-6  (rows split over several waves are summed
+                                                                      in pieces, the read-out on the matrix cores
+                                                                      in 4 partial sums of 2-product steps rather
+                                                                      than in row order; softplus may differ by an
+                                                                      ulp)
   each of the seven gradient arrays vs the float64 oracle    <= 1e-4
   argmax identical wherever the top-2 margin exceeds 1e-4.
 """
@@ -40,7 +43,7 @@ def check_forward(s, params, obs, core=None, states=True):
     w32 = o32.forward(obs)
     assert np.isfinite(got).all()
     assert rel(got, want) <= 1e-5, rel(got, want)
-    assert rel(got, w32) <= 1e-6, rel(got, w32)
+    assert rel(got, w32) <= 4e-6, rel(got, w32)
     ok, ties = argmax_agrees(got, want)
     assert ok
     if states:
