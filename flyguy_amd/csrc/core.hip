@@ -441,8 +441,10 @@ bool backward(Core& c, const float* dlogits, int B) {
     et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
     {
         Timed t(c, ST_RBWD);
-        FG_CHECK(launch_readout_bwd_h(dlogits, c.arr(SET_P, 5), c.dn_inv, c.n_dn, c.n_act, top.rows, et, B, st), false);
-        FG_CHECK(launch_readout_bwd_w(dlogits, top.h, tiled(top.rows), c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st), false);
+        FG_CHECK(launch_owT(c.arr(SET_P, 5), c.n_act, c.n_dn, c.owT, st), false);
+        FG_CHECK(launch_readout_bwd_h_mfma(dlogits, c.owT, c.dn_inv, c.n_act, top.rows, et, B, st), false);
+        FG_CHECK(launch_readout_bwd_w_mfma(dlogits, top.h, false, top.rows, c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st),
+                 false);
     }
     const int nch = readout_chunks(B);
     {
@@ -566,8 +568,10 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
     {
         Timed t(c, ST_RBWD);
-        FG_CHECK(launch_readout_bwd_h16(dlogits, c.arr(SET_P, 5), c.dn_inv, c.n_dn, c.n_act, top.rows, et, B, st), false);
-        FG_CHECK(launch_readout_bwd_w16(dlogits, s16(top.h), top.rows, c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st), false);
+        FG_CHECK(launch_owT(c.arr(SET_P, 5), c.n_act, c.n_dn, c.owT, st), false);
+        FG_CHECK(launch_readout_bwd_h16_mfma(dlogits, c.owT, c.dn_inv, c.n_act, top.rows, et, B, st), false);
+        FG_CHECK(launch_readout_bwd_w_mfma(dlogits, top.h, true, top.rows, c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st),
+                 false);
     }
     const int nch = readout_chunks(B);
     {

@@ -11,6 +11,7 @@
 // gradient collects the hops' gz before their rounding.  Float32 tensors beside them (partials, the drive's gradient)
 // use the same tiling, [T][rows][64] floats.
 #include "half.h"
+#include "readout.h"
 
 namespace fg {
 
@@ -337,122 +338,23 @@ __global__ __launch_bounds__(WG) void k_obs_in16(const float* __restrict__ obs, 
     }
 }
 
-// logits[b][a] = ob[a] + sum_j ow[a][j] * hK[dn[j]][b] in j order (as k_logits); one workgroup per (tile, 32 actions)
-constexpr int LG_J16 = 32;
-__global__ __launch_bounds__(WG) void k_logits16(const bf16_t* __restrict__ hK, int rows, const int* __restrict__ dn,
-                                                 int n_dn, const float* __restrict__ ow, const float* __restrict__ ob,
-                                                 int n_act, float* __restrict__ logits) {
-    __shared__ float hs[LG_J16][TW16];
-    __shared__ float ws[RPG][LG_J16 + 1];
-    const int tile = blockIdx.x, a0 = blockIdx.y * RPG;
-    const int g = threadIdx.x >> 3, sub = threadIdx.x & 7, a = a0 + g;
-    const float b0 = a < n_act ? ob[a] : 0.f;
-    float acc[8] = {b0, b0, b0, b0, b0, b0, b0, b0};
-    for (int j0 = 0; j0 < n_dn; j0 += LG_J16) {
-        const int nj = min(LG_J16, n_dn - j0);
-        __syncthreads();
-        for (int i = threadIdx.x; i < LG_J16 * LPR; i += WG) {
-            const int jj = i / LPR, qq = i % LPR;
-            float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (jj < nj) ld8(hK, rows, tile, dn[j0 + jj], qq, f);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) hs[jj][qq * 8 + k] = f[k];
-        }
-        for (int i = threadIdx.x; i < RPG * LG_J16; i += WG) {
-            const int aa = i / LG_J16, jj = i % LG_J16;
-            ws[aa][jj] = (jj < nj && a0 + aa < n_act) ? ow[(size_t)(a0 + aa) * n_dn + j0 + jj] : 0.f;
-        }
-        __syncthreads();
-        for (int jj = 0; jj < nj; ++jj) {
-            const float wv = ws[g][jj];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc[k] = fmaf(wv, hs[jj][sub * 8 + k], acc[k]);
-        }
-    }
-    if (a >= n_act) return;
-    float* o = logits + (size_t)(tile * TW16 + sub * 8) * n_act + a;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) o[(size_t)k * n_act] = acc[k];
-}
-
-// gh of the top layer from the logits' gradient, then its neuron backward (as k_readout_bwd_h)
-__global__ __launch_bounds__(WG) void k_rbwd_h16(const float* __restrict__ dl, const float* __restrict__ ow,
-                                                 const int* __restrict__ dn_inv, int n_dn, int n_act, int rows,
-                                                 BwdEpi16 epi) {
-    extern __shared__ float sm[];
-    float* dlT = sm;                         // [n_act][64]
-    float* owc = sm + (size_t)n_act * TW16;  // [32][n_act]
+// gh of the top layer from the logits' gradient on the matrix cores (readout.h): 32 rows x the tile's 64 samples
+// (two 32-sample blocks), then its neuron backward
+__global__ __launch_bounds__(WG) void k_rbwd_h16_mfma(const float* __restrict__ dl, const float* __restrict__ owT, int ma,
+                                                      const int* __restrict__ dn_inv, int n_act, int rows, BwdEpi16 epi) {
+    __shared__ float part[4 * 32 * 33];
+    __shared__ float gh[32 * 65];
     const int tile = blockIdx.y, r0 = blockIdx.x * RPG;
-    for (int i = threadIdx.x; i < n_act * TW16; i += WG) {
-        const int c = i / n_act, a = i % n_act;
-        dlT[a * TW16 + c] = dl[(size_t)(tile * TW16 + c) * n_act + a];
-    }
-    for (int i = threadIdx.x; i < RPG * n_act; i += WG) {
-        const int r = i / n_act, a = i % n_act, t = r0 + r;
-        const int j = t < rows ? dn_inv[t] : -1;
-        owc[r * n_act + a] = j >= 0 ? ow[(size_t)a * n_dn + j] : 0.f;
-    }
-    __syncthreads();
+    readout_gh_block(dl, owT, ma, dn_inv, rows, n_act, r0, tile * TW16, part, gh, 65);
+    readout_gh_block(dl, owT, ma, dn_inv, rows, n_act, r0, tile * TW16 + 32, part, gh + 32, 65);
     const int r = threadIdx.x >> 3, sub = threadIdx.x & 7, t = r0 + r;
     if (t >= rows) return;                   // whole 8-lane groups
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (dn_inv[t] >= 0)
-        for (int a = 0; a < n_act; ++a) {
-            const float wv = owc[r * n_act + a];
-            const float* d = dlT + a * TW16 + sub * 8;
+    float acc[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) acc[k] = fmaf(wv, d[k], acc[k]);
-        }
+    for (int k = 0; k < 8; ++k) acc[k] = gh[r * 65 + sub * 8 + k];
     BwdIn16 in{};
     bwd_inputs16<1>(epi, t, epi.drow ? epi.drow[t] : -1, tile, sub, in);
     bwd_finish16<1>(epi, t, tile, sub, acc, in);
-}
-
-// per chunk of 8 tiles (512 samples): gow[a][j] partial = sum_b dl[b][a] * hK[dn[j]][b], gob[a] partial = sum_b dl[b][a]
-constexpr int RO_CHUNK16 = 8;
-__global__ __launch_bounds__(WG) void k_rbwd_w16(const float* __restrict__ dl, const bf16_t* __restrict__ hK, int rows,
-                                                 const int* __restrict__ dn, int n_dn, int n_act, int T,
-                                                 float* __restrict__ gow_part, float* __restrict__ gob_part) {
-    __shared__ float hT[32][TW16 + 1];
-    __shared__ float ds[TW16][97];
-    const int j0 = blockIdx.x * 32, chunk = blockIdx.y;
-    const int jj = threadIdx.x & 31, ag = threadIdx.x >> 5;
-    const int t0 = chunk * RO_CHUNK16, t1 = min(T, t0 + RO_CHUNK16);
-    for (int a0 = 0; a0 < n_act; a0 += 96) {
-        float acc[12];
-        float accb = 0.f;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) acc[i] = 0.f;
-        for (int tile = t0; tile < t1; ++tile) {
-            __syncthreads();
-            for (int i = threadIdx.x; i < 32 * TW16; i += WG) {
-                const int j = i / TW16, c = i % TW16;
-                hT[j][c] = (j0 + j < n_dn)
-                               ? __uint_as_float((unsigned)hK[((size_t)tile * rows + dn[j0 + j]) * TW16 + c] << 16)
-                               : 0.f;
-            }
-            for (int i = threadIdx.x; i < TW16 * 96; i += WG) {
-                const int c = i / 96, a = i % 96;
-                ds[c][a] = (a0 + a < n_act) ? dl[(size_t)(tile * TW16 + c) * n_act + a0 + a] : 0.f;
-            }
-            __syncthreads();
-            for (int c = 0; c < TW16; ++c) {
-                const float hv = hT[jj][c];
-#pragma unroll
-                for (int i = 0; i < 12; ++i) acc[i] = fmaf(ds[c][ag + 8 * i], hv, acc[i]);
-            }
-            if (blockIdx.x == 0 && threadIdx.x < 96)
-                for (int c = 0; c < TW16; ++c) accb += ds[c][threadIdx.x];
-        }
-        const size_t base = (size_t)chunk * n_act * n_dn;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) {
-            const int a = a0 + ag + 8 * i;
-            if (a < n_act && j0 + jj < n_dn) gow_part[base + (size_t)a * n_dn + j0 + jj] = acc[i];
-        }
-        if (blockIdx.x == 0 && threadIdx.x < 96 && a0 + threadIdx.x < n_act)
-            gob_part[(size_t)chunk * n_act + a0 + threadIdx.x] = accb;
-    }
 }
 
 // a 16-bit state -> [rows][B] float32 (tests and diagnostics)
@@ -509,26 +411,10 @@ hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_logits16(const unsigned short* hK, int rows, const int* dn, int n_dn, const float* ow, const float* ob,
-                           int n_act, float* logits, int B, hipStream_t st) {
-    k_logits16<<<dim3((unsigned)(B / TW16), (unsigned)((n_act + RPG - 1) / RPG)), WG, 0, st>>>(hK, rows, dn, n_dn, ow, ob,
-                                                                                             n_act, logits);
-    return hipGetLastError();
-}
-
-hipError_t launch_readout_bwd_h16(const float* dl, const float* ow, const int* dn_inv, int n_dn, int n_act, int rows,
-                                  const BwdEpi16& epi, int B, hipStream_t st) {
+hipError_t launch_readout_bwd_h16_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
+                                       const BwdEpi16& epi, int B, hipStream_t st) {
     dim3 grid((unsigned)((rows + RPG - 1) / RPG), (unsigned)(B / TW16));
-    const size_t sm = (size_t)n_act * (TW16 + RPG) * sizeof(float);
-    k_rbwd_h16<<<grid, WG, sm, st>>>(dl, ow, dn_inv, n_dn, n_act, rows, epi);
-    return hipGetLastError();
-}
-
-hipError_t launch_readout_bwd_w16(const float* dl, const unsigned short* hK, int rows, const int* dn, int n_dn,
-                                  int n_act, float* gow_part, float* gob_part, int B, hipStream_t st) {
-    const int T = B / TW16;
-    dim3 grid((unsigned)((n_dn + 31) / 32), (unsigned)((T + RO_CHUNK16 - 1) / RO_CHUNK16));
-    k_rbwd_w16<<<grid, WG, 0, st>>>(dl, hK, rows, dn, n_dn, n_act, T, gow_part, gob_part);
+    k_rbwd_h16_mfma<<<grid, WG, 0, st>>>(dl, owT, readout_pad(n_act), dn_inv, n_act, rows, epi);
     return hipGetLastError();
 }
 

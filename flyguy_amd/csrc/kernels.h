@@ -100,14 +100,13 @@ hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStre
 // the read-out on the matrix cores (readout.hip): owT, n_dn x readout_pad(n_act) floats of scratch for the
 // transposed weights; hK float32 tiles of 32 or (bf16_states) bfloat16 tiles of 64
 int readout_pad(int n_act);
+hipError_t launch_owT(const float* ow, int n_act, int n_dn, float* owT, hipStream_t st);
+hipError_t launch_readout_bwd_w_mfma(const float* dl, const void* hK, bool bf16_states, int rows, const int* dn,
+                                     int n_dn, int n_act, float* gow_part, float* gob_part, int B, hipStream_t st);
+hipError_t launch_readout_bwd_h_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
+                                     const BwdEpi& epi, int B, hipStream_t st);
 hipError_t launch_logits_mfma(const void* hK, bool bf16_states, int rows, const int* dn, int n_dn, const float* ow,
                               const float* ob, int n_act, float* owT, float* logits, int B, hipStream_t st);
-hipError_t launch_logits(const float* hK, Lay lh, const int* dn, int n_dn, const float* ow, const float* ob, int n_act,
-                         float* logits, int B, hipStream_t st);
-hipError_t launch_readout_bwd_h(const float* dl, const float* ow, const int* dn_inv, int n_dn, int n_act, int rows,
-                                const BwdEpi& epi, int B, hipStream_t st);
-hipError_t launch_readout_bwd_w(const float* dl, const float* hK, Lay lh, const int* dn, int n_dn, int n_act,
-                                float* gow_part, float* gob_part, int B, hipStream_t st);
 int readout_chunks(int B);
 // G[idx[i]] += sum over nt tiles of part[t * ld + i] (times -sigmoid(theta[idx[i]]) if theta); idx[i] < 0: skipped,
 // idx == nullptr: i itself.  The indices a launch names are distinct, so no two threads add to one entry.
@@ -149,13 +148,9 @@ hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* sr
                          float* part, int T, hipStream_t st);
 hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
                          long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st);
-hipError_t launch_logits16(const unsigned short* hK, int rows, const int* dn, int n_dn, const float* ow, const float* ob,
-                           int n_act, float* logits, int B, hipStream_t st);
-hipError_t launch_readout_bwd_h16(const float* dl, const float* ow, const int* dn_inv, int n_dn, int n_act, int rows,
-                                  const BwdEpi16& epi, int B, hipStream_t st);
-hipError_t launch_readout_bwd_w16(const float* dl, const unsigned short* hK, int rows, const int* dn, int n_dn,
-                                  int n_act, float* gow_part, float* gob_part, int B, hipStream_t st);
 hipError_t launch_export16(const unsigned short* src, int rows, float* dst, int B, hipStream_t st);
+hipError_t launch_readout_bwd_h16_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
+                                       const BwdEpi16& epi, int B, hipStream_t st);
 
 // KL(teacher || student) per sample (flyguy_train.cu:104-123): dl [B][n_act]; stats {KL sum, agreements} set, or
 // added to when accumulate

@@ -8,6 +8,7 @@
 // reach the 8 lanes of each group through LDS; the 8 source rows are then gathered as independent 128-byte lines
 // of the tile's slab, with no branch per edge (unused positions gather NO_ROW, which reads zeros).
 #include "device.h"
+#include "readout.h"
 
 namespace fg {
 
@@ -293,113 +294,25 @@ __global__ __launch_bounds__(WG) void k_obs_in(const float* __restrict__ obs, fl
     }
 }
 
-// logits[b][a] = ob[a] + sum_j ow[a][j] * hK[dn[j]][b], summed in j order (flyguy_train.cu:95-101).  One workgroup per
-// (tile, 32 actions): lane group g (8 lanes, a float4 of the tile's samples each) owns action a0 + g; chunks of 64
-// read-out rows and the matching weights are staged in LDS.
-constexpr int LG_J = 64;
-__global__ __launch_bounds__(WG) void k_logits(const float* __restrict__ hK, Lay lh, const int* __restrict__ dn, int n_dn,
-                                               const float* __restrict__ ow, const float* __restrict__ ob, int n_act,
-                                               float* __restrict__ logits) {
-    __shared__ float4 hs[LG_J][LPR];
-    __shared__ float ws[RPG][LG_J + 1];
-    const int tile = blockIdx.x, a0 = blockIdx.y * RPG;
-    const int g = threadIdx.x >> 3, sub = threadIdx.x & 7, a = a0 + g;
-    float4 acc = splat(a < n_act ? ob[a] : 0.f);
-    for (int j0 = 0; j0 < n_dn; j0 += LG_J) {
-        const int nj = min(LG_J, n_dn - j0);
-        __syncthreads();
-        for (int i = threadIdx.x; i < LG_J * LPR; i += WG) {
-            const int jj = i / LPR, q = i % LPR;
-            hs[jj][q] = jj < nj ? *at4(hK, lh, tile, dn[j0 + jj], q) : splat(0.f);
-        }
-        for (int i = threadIdx.x; i < RPG * LG_J; i += WG) {
-            const int aa = i / LG_J, jj = i % LG_J;
-            ws[aa][jj] = (jj < nj && a0 + aa < n_act) ? ow[(size_t)(a0 + aa) * n_dn + j0 + jj] : 0.f;
-        }
-        __syncthreads();
-        for (int jj = 0; jj < nj; ++jj) fma4(ws[g][jj], hs[jj][sub], acc);
-    }
-    if (a >= n_act) return;
-    float* o = logits + (size_t)(tile * TW + sub * 4) * n_act + a;
-    o[0] = acc.x;
-    o[n_act] = acc.y;
-    o[2 * n_act] = acc.z;
-    o[3 * n_act] = acc.w;
-}
-
-// gh of the top layer from the logits' gradient, then the neuron backward (flyguy_train.cu:136-141, 143-156)
-__global__ __launch_bounds__(WG) void k_readout_bwd_h(const float* __restrict__ dl, const float* __restrict__ ow,
-                                                      const int* __restrict__ dn_inv, int n_dn, int n_act, int rows,
-                                                      BwdEpi epi) {
-    extern __shared__ float sm[];
-    float* dlT = sm;                       // [n_act][32]
-    float* owc = sm + (size_t)n_act * TW;  // [32][n_act]
+// gh of the top layer from the logits' gradient (flyguy_train.cu:136-141) on the matrix cores (readout.h): 32 rows x
+// 32 samples per workgroup, then the neuron backward (:143-156) per row and lane
+__global__ __launch_bounds__(WG) void k_readout_bwd_h_mfma(const float* __restrict__ dl, const float* __restrict__ owT,
+                                                           int ma, const int* __restrict__ dn_inv, int n_act, int rows,
+                                                           BwdEpi epi) {
+    __shared__ float part[4 * 32 * 33];
+    __shared__ float gh[32 * 33];
     const int tile = blockIdx.y, r0 = blockIdx.x * RPG;
-    for (int i = threadIdx.x; i < n_act * TW; i += WG) {
-        const int c = i / n_act, a = i % n_act;
-        dlT[a * TW + c] = dl[(size_t)(tile * TW + c) * n_act + a];
-    }
-    for (int i = threadIdx.x; i < RPG * n_act; i += WG) {
-        const int r = i / n_act, a = i % n_act, t = r0 + r;
-        const int j = t < rows ? dn_inv[t] : -1;
-        owc[r * n_act + a] = j >= 0 ? ow[(size_t)a * n_dn + j] : 0.f;
-    }
-    __syncthreads();
+    readout_gh_block(dl, owT, ma, dn_inv, rows, n_act, r0, tile * TW, part, gh, 33);
     const int r = threadIdx.x >> 3, sub = threadIdx.x & 7, t = r0 + r;
     if (t >= rows) return;                 // whole 8-lane groups
-    float4 acc = splat(0.f);
-    if (dn_inv[t] >= 0) {
-        const float4* d4 = reinterpret_cast<const float4*>(dlT) + sub;
-        for (int a = 0; a < n_act; ++a) fma4(owc[r * n_act + a], d4[a * LPR], acc);
-    }
+    const float* g = gh + r * 33 + sub * 4;
+    const float4 acc = make_float4(g[0], g[1], g[2], g[3]);
     bwd_finish<1>(epi, t, tile, sub, acc, bwd_inputs<1>(epi, t, epi.drow ? epi.drow[t] : -1, tile, sub));
 }
 
-// per chunk of 16 tiles: gow[a][j] partial = sum_b dl[b][a] * hK[dn[j]][b], gob[a] partial = sum_b dl[b][a]
+// per chunk of 512 samples (16 tiles): the read-out weights' gradient partials (readout.hip)
 constexpr int RO_CHUNK = 16;
 int readout_chunks(int B) { return (B / TW + RO_CHUNK - 1) / RO_CHUNK; }
-__global__ __launch_bounds__(WG) void k_readout_bwd_w(const float* __restrict__ dl, const float* __restrict__ hK, Lay lh,
-                                                      const int* __restrict__ dn, int n_dn, int n_act, int T,
-                                                      float* __restrict__ gow_part, float* __restrict__ gob_part) {
-    __shared__ float hT[32][33];
-    __shared__ float ds[TW][97];
-    const int j0 = blockIdx.x * 32, chunk = blockIdx.y;
-    const int jj = threadIdx.x & 31, ag = threadIdx.x >> 5;
-    const int t0 = chunk * RO_CHUNK, t1 = min(T, t0 + RO_CHUNK);
-    for (int a0 = 0; a0 < n_act; a0 += 96) {
-        float acc[12];
-        float accb = 0.f;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) acc[i] = 0.f;
-        for (int tile = t0; tile < t1; ++tile) {
-            __syncthreads();
-            for (int i = threadIdx.x; i < 32 * TW; i += WG) {
-                const int j = i / TW, c = i % TW;
-                hT[j][c] = (j0 + j < n_dn) ? hK[(size_t)tile * lh.tile + (size_t)dn[j0 + j] * lh.row + c] : 0.f;
-            }
-            for (int i = threadIdx.x; i < TW * 96; i += WG) {
-                const int c = i / 96, a = i % 96;
-                ds[c][a] = (a0 + a < n_act) ? dl[(size_t)(tile * TW + c) * n_act + a0 + a] : 0.f;
-            }
-            __syncthreads();
-            for (int c = 0; c < TW; ++c) {
-                const float hv = hT[jj][c];
-#pragma unroll
-                for (int i = 0; i < 12; ++i) acc[i] = fmaf(ds[c][ag + 8 * i], hv, acc[i]);
-            }
-            if (blockIdx.x == 0 && threadIdx.x < 96)
-                for (int c = 0; c < TW; ++c) accb += ds[c][threadIdx.x];
-        }
-        const size_t base = (size_t)chunk * n_act * n_dn;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) {
-            const int a = a0 + ag + 8 * i;
-            if (a < n_act && j0 + jj < n_dn) gow_part[base + (size_t)a * n_dn + j0 + jj] = acc[i];
-        }
-        if (blockIdx.x == 0 && threadIdx.x < 96 && a0 + threadIdx.x < n_act)
-            gob_part[(size_t)chunk * n_act + a0 + threadIdx.x] = accb;
-    }
-}
 
 // ------------------------------------------------------------------------------------------------ reductions
 // G[idx[i]] += sum_t part[t * ld + i]  (times -sigmoid(theta[idx[i]]) when theta is given: the threshold's gradient);
@@ -612,26 +525,10 @@ hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStre
     return hipGetLastError();
 }
 
-hipError_t launch_logits(const float* hK, Lay lh, const int* dn, int n_dn, const float* ow, const float* ob, int n_act,
-                         float* logits, int B, hipStream_t st) {
-    k_logits<<<dim3((unsigned)(B / TW), (unsigned)((n_act + RPG - 1) / RPG)), WG, 0, st>>>(hK, lh, dn, n_dn, ow, ob, n_act,
-                                                                                         logits);
-    return hipGetLastError();
-}
-
-hipError_t launch_readout_bwd_h(const float* dl, const float* ow, const int* dn_inv, int n_dn, int n_act, int rows,
-                                const BwdEpi& epi, int B, hipStream_t st) {
+hipError_t launch_readout_bwd_h_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
+                                     const BwdEpi& epi, int B, hipStream_t st) {
     dim3 grid((unsigned)((rows + RPG - 1) / RPG), (unsigned)(B / TW));
-    size_t sm = (size_t)2 * n_act * TW * sizeof(float);
-    k_readout_bwd_h<<<grid, WG, sm, st>>>(dl, ow, dn_inv, n_dn, n_act, rows, epi);
-    return hipGetLastError();
-}
-
-hipError_t launch_readout_bwd_w(const float* dl, const float* hK, Lay lh, const int* dn, int n_dn, int n_act,
-                                float* gow_part, float* gob_part, int B, hipStream_t st) {
-    const int T = B / TW;
-    dim3 grid((unsigned)((n_dn + 31) / 32), (unsigned)readout_chunks(B));
-    k_readout_bwd_w<<<grid, WG, 0, st>>>(dl, hK, lh, dn, n_dn, n_act, T, gow_part, gob_part);
+    k_readout_bwd_h_mfma<<<grid, WG, 0, st>>>(dl, owT, readout_pad(n_act), dn_inv, n_act, rows, epi);
     return hipGetLastError();
 }
 

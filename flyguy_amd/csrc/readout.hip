@@ -5,11 +5,9 @@
 // weights are read from a transposed copy owT[j][a] (actions padded to a multiple of 32 with zeros) so that a
 // half-wave's operand is one 128-byte line; the read-out rows are gathered from the tiled states (float32 tiles of 32
 // samples, or bfloat16 tiles of 64).
-#include "device.h"
+#include "readout.h"
 
 namespace fg {
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // owT[j][a] = ow[a][j] for a < n_act, 0 up to ma (a multiple of 32)
 __global__ void k_owT(const float* __restrict__ ow, int n_act, int n_dn, int ma, float* __restrict__ owT) {
@@ -88,7 +86,85 @@ __global__ __launch_bounds__(64 * RO_WAVES) void k_logits_mfma(const void* __res
     }
 }
 
+// The read-out weights' gradient per chunk of 512 samples (flyguy_train.cu:125-135):
+//   gow_part[chunk][a][j] = sum_b dl[b][a] hK[dn[j]][b],  gob_part[chunk][a] = sum_b dl[b][a]  (b in the chunk)
+// Grid (n_dn / 32 blocks of read-out rows, chunks), 256 threads: the 4 waves each take 128 of the chunk's samples for
+// every block of 32 actions (M = actions, N = read-out rows, K = samples); partials added through LDS in wave order.
+template <bool BF16S>
+__global__ __launch_bounds__(WG) void k_readout_bwd_w_mfma(const float* __restrict__ dl, const void* __restrict__ hK,
+                                                           int rows, int tw, const int* __restrict__ dn, int n_dn,
+                                                           int n_act, int B, float* __restrict__ gow_part,
+                                                           float* __restrict__ gob_part) {
+    __shared__ float part[4 * 32 * 33];
+    const int j0 = blockIdx.x * 32, chunk = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 31, kk = lane >> 5;
+    const int nb = (n_act + 31) / 32;
+    const int row = j0 + i < n_dn ? dn[j0 + i] : -1;
+    const int bs = min(B, chunk * 512 + wave * 128), be = min(B, bs + 128);
+    f32x16 acc[RO_MAXB];
+#pragma unroll
+    for (int m = 0; m < RO_MAXB; ++m)
+        acc[m] = f32x16{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int b = bs; b < be; b += 8) {
+        float bv[4], av[4][RO_MAXB];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int sm = b + 2 * u + kk;
+            const bool ok = sm < be;
+            bv[u] = (ok && row >= 0) ? state_at<BF16S>(hK, ((size_t)(sm / tw) * rows + row) * tw + sm % tw) : 0.f;
+#pragma unroll
+            for (int m = 0; m < RO_MAXB; ++m)
+                av[u][m] = (ok && m < nb && m * 32 + i < n_act) ? dl[(size_t)sm * n_act + m * 32 + i] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int m = 0; m < RO_MAXB; ++m)
+                if (m < nb) acc[m] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u][m], bv[u], acc[m], 0, 0, 0);
+    }
+    const size_t base = (size_t)chunk * n_act * n_dn;
+#pragma unroll
+    for (int m = 0; m < RO_MAXB; ++m) {
+        if (m >= nb) break;
+        float* pw = part + (size_t)wave * 32 * 33;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pw[mfma_row(r, lane) * 33 + i] = acc[m][r];
+        __syncthreads();
+        for (int e = threadIdx.x; e < 32 * 32; e += WG) {
+            const int ai = e >> 5, jc = e & 31, a = m * 32 + ai;
+            if (a < n_act && j0 + jc < n_dn)
+                gow_part[base + (size_t)a * n_dn + j0 + jc] =
+                    ((part[ai * 33 + jc] + part[32 * 33 + ai * 33 + jc]) + part[2 * 32 * 33 + ai * 33 + jc]) +
+                    part[3 * 32 * 33 + ai * 33 + jc];
+        }
+        __syncthreads();
+    }
+    if (blockIdx.x == 0 && (int)threadIdx.x < n_act) {
+        float sb = 0.f;
+        for (int b = min(B, chunk * 512); b < min(B, chunk * 512 + 512); ++b) sb += dl[(size_t)b * n_act + threadIdx.x];
+        gob_part[(size_t)chunk * n_act + threadIdx.x] = sb;
+    }
+}
+
 int readout_pad(int n_act) { return (n_act + 31) / 32 * 32; }
+
+hipError_t launch_owT(const float* ow, int n_act, int n_dn, float* owT, hipStream_t st) {
+    const int ma = readout_pad(n_act);
+    const long long n = (long long)n_dn * ma;
+    k_owT<<<(unsigned)((n + WG - 1) / WG), WG, 0, st>>>(ow, n_act, n_dn, ma, owT);
+    return hipGetLastError();
+}
+
+hipError_t launch_readout_bwd_w_mfma(const float* dl, const void* hK, bool bf16_states, int rows, const int* dn,
+                                     int n_dn, int n_act, float* gow_part, float* gob_part, int B, hipStream_t st) {
+    if (readout_pad(n_act) > 32 * RO_MAXB || n_act > WG) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n_dn + 31) / 32), (unsigned)readout_chunks(B));
+    if (bf16_states)
+        k_readout_bwd_w_mfma<true><<<grid, WG, 0, st>>>(dl, hK, rows, TW16, dn, n_dn, n_act, B, gow_part, gob_part);
+    else
+        k_readout_bwd_w_mfma<false><<<grid, WG, 0, st>>>(dl, hK, rows, TW, dn, n_dn, n_act, B, gow_part, gob_part);
+    return hipGetLastError();
+}
 
 hipError_t launch_logits_mfma(const void* hK, bool bf16_states, int rows, const int* dn, int n_dn, const float* ow,
                               const float* ob, int n_act, float* owT, float* logits, int B, hipStream_t st) {
