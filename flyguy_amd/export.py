@@ -57,6 +57,37 @@ def net_bytes(s: dict) -> bytes:
     return b"".join(parts)
 
 
+def read_net(src) -> dict:
+    """The structure dict of a NET.bin (a path or its bytes), the inverse of net_bytes (export.py:52-65 layout)."""
+    raw = src if isinstance(src, (bytes, bytearray)) else Path(src).read_bytes()
+    if raw[:4] != b"FLY1":
+        raise ValueError("not a FLY1 network file")
+    at = [4]
+
+    def ints(n):
+        a = np.frombuffer(raw, np.int32, n, at[0]).astype(np.int64)
+        at[0] += 4 * n
+        return a
+    od, na, K, nn, nw, ns, fan, ndn = (int(v) for v in ints(8))
+    s = {"obs_dim": od, "n_act": na, "hops": K, "n_neurons": nn, "n_w": nw, "n_s": ns, "fan": fan, "n_dn": ndn}
+    s["sizes"] = [int(v) for v in ints(K + 1)]
+    E = [int(v) for v in ints(K)]
+    E_in = ns * fan
+    s["in_crow"], s["in_col"] = ints(ns + 1), ints(E_in)
+    s["in_tcrow"], s["in_tcol"], s["in_tperm"] = ints(od + 1), ints(E_in), ints(E_in)
+    s["n0"] = ints(ns)
+    s["hop"] = []
+    for k in range(K):
+        rows, src = s["sizes"][k + 1], s["sizes"][k]
+        h = {"nid": ints(rows), "crow": ints(rows + 1), "col": ints(E[k]), "widx": ints(E[k]), "tcrow": ints(src + 1),
+             "tcol": ints(E[k]), "twidx": ints(E[k]), "drow": ints(rows)}
+        s["hop"].append(h)
+    s["dn_rows"], s["wmap"] = ints(ndn), ints(nw)
+    if at[0] != len(raw):
+        raise ValueError("network file of unexpected length")
+    return s
+
+
 def write_net(f, out: Path) -> dict:
     s = structure(f)
     Path(out).write_bytes(net_bytes(s))
