@@ -47,6 +47,13 @@ __device__ __forceinline__ int tile_of(int bid, int RB, int T, int& rb) {
     return bid / RB;
 }
 
+// a compile-time flag as a type (the hop kernels' step bodies take it: Full<true> for a step whose 8 slots are all
+// needed, Full<false> for a wave's last step)
+template <bool B>
+struct Full {
+    static constexpr bool value = B;
+};
+
 // broadcast lane (group_base + S) of each 8-lane group (ds_swizzle bit mode inside each 32-lane half)
 template <int S>
 __device__ __forceinline__ int bcast8(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x18 | (S << 5)); }

@@ -153,10 +153,27 @@ __global__ __launch_bounds__(WG) void k_cfwd16_combine(Plan p, const float* __re
 
 // ------------------------------------------------------------------------------------------------ backward
 struct BwdIn16 {
-    float h[8], z[8], gd[8];
+    u32x4 hr;                                   // the layer's h, as stored (8 bfloat16)
+    float z[8], gd[8];
     float gn, sp;
     int d;
 };
+__device__ __forceinline__ u32x4 ldr8(const bf16_t* base, int rows, int tile, int row, int sub) {
+    return *reinterpret_cast<const u32x4*>(base + ((size_t)tile * rows + row) * TW16 + sub * 8);
+}
+// sum over the lane's 8 samples of a * b, both bfloat16 as stored, in float32 (v_dot2_f32_bf16: two exact products
+// per instruction, samples in pairs).  The pairs are taken from a whole-vector cast with shufflevector: hipcc turns
+// a bit_cast of a vector ELEMENT (a[k]) into a read of element 0 for every k.
+__device__ __forceinline__ float dot8(const u32x4& a, const u32x4& b) {
+    typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+    const bf8 x = __builtin_bit_cast(bf8, a), y = __builtin_bit_cast(bf8, b);
+    float d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 0, 1), __builtin_shufflevector(y, y, 0, 1),
+                                              0.f, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 2, 3), __builtin_shufflevector(y, y, 2, 3), d, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 4, 5), __builtin_shufflevector(y, y, 4, 5), d, false);
+    d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(x, x, 6, 7), __builtin_shufflevector(y, y, 6, 7), d, false);
+    return d;
+}
 // MODE 1: a hop layer (d: the row's re-drive row); 2: the sensory layer
 template <int MODE>
 __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, int tile, int sub, BwdIn16& in) {
@@ -164,7 +181,7 @@ __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, in
     for (int k = 0; k < 8; ++k) in.z[k] = in.gd[k] = 0.f;
     in.d = MODE == 2 ? j : d;
     if (in.d >= 0) ldf8(f8p(e.gdrive, e.n_s, tile, in.d, sub), in.gd);
-    ld8(e.h, e.rows, tile, j, sub, in.h);
+    in.hr = ldr8(e.h, e.rows, tile, j, sub);
     if constexpr (MODE == 2) ld8(e.z, e.rows, tile, j, sub, in.z);
     const float4 r = e.info[j];
     in.gn = r.x;
@@ -174,14 +191,15 @@ __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, in
 template <int MODE>
 __device__ __forceinline__ void bwd_finish16(const BwdEpi16& e, int j, int tile, int sub, const float (&gh)[8],
                                              const BwdIn16& in) {
-    float g[8], gzv[8];
+    float g[8], gzv[8], h[8];
     float sg = 0.f, sgh = 0.f;
+    unpack8<BF16>(in.hr, h);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        g[k] = in.h[k] > 0.f ? gh[k] : 0.f;
+        g[k] = h[k] > 0.f ? gh[k] : 0.f;
         gzv[k] = g[k] * in.gn;
         sg += g[k];
-        sgh = fmaf(g[k], MODE == 1 ? in.h[k] : in.z[k], sgh);
+        sgh = fmaf(g[k], MODE == 1 ? h[k] : in.z[k], sgh);
     }
     const float ps = gsum8(sg);
     float pg;
@@ -255,43 +273,47 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
         (void*)(gz + (size_t)tile * gz_rows * TW16), (short)0, gz_rows * 128, 0x00020000);
     float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
     const bool whole = live && sg.y < 0;
-    float hj[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    u32x4 hj = {0u, 0u, 0u, 0u};                // the row's h, as stored: the weight gradient's operand
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     BwdIn16 in{};
-    for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
+    int j = 0, left = wok ? wv.y : 0;
+    auto step = [&](auto full) {               // (as in k_cfwd16: full steps, then the wave's last)
+        constexpr bool FULL = decltype(full)::value;
         int c[8];
         float wt[8];
         stage8(slots[grp], sub, nxt, c, wt);
         u32x4 raw[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) raw[s] = s < left ? gather16(rs, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
+        for (int s = 0; s < 8; ++s)
+            if (FULL || s < left) raw[s] = gather16(rs, c[s], sub);
         __builtin_amdgcn_sched_barrier(0);
-        if (left > 8) nxt = q[64 * (j + 1)];
+        if constexpr (FULL) nxt = q[64 * (j + 1)];
         if (j == 0) {                           // the row's own inputs, after the first gathers
             if (whole) {
                 bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in);
-#pragma unroll
-                for (int k = 0; k < 8; ++k) hj[k] = in.h[k];
+                hj = in.hr;
             } else if (live) {
-                ld8(epi.h, epi.rows, tile, sg.x, sub, hj);
+                hj = ldr8(epi.h, epi.rows, tile, sg.x, sub);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
         float d[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            float f[8];
-            unpack8<BF16>(raw[s], f);
-            float dp = 0.f;
+            if (FULL || s < left) {
+                float f[8];
+                unpack8<BF16>(raw[s], f);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                acc[k] = fmaf(wt[s], f[k], acc[k]);
-                dp = fmaf(hj[k], f[k], dp);
+                for (int k = 0; k < 8; ++k) acc[k] = fmaf(wt[s], f[k], acc[k]);
+                d[s] = dot8(hj, raw[s]);
+            } else {
+                d[s] = 0.f;                     // (a position no edge uses)
             }
-            d[s] = dp;
         }
         if (gwp) gwp[64 * j] = rs8(d, sub);
-    }
+    };
+    for (; left > 8; ++j, left -= 8) step(Full<true>{});
+    if (left > 0) step(Full<false>{});
     if (whole && !(wok && wv.y > 0)) bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in);
     if (!live) return;
     if (sg.y >= 0) {
