@@ -13,7 +13,8 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
   roofline: the dominant kernel's algorithmic bytes per launch / its mean duration (HIP events on the library's
            stream over the timed region), against 8 TB/s;
   cpu_baseline: the reference's own CPU forward (fly_infer.cpp, compiled into oracle/_ref) on a bounded sample of
-           the same network, one core; train: the oracle's float32 restatement on a small batch.
+           the same network, one core (and, under "all_cores", one handle per thread on up to 16 host cores);
+           train: the oracle's float32 restatement on a small batch.
   config5: the bfloat16-state core at B = 16384 (forward and teaching step) on the same network and on its
            Erdos-Renyi control;
   trainer: samples / s of the teaching trainer's own loop (flyguy_amd/flyguy_train, run as a child process on
@@ -72,6 +73,26 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
         fwd = {"value": sample / dt, "unit": "decisions/s", "cores": 1, "kind": "reference",
                "sample": f"{sample} batch-1 decisions of the same network through fly_infer.cpp (compiled from the "
                          f"reference), {dt:.1f} s"}
+        # the same on every host core this process may use (at most 16, a GPU's share of the host): one handle per
+        # thread (a handle is not thread-safe; ctypes releases the GIL during the call), sample / 4 decisions each
+        n_thr = max(1, min(16, len(os.sched_getaffinity(0))))
+        if n_thr > 1:
+            import threading
+            refs = [refinfer.RefInfer(s, params) for _ in range(n_thr)]
+            per = max(1, sample // 4)
+            xs = [rng.standard_normal((per, s["obs_dim"])).astype(np.float32) for _ in range(n_thr)]
+            for r, x in zip(refs, xs):
+                r.forward(x[:2])
+            th = [threading.Thread(target=r.forward, args=(x,)) for r, x in zip(refs, xs)]
+            t0 = time.perf_counter()
+            for t in th:
+                t.start()
+            for t in th:
+                t.join()
+            dt = time.perf_counter() - t0
+            fwd["all_cores"] = {"value": n_thr * per / dt, "unit": "decisions/s", "cores": n_thr,
+                                "sample": f"{n_thr} threads x {per} batch-1 decisions, {dt:.1f} s"}
+            del refs
     train = None
     if train_batch > 0:
         from flyguy_amd.export import net_bytes
