@@ -534,8 +534,8 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
     {
         Timed t(c, ST_PACK);
-        FG_CHECK(launch_pack(c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos, st), false);
-        for (auto& d : c.hop) FG_CHECK(launch_pack(d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos, st), false);
+        FG_CHECK(launch_pack(c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos, st, true), false);
+        for (auto& d : c.hop) FG_CHECK(launch_pack(d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos, st, true), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
     FwdEpi16 e0;
@@ -575,7 +575,7 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     { Timed t(c, ST_ZERO); FG_CHECK(launch_fill(c.gdrive, 0.f, (long long)B * c.n_s, st), false); }
     {
         Timed t(c, ST_PACK);
-        for (auto& d : c.hop) FG_CHECK(launch_pack(d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos, st), false);
+        for (auto& d : c.hop) FG_CHECK(launch_pack(d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos, st, true), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
     HopD& top = c.hop[K - 1];

@@ -40,6 +40,22 @@ __device__ __forceinline__ void ldf8(const float* p, float (&f)[8]) {
     f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
 }
 
+// The products of the hop kernels: acc[k] += w_a g_a[k] + w_b g_b[k] over the lane's 8 samples, for two edges a, b
+// at once on v_dot2_f32_bf16 (two exact products and the sum in float32).  The weights come packed as bfloat16
+// values in float32 (low halves zero, k_pack<true>); v_perm_b32 pairs the two edges' weights, and the two gathered
+// states sample by sample.
+__device__ __forceinline__ void fma_pair(float wa, float wb, const u32x4& ga, const u32x4& gb, float (&acc)[8]) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    const bf2 w2 = __builtin_bit_cast(bf2, __builtin_amdgcn_perm(__float_as_uint(wb), __float_as_uint(wa), 0x07060302u));
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const unsigned a = ga[m], b = gb[m];
+        const unsigned lo = __builtin_amdgcn_perm(b, a, 0x05040100u), hi = __builtin_amdgcn_perm(b, a, 0x07060302u);
+        acc[2 * m] = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(bf2, lo), acc[2 * m], false);
+        acc[2 * m + 1] = __builtin_amdgcn_fdot2_f32_bf16(w2, __builtin_bit_cast(bf2, hi), acc[2 * m + 1], false);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ forward
 struct FwdIn16 {
     float dv[8];
@@ -107,12 +123,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            float f[8];
-            unpack8<BF16>(raw[s], f);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc[k] = fmaf(wt[s], f[k], acc[k]);
-        }
+        for (int s = 0; s < 8; s += 2) fma_pair(wt[s], wt[s + 1], raw[s], raw[s + 1], acc);
     }
     if (whole && !(wok && wv.y > 0)) {          // a wave without edges
         fwd_inputs16(epi, sg.x, sg.z, tile, sub, in);
@@ -284,8 +295,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
         stage8(slots[grp], sub, nxt, c, wt);
         u32x4 raw[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
-            if (FULL || s < left) raw[s] = gather16(rs, c[s], sub);
+        for (int s = 0; s < 8; ++s) raw[s] = (FULL || s < left) ? gather16(rs, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (FULL) nxt = q[64 * (j + 1)];
         if (j == 0) {                           // the row's own inputs, after the first gathers
@@ -299,17 +309,10 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
         __builtin_amdgcn_sched_barrier(0);
         float d[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            if (FULL || s < left) {
-                float f[8];
-                unpack8<BF16>(raw[s], f);
+        for (int s = 0; s < 8; s += 2)
+            if (FULL || s < left) fma_pair(wt[s], wt[s + 1], raw[s], raw[s + 1], acc);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) acc[k] = fmaf(wt[s], f[k], acc[k]);
-                d[s] = dot8(hj, raw[s]);
-            } else {
-                d[s] = 0.f;                     // (a position no edge uses)
-            }
-        }
+        for (int s = 0; s < 8; ++s) d[s] = (FULL || s < left) ? dot8(hj, raw[s]) : 0.f;   // (0: no edge there)
         if (gwp) gwp[64 * j] = rs8(d, sub);
     };
     for (; left > 8; ++j, left -= 8) step(Full<true>{});

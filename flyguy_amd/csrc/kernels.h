@@ -89,8 +89,10 @@ struct BwdEpi {
 };
 
 // launch wrappers (all asynchronous on `st`)
-// cw[p] = (pcol[p], w[pidx[p]]) for the npos positions of a plan; pidx[p] < 0: (NO_ROW, 0)
-hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* cw, long long npos, hipStream_t st);
+// cw[p] = (pcol[p], w[pidx[p]]) for the npos positions of a plan; pidx[p] < 0: (NO_ROW, 0).  bf16w: the weight
+// rounded to bfloat16 (nearest even), as the float32 of that value (the bfloat16-state core's products)
+hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* cw, long long npos, hipStream_t st,
+                       bool bf16w = false);
 // src_rows / gz_rows: rows of the gathered state (a gather of a row outside it reads zeros)
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st);

@@ -13,13 +13,17 @@
 namespace fg {
 
 // ------------------------------------------------------------------------------------------------ packing
-// the (source, weight) pair of every plan position, from the current weights
+// the (source, weight) pair of every plan position, from the current weights; BF16W: the weight rounded to bfloat16
+// (nearest even), kept as the float32 of that value (low 16 bits zero)
+template <bool BF16W>
 __global__ void k_pack(const int* __restrict__ pcol, const int* __restrict__ pidx, const float* __restrict__ w,
                        int2* __restrict__ cw, long long n) {
     const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= n) return;
     const int i = pidx[p];
-    cw[p] = i >= 0 ? make_int2(pcol[p], __float_as_int(w[i])) : make_int2(NO_ROW, 0);
+    float v = i >= 0 ? w[i] : 0.f;
+    if (BF16W) v = (float)(__bf16)v;
+    cw[p] = i >= 0 ? make_int2(pcol[p], __float_as_int(v)) : make_int2(NO_ROW, 0);
 }
 
 // ------------------------------------------------------------------------------------------------ forward
@@ -459,9 +463,13 @@ __global__ void k_export(const float* __restrict__ src, Lay ls, float* __restric
 // ------------------------------------------------------------------------------------------------ launchers
 static inline unsigned blocks(long long n, int per = WG) { return (unsigned)((n + per - 1) / per); }
 
-hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* cw, long long npos, hipStream_t st) {
+hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* cw, long long npos, hipStream_t st,
+                       bool bf16w) {
     if (npos <= 0) return hipSuccess;
-    k_pack<<<blocks(npos), WG, 0, st>>>(pcol, pidx, w, cw, npos);
+    if (bf16w)
+        k_pack<true><<<blocks(npos), WG, 0, st>>>(pcol, pidx, w, cw, npos);
+    else
+        k_pack<false><<<blocks(npos), WG, 0, st>>>(pcol, pidx, w, cw, npos);
     return hipGetLastError();
 }
 

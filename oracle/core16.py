@@ -2,13 +2,16 @@
 
 The arithmetic is the reference's (flyguy/native/flyguy_train.cu:73-203: plug, neuron layers, hops, read-out and
 their backward, as oracle/fly_oracle.c restates them), done here in float64 with the sums of scipy's sparse products.
-What makes it the 16-bit variant is where values are rounded to bfloat16 (round to nearest even), the points where
-the library stores a state:
-  x = bf16(obs); drive = in_b + in_w . x; h0 = bf16(relu(gain drive - softplus theta)); the stored drive bf16(drive);
-  hop k: z = W . h_{k-1} (+ the stored drive of a re-drive row), h_k = bf16(relu(gain z - softplus theta));
+What makes it the 16-bit variant is where values are rounded to bfloat16 (round to nearest even): the points where
+the library stores a state, and the connection strengths and plug weights its sparse products use (the masters,
+their gradients and Adam stay float32):
+  x = bf16(obs); drive = in_b + bf16(in_w) . x; h0 = bf16(relu(gain drive - softplus theta)); the stored drive
+  bf16(drive);
+  hop k: z = bf16(W) . h_{k-1} (+ the stored drive of a re-drive row), h_k = bf16(relu(gain z - softplus theta));
   backward: gz = g gain with g = gh where h > 0, gathered as bf16(gz); the drive's gradient sums the hops' gz before
   rounding; a hop layer's gain gradient is sum g (h + softplus theta) / gain over its stored h (0 when gain = 0), the
-  sensory layer's sum g . bf16(drive); per-connection gradients multiply bf16(gz) by the stored source states.
+  sensory layer's sum g . bf16(drive); per-connection gradients multiply bf16(gz) by the stored source states; the
+  gradient of a layer's output is bf16(W)^T . bf16(gz).
 softplus is taken in float32 (the library computes it so).
 
 Pinned by tests/test_gpu_core16.py: bit-exact agreement on networks whose every value and sum is exact (integer
@@ -43,10 +46,14 @@ def _csr(vals, col, crow, shape):
 class Core16:
     """One network (structure dict of flyguy_amd.export.structure) with its seven weight arrays."""
 
-    def __init__(self, s: dict, params: list[np.ndarray], round: bool = True):
+    def __init__(self, s: dict, params: list[np.ndarray], round: bool = True, round_weights: bool = True):
+        """round: the bfloat16 rounding on (states, and the weights of the sparse products unless round_weights is
+        False) or off (the float32 / float64 core)."""
         self.s = s
         self.P = [np.asarray(p, np.float64) for p in params]
-        self.r = bf16 if round else (lambda a: np.asarray(a, np.float64))
+        ident = lambda a: np.asarray(a, np.float64)                              # noqa: E731
+        self.r = bf16 if round else ident
+        self.rw = bf16 if round and round_weights else ident
 
     def forward(self, obs: np.ndarray) -> np.ndarray:
         s, r = self.s, self.r
@@ -54,7 +61,7 @@ class Core16:
         spl = _softplus32(theta)
         n_s, od = s["n_s"], s["obs_dim"]
         self.x = r(np.asarray(obs, np.float32).T.astype(np.float64))             # [obs_dim][B]
-        drive = in_b[:, None] + _csr(in_w, s["in_col"], s["in_crow"], (n_s, od)) @ self.x
+        drive = in_b[:, None] + _csr(self.rw(in_w), s["in_col"], s["in_crow"], (n_s, od)) @ self.x
         n0 = np.asarray(s["n0"])
         h0 = r(np.maximum(gain[n0][:, None] * drive - spl[n0][:, None], 0.0))
         self.drive = r(drive)
@@ -63,7 +70,7 @@ class Core16:
         for k, h in enumerate(s["hop"]):
             rows, src = s["sizes"][k + 1], s["sizes"][k]
             widx = np.asarray(h["widx"])
-            z = _csr(W[widx], h["col"], h["crow"], (rows, src)) @ hp
+            z = _csr(self.rw(W[widx]), h["col"], h["crow"], (rows, src)) @ hp
             drow = np.asarray(h["drow"])
             m = drow >= 0
             z[m] += self.drive[drow[m]]
@@ -112,7 +119,7 @@ class Core16:
             crow, col, widx = (np.asarray(h[x]) for x in ("crow", "col", "widx"))
             tgt = np.repeat(np.arange(len(crow) - 1), np.diff(crow))
             np.add.at(gW, widx, (gz16[tgt] * below[col]).sum(1))
-            A = _csr(W[widx], col, crow, (s["sizes"][k], s["sizes"][k - 1]))
+            A = _csr(self.rw(W[widx]), col, crow, (s["sizes"][k], s["sizes"][k - 1]))
             gh = A.T @ gz16
         h0, dr = self.states[0]
         n0 = np.asarray(s["n0"])

@@ -4,7 +4,8 @@
 Bars:
   * the rounding (obs -> x) bit-exact against hand-worked ties and special values;
   * networks whose values and sums are all exact (integer states, weights +-1): logits, every layer's state and all
-    seven gradients bit-exact;
+    seven gradients bit-exact; the same with strengths and plug weights off the bfloat16 grid (1 + 2^-9, a tie
+    1 + 2^-8, 1 - 2^-10), which the products must round to +-1 first;
   * general networks: logits within 1e-3 and gradients within 1e-2 of the largest entry (a float32 sum and the
     float64 oracle may round a state to neighbouring bfloat16 values, 2^-8 apart), argmax identical where the top-2
     margin exceeds 1e-2;
@@ -92,6 +93,38 @@ def test_exact_forward_backward(gpu_lib, name, hops, fan):
     wg = o.backward(dl)
     for n, g, w in zip(NAMES, grads, wg):
         assert np.array_equal(g, w.astype(np.float32)), (n, rel(g, w))
+
+
+def test_weights_are_rounded_to_bfloat16(gpu_lib):
+    """The sparse products use the strengths and plug weights rounded to bfloat16 (nearest even); the masters keep
+    their float32 values.  Weights 1 + 2^-9, 1 + 2^-8 (a tie, to even: 1) and 1 - 2^-10 all round to 1, so the case
+    stays exact and the library must equal the rounding oracle bit for bit, while the oracle without weight rounding
+    differs."""
+    s, P, obs = _exact_case("a", 3, 5, 5)
+    rng = np.random.default_rng(12)
+    off = np.array([1 + 2.0 ** -9, 1 + 2.0 ** -8, 1 - 2.0 ** -10], np.float32)
+    for i in (0, 3):
+        nz = P[i] != 0
+        P[i][nz] = np.sign(P[i][nz]) * off[rng.integers(0, 3, int(nz.sum()))]
+    assert not np.array_equal(bf16(P[0]), P[0].astype(np.float64))
+    say("bf16 weights off the bfloat16 grid")
+    o = Core16(s, P)
+    want = o.forward(obs)
+    for layer, (h, _) in enumerate(o.states):
+        assert np.array_equal(bf16(h), h) and np.abs(h).max() < 256, layer
+    core = Core(s, P, max_batch=64, flags=BF16)
+    got = core.forward(obs)
+    assert np.array_equal(got, want.astype(np.float32))
+    dl = np.random.default_rng(13).choice([-1.0, 0.0, 1.0], got.shape).astype(np.float32)
+    core.zero_grad()
+    core.backward(dl)
+    wg = o.backward(dl)
+    for n, g, w in zip(NAMES, core.get(4), wg):
+        assert np.array_equal(g, w.astype(np.float32)), (n, rel(g, w))
+    un = Core16(s, P, round_weights=False)                      # the check has teeth: unrounded weights differ
+    un.forward(obs)
+    assert any(not np.array_equal(a, b) for a, b in zip(un.backward(dl), wg))
+    assert np.array_equal(core.get(0)[0], P[0])                 # the master strengths are untouched
 
 
 def _general(s, params, B, seed):
