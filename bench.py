@@ -19,7 +19,7 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
            Erdos-Renyi control;
   trainer: samples / s of the teaching trainer's own loop (flyguy_amd/flyguy_train, run as a child process on
            synthetic binary16 FLYD chunks of the same network: draw, gather, step, as its log reports them) at
-           B = 4096 and at the reference trainer's default B = 512.
+           B = 4096, at the reference trainer's default B = 512, and with --bf16 1 at B = 16384.
 One JSON line on stdout.  Only one GPU: --gpus N > 1 exits with a message.
 """
 from __future__ import annotations
@@ -142,17 +142,18 @@ def trainer_leg(s, params, batches, steps: int) -> dict:
                 fh.write(b"FLYD" + struct.pack("<qii", n, s["obs_dim"], s["n_act"]))
                 fh.write(rng.standard_normal((n, s["obs_dim"]), dtype=np.float32).astype(np.float16).tobytes())
                 fh.write((2 * rng.standard_normal((n, s["n_act"]), dtype=np.float32)).astype(np.float16).tobytes())
-        for B in batches:
+        for B, bf16 in batches:
             n_steps = steps * max(1, 4096 // B)
-            cmd = [str(exe), str(tmp / "net.bin"), str(tmp / "init.bin"), str(data), str(tmp / f"out{B}"),
+            key = f"B={B}" + (" bf16" if bf16 else "")
+            cmd = [str(exe), str(tmp / "net.bin"), str(tmp / "init.bin"), str(data), str(tmp / f"out{B}{bf16}"),
                    "--batch", str(B), "--steps", str(n_steps), "--log", str(n_steps // 2), "--eval-batches", "0",
-                   "--save-sec", "1e9", "--ring", "3"]
-            print(f"# trainer B={B}: {n_steps} steps", file=sys.stderr, flush=True)
+                   "--save-sec", "1e9", "--ring", "3", "--bf16", str(int(bf16))]
+            print(f"# trainer {key}: {n_steps} steps", file=sys.stderr, flush=True)
             r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
             rates = [float(m.group(1)) for m in re.finditer(r"^step \d+ \| ([0-9.]+) samples/s", r.stdout, re.M)]
             if r.returncode != 0 or not rates:
                 raise RuntimeError(f"flyguy_train failed ({r.returncode}): {r.stderr[-2000:]}")
-            out[f"B={B}"] = {"value": rates[-1], "unit": "samples/s", "steps_timed": n_steps - n_steps // 2}
+            out[key] = {"value": rates[-1], "unit": "samples/s", "steps_timed": n_steps - n_steps // 2}
     return out
 
 
@@ -387,13 +388,15 @@ def main() -> int:
     config4 = config4_leg(args.config4_steps, W) if args.config4_steps > 0 else None
     trainer = None
     if args.trainer_steps > 0:
-        trainer = trainer_leg(s, params, (4096, 512), args.trainer_steps)
+        trainer = trainer_leg(s, params, ((4096, False), (512, False), (16384, True)), args.trainer_steps)
         trainer["workload"] = ("flyguy_train loop on synthetic binary16 FLYD chunks (3 x 32,768 samples, ring of 3) of "
-                               "the same network: draw, gather, teaching step, samples/s from its own log")
+                               "the same network: draw, gather, teaching step, samples/s from its own log; float32 "
+                               "at B=4096 and 512, and --bf16 1 (bfloat16 states and edge weights) at B=16384")
         trainer["reference_published"] = {"value": 10300, "unit": "samples/s", "batch": 512,
                                           "hardware": "RTX 4070 laptop"}
         print(f"# trainer: {trainer['B=4096']['value']:,.0f} samples/s at B=4096, "
-              f"{trainer['B=512']['value']:,.0f} at B=512", file=sys.stderr, flush=True)
+              f"{trainer['B=512']['value']:,.0f} at B=512, {trainer['B=16384 bf16']['value']:,.0f} at B=16384 bf16",
+              file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC, "value": round(dps, 1), "unit": "decisions/s", "n_gpus": 1, "steps": K, "warmup": W,

@@ -552,6 +552,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
         e.info = d.info;
         if (d.has_drive) { e.drive = s16(c.drive); e.n_s = c.n_s; }
         e.h = s16(d.h);
+        if (c.keep_z) e.z = s16(d.zk);
         e.rows = d.rows;
         { Timed t(c, ST_HOP + std::min(hk, 7)); FG_CHECK(launch_fwd16c(d.fp.view(), d.cw, hp, d.src, e, c.part, T, st), false); }
         hp = s16(d.h);

@@ -102,9 +102,50 @@ __global__ __launch_bounds__(256) void k_fired(const float* __restrict__ h, cons
     }
 }
 
-static hipError_t launch_fired(const float* h, const float* z, int rows, int T, int* cnt, float* sq, hipStream_t st) {
+// the same over a bfloat16 layer [T][rows][64]: each of the 8 lanes of a row takes 8 samples of every tile
+__global__ __launch_bounds__(256) void k_fired16(const unsigned short* __restrict__ h, const unsigned short* __restrict__ z,
+                                                 int rows, int T, int* __restrict__ cnt, float* __restrict__ sq) {
+    const int row = blockIdx.x * 32 + (int)(threadIdx.x >> 3), sub = threadIdx.x & 7;
+    int c = 0;
+    float v = 0.f;
+    if (row < rows) {
+        for (int t = 0; t < T; ++t) {
+            const size_t o = ((size_t)t * rows + row) * TW16 + 8 * sub;
+            const uint4 hv = *reinterpret_cast<const uint4*>(h + o);
+            const unsigned hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                c += (__uint_as_float(hw[k] << 16) > 0.f) + (__uint_as_float(hw[k] & 0xffff0000u) > 0.f);
+            if (z) {
+                const uint4 zv = *reinterpret_cast<const uint4*>(z + o);
+                const unsigned zw[4] = {zv.x, zv.y, zv.z, zv.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float a = __uint_as_float(zw[k] << 16), b = __uint_as_float(zw[k] & 0xffff0000u);
+                    v += a * a + b * b;
+                }
+            }
+        }
+    }
+    c = isum8(c);
+    v = sum8(v);
+    if (row < rows && sub == 0) {
+        cnt[row] += c;
+        sq[row] += v;
+    }
+}
+
+// the survey sums of one layer's states (float32 [T][rows][32] or, bf16, bfloat16 [T][rows][64]; z nullable) over
+// B samples
+static hipError_t launch_fired(const void* h, const void* z, bool bf16, int rows, int B, int* cnt, float* sq,
+                               hipStream_t st) {
+    const int T = B / (bf16 ? TW16 : TW);
     if (rows <= 0 || T <= 0) return hipSuccess;
-    k_fired<<<(unsigned)((rows + 31) / 32), 256, 0, st>>>(h, z, rows, T, cnt, sq);
+    if (bf16)
+        k_fired16<<<(unsigned)((rows + 31) / 32), 256, 0, st>>>((const unsigned short*)h, (const unsigned short*)z, rows,
+                                                                 T, cnt, sq);
+    else
+        k_fired<<<(unsigned)((rows + 31) / 32), 256, 0, st>>>((const float*)h, (const float*)z, rows, T, cnt, sq);
     return hipGetLastError();
 }
 
@@ -121,17 +162,14 @@ static bool put_dev(Core& c, float* d, const std::vector<float>& v) {
 
 // ================================================================================================ survey
 static bool ensure_survey(Core& c) {
-    if (c.prec) {
-        set_error("surveys need a float32 core");
-        return false;
-    }
     if (c.scnt) return true;
     c.scnt = dalloc<int>(c, (size_t)c.rows_total);
     c.ssq = dalloc<float>(c, (size_t)c.rows_total);
     c.sstats = dalloc<float>(c, 4);
     bool ok = c.scnt && c.ssq && c.sstats;
-    for (auto& d : c.hop) {
-        d.zk = dalloc<float>(c, (size_t)c.Tm * d.rows * TW);
+    for (auto& d : c.hop) {                     // the pre-activation, stored like the layer's states
+        d.zk = c.prec ? reinterpret_cast<float*>(dalloc<unsigned short>(c, (size_t)c.maxB * d.rows))
+                      : dalloc<float>(c, (size_t)c.maxB * d.rows);
         ok = ok && d.zk;
     }
     return ok;
@@ -153,11 +191,11 @@ static bool survey_batch(Core& c, const float* obs, const float* teacher, int B,
     c.keep_z = false;
     if (!ok) return false;
     FG_CHECK(launch_loss(c.lg, teacher, c.dl, c.stats_part, c.sstats, c.n_act, B, it, c.st, true), false);
-    const int T = B / TW;
-    FG_CHECK(launch_fired(c.h0, nullptr, c.n_s, T, c.scnt, c.ssq, c.st), false);
+    const bool b16 = c.prec != 0;
+    FG_CHECK(launch_fired(c.h0, nullptr, b16, c.n_s, B, c.scnt, c.ssq, c.st), false);
     long long off = c.n_s;
     for (auto& d : c.hop) {
-        FG_CHECK(launch_fired(d.h, d.zk, d.rows, T, c.scnt + off, c.ssq + off, c.st), false);
+        FG_CHECK(launch_fired(d.h, d.zk, b16, d.rows, B, c.scnt + off, c.ssq + off, c.st), false);
         off += d.rows;
     }
     c.s_samples += B;
@@ -730,13 +768,13 @@ static bool fwd_bwd(Core& c, const float* obs, const float* tl, int B, float it,
 
 typedef std::unique_ptr<Core, void (*)(Core*)> CoreP;
 
-static CoreP open_net(const std::string& path, int B) {
+static CoreP open_net(const std::string& path, int B, int flags = 0) {
     auto bytes = read_file(path);
     if (bytes.empty()) {
         fprintf(stderr, "cannot open %s\n", path.c_str());
         return CoreP(nullptr, release);
     }
-    CoreP c(build(bytes.data(), (long long)bytes.size(), B), release);
+    CoreP c(build(bytes.data(), (long long)bytes.size(), B, flags), release);
     if (!c) fprintf(stderr, "%s: %s\n", path.c_str(), last_error());
     return c;
 }
@@ -794,6 +832,7 @@ static int train_main(int argc, const char* const* argv) {
     float lr = 3e-4f, lr_neuron = 1e-4f, lr_plug = 3e-4f, lr_min = 3e-5f, ema = 0.999f, clip = 0.f, temp = 1.f,
           revive_target = 0.4f;
     double max_reuse = -1;
+    int flags = 0;                                      // --bf16 1: the bfloat16-state core (FC_STATES_BF16)
     for (int i = 5; i + 1 < argc; i += 2) {
         const std::string a = argv[i];
         const double v = atof(argv[i + 1]);
@@ -819,11 +858,13 @@ static int train_main(int argc, const char* const* argv) {
         else if (a == "--ring") ring_k = std::max(1, (int)v);
         else if (a == "--holdout") holdout = (int)v;
         else if (a == "--passes") { }                  // (of the one-chunk-at-a-time trainer: ignored)
+        else if (a == "--bf16") flags = v != 0 ? FC_STATES_BF16 : 0;
         else { fprintf(stderr, "unknown option %s\n", a.c_str()); return 2; }
     }
-    if (B <= 0 || B % TW) { fprintf(stderr, "--batch must be a multiple of 32\n"); return 2; }
+    const int bq = flags & FC_STATES_BF16 ? TW16 : TW;
+    if (B <= 0 || B % bq) { fprintf(stderr, "--batch must be a multiple of %d\n", bq); return 2; }
     const std::string data = argv[3], out = argv[4];
-    CoreP cp = open_net(argv[1], B);
+    CoreP cp = open_net(argv[1], B, flags);
     if (!cp) return 1;
     Core& c = *cp;
     // a restart from this run's own save keeps the running average and the optimiser state
@@ -845,8 +886,9 @@ static int train_main(int argc, const char* const* argv) {
     std::mt19937_64 rng(12345 + step);
     const float it = 1.f / temp;
     printf("flyguy native trainer: %d neurons, %d strengths in play, %d hops, batch %d, lr %g (neurons %g, plugs %g), "
-           "teacher temperature %g, ring of %d chunks, start step %lld%s\n",
-           c.n_neurons, c.n_w, c.hops, B, lr, lr_neuron, lr_plug, temp, ring_k, step, opt ? ", optimiser state restored" : "");
+           "teacher temperature %g, ring of %d chunks, start step %lld%s%s\n",
+           c.n_neurons, c.n_w, c.hops, B, lr, lr_neuron, lr_plug, temp, ring_k, step, opt ? ", optimiser state restored" : "",
+           c.prec ? ", bfloat16 states" : "");
     fflush(stdout);
 
     Loader ld;

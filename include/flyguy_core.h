@@ -74,8 +74,8 @@ void* fc_create_from_memory(const void* net_bytes, long long len, int max_batch)
  * gradients the backward gathers) are kept as bfloat16, rounded to nearest even, in tiles of 64 samples, and the
  * sparse products (plug and hops, forward and backward) use the connection strengths and plug weights rounded to
  * bfloat16; sums, gradients, the float32 master weights and Adam stay float32.  Batches are then a multiple of 64.
- * Every other entry point works on such a handle as on a float32 one, except the surveys (fc_survey), which need
- * float32 states. */
+ * Every other entry point works on such a handle as on a float32 one (the surveys of include/flyguy_train.h count
+ * and square its stored bfloat16 states). */
 #define FC_STATES_BF16 1
 void* fc_create_ex(const void* net_bytes, long long len, int max_batch, int flags);
 

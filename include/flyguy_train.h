@@ -21,7 +21,9 @@ extern "C" {
  *   NET PARAMS_IN DATA_DIR OUT_PREFIX [--batch 512] [--lr 3e-4] [--lr-neuron 1e-4] [--lr-plug 3e-4] [--lr-min 3e-5]
  *     [--half-life 20000] [--passes 1] [--ema 0.999] [--log 100] [--save-sec 120] [--steps 0] [--clip 0] [--temp 1]
  *     [--eval-batches 16] [--revive-every 0] [--revive-batches 4] [--revive-target 0.4] [--revive-first 0]
- *     [--ring 3] [--max-reuse 4] [--holdout 0] [--eval-every 0]
+ *     [--ring 3] [--max-reuse 4] [--holdout 0] [--eval-every 0] [--bf16 0]
+ *   --bf16 1 trains on the library core with bfloat16 states and edge weights (FC_STATES_BF16; the batch a multiple
+ *   of 64): an addition of this library, the reference's trainer is float32 only.
  *   --check NET PARAMS BATCH      one forward + backward of a FLYB batch; prints loss, agreement, logits, gradients
  * argv[0] is the program name.  Returns the process exit status (0 done or stopped, 1 file or device error,
  * 2 usage).  Writes OUT_PREFIX.bin, .ema.bin, .opt.bin; a file OUT_PREFIX.STOP ends the run after a save. */
@@ -64,7 +66,8 @@ int fc_layers(void* core, int* sizes, int cap);
  * average) of obs [B][obs_dim] (device), the loss against teacher [B][n_act] (device) at 1/temperature `it`,
  * and per row of every layer the samples for which it fires (h > 0) and the sum of its squared pre-activation
  * (hop layers; 0 for the sensory layer).  reset = 1 clears the sums first.  Replaces the states of the last
- * forward (an fc_backward must follow a new fc_forward).  Returns 0 or -1. */
+ * forward (an fc_backward must follow a new fc_forward).  On a bfloat16-state handle (FC_STATES_BF16) the counts
+ * and squares are those of the stored bfloat16 states and pre-activations.  Returns 0 or -1. */
 int fc_survey(void* core, const float* obs, const float* teacher, int B, int ema, float it, int reset);
 
 /* The survey sums so far: cnt, sq [rows of every layer]; stats = {KL sum, agreements, samples}.  Returns the

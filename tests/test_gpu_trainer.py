@@ -5,7 +5,9 @@ Bars: the batch gather is bit-exact (binary16 -> float32 is exact); survey count
 library exports, and the sums of squares and loss sums within 1e-5 of the float64 oracle; the revive surgery marks,
 signs and resets exactly what the oracle's restatement does, and scales within 1e-4 (its scale factors come from
 float32 surveys); the network's output is bit-identical before and after a revive.  A trainer run leaves weights,
-running average and Adam state bit-identical to the replay (the same kernels on the same batches)."""
+running average and Adam state bit-identical to the replay (the same kernels on the same batches).  On a
+bfloat16-state handle: survey counts exact against its own stored states, sums of squares and the loss sum within
+1e-3 of the bfloat16 oracle (oracle/core16.py); a --bf16 trainer run bit-identical to its replay."""
 from __future__ import annotations
 
 import ctypes
@@ -24,6 +26,7 @@ from flyguy_amd.export import net_bytes, param_sizes, params_from_torch, structu
 from flyguy_amd.fly import FlyActor
 from gpu_helpers import Core, rel, say
 from oracle import trainer as ot
+from oracle.core16 import Core16, bf16
 from oracle.oracle import Oracle
 
 pytestmark = pytest.mark.gpu
@@ -146,6 +149,46 @@ def test_survey_matches_oracle(gpu_lib):
         assert rel(sq, osq) <= 1e-5, rel(sq, osq)
         assert abs(kl - okl) <= 1e-5 * max(abs(okl), 1.0), (kl, okl)
         assert abs(agree - oagree) <= 2, (agree, oagree)
+
+
+def test_bf16_survey_matches_oracle(gpu_lib):
+    """Surveys of a bfloat16-state handle count and square its stored bfloat16 states (oracle/core16.py)."""
+    s, params = toy_net("b", 3, 8, seed=3)
+    B = 128
+    core = Core(s, params, max_batch=B, flags=1)
+    rows = _layers(core.h)
+    R = sum(rows)
+    rng = np.random.default_rng(5)
+    batches = [(rng.standard_normal((B, OD)).astype(np.float32), (2 * rng.standard_normal((B, NA))).astype(np.float32))
+               for _ in range(2)]
+    o = Core16(s, params)
+    mine = np.zeros(R, np.int64)
+    ocnt, osq = np.zeros(R, np.int64), np.zeros(R)
+    near = np.zeros(R, bool)
+    okl = 0.0
+    for i, (obs, tl) in enumerate(batches):
+        x, t = torch.as_tensor(obs).cuda(), torch.as_tensor(tl).cuda()
+        say("bf16 fc_survey", i)
+        call("fc_survey", core.h, x.data_ptr(), t.data_ptr(), B, 0, 1.0, int(i == 0))
+        mine += np.concatenate([(core.state(k, 0, rows[k], B) > 0).sum(1) for k in range(len(rows))])
+        lg = o.forward(obs)
+        states = [(o.states[0][0], None)] + [(h, bf16(z)) for h, z in o.states[1:]]
+        c, q = ot.survey_sums(states)
+        ocnt += c
+        osq += q
+        near |= np.concatenate([((h > 0) & (h < 1e-2)).any(1) for h, _ in states])
+        lp = lg - lg.max(1, keepdims=True)
+        lp = lp - np.log(np.exp(lp).sum(1, keepdims=True))
+        tp = tl - tl.max(1, keepdims=True)
+        tp = tp - np.log(np.exp(tp).sum(1, keepdims=True))
+        okl += float((np.exp(tp) * (tp - lp)).sum())
+    cnt, sq, (kl, agree, samples) = _survey_read(core.h, R)
+    assert samples == 2 * B
+    assert np.array_equal(cnt, mine)                                   # the counts of the library's own states
+    assert np.array_equal(cnt[~near], ocnt[~near]), int((cnt != ocnt).sum())
+    assert (sq[:rows[0]] == 0).all()
+    assert rel(sq, osq) <= 1e-3, rel(sq, osq)
+    assert abs(kl - okl) <= 1e-3 * max(abs(okl), 1.0), (kl, okl)
 
 
 def _dead_case(seed=0):
@@ -297,6 +340,29 @@ def test_trainer_run_matches_replay(gpu_lib, tmp_path, capfd):
     ring = ot.scan_order(data, 2)
     assert ring == ["chunk_0001.bin", "chunk_0002.bin"]
     core = Core(s, params, max_batch=B)
+    _replay(core, ring, chunks, ot.MT19937_64(12345), steps, 0, B, OPTS["lr"], OPTS["lrn"], OPTS["lrp"], OPTS["lmin"],
+            OPTS["hl"], 0.0, OPTS["ema"])
+    _same(core, saved)
+
+
+def test_bf16_trainer_run_matches_replay(gpu_lib, tmp_path, capfd):
+    """--bf16 1: the trainer on a bfloat16-state handle, step for step what fc_teach_step does on one."""
+    s, params = toy_net("b", 3, 8, seed=2)
+    data, chunks = _setup(tmp_path, s, params)
+    B, steps = 64, 4
+    assert _run(tmp_path / "net.bin", tmp_path / "init.bin", data, tmp_path / "out",
+                *_opts(96, steps, bf16=1)) == 2                 # the batch must be a multiple of 64
+    rc = _run(tmp_path / "net.bin", tmp_path / "init.bin", data, tmp_path / "out",
+              *_opts(B, steps, log=2, eval_batches=2, bf16=1))
+    out = capfd.readouterr().out
+    say(out)
+    assert rc == 0
+    assert "bfloat16 states" in out and "done at step 4" in out
+    assert re.search(r"eval step 0 \| kl [0-9.]+ agree [0-9.]+ \| raw kl", out)
+    step, adam_t, saved = _saved(tmp_path, s)
+    assert step == 4 and adam_t == 4
+    ring = ot.scan_order(data, 2)
+    core = Core(s, params, max_batch=B, flags=1)
     _replay(core, ring, chunks, ot.MT19937_64(12345), steps, 0, B, OPTS["lr"], OPTS["lrn"], OPTS["lrp"], OPTS["lmin"],
             OPTS["hl"], 0.0, OPTS["ema"])
     _same(core, saved)
