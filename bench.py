@@ -58,6 +58,21 @@ def algorithmic_bytes(s: dict, B: int, sz: int = 4) -> dict:
     return {"hop_fwd": hop_fwd, "hop_bwd": hop_bwd, "infer": infer, "train": train, "n_params": n_params}
 
 
+# The vector-memory gather pipe of MI355X, measured (not a published figure): a wave-wide 16-byte-per-lane gather
+# takes about 19.5 CU-cycles per KB, i.e. 256 CUs x 2.4 GHz x 1024 / 19.5 bytes / s, whether the rows hit L2 or not.
+PEAK_GATHER = 256 * 2.4e9 * 1024 / 19.5
+
+
+def gather_pipe(E: int, B: int, ms: float) -> dict:
+    """The hop kernel against the gather pipe: one 128-byte line per connection and 32-sample tile."""
+    byts = E * (B // 32) * 128
+    ach = byts / (ms * 1e-3)
+    return {"bytes_per_launch": byts, "achieved": round(ach / 1e9, 1), "peak": round(PEAK_GATHER / 1e9, 1),
+            "unit": "GB/s", "frac": round(ach / PEAK_GATHER, 4),
+            "note": "gathered lines (connections x tiles x 128 B) against the measured line rate of the vector-memory "
+                    "pipe; the peak is a probe measurement, not a published figure"}
+
+
 def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None, dict | None]:
     import numpy as np
     from oracle import refinfer
@@ -410,7 +425,8 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(ach_f / PEAK_HBM, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": ab["hop_fwd"][kf], "mean_launch_ms": round(fwd_hops[dom_f], 4),
                      "whole_batch_frac": round(ab["infer"] / (t_fwd / K) / PEAK_HBM, 4),
-                     "whole_batch_algorithmic_bytes": ab["infer"]},
+                     "whole_batch_algorithmic_bytes": ab["infer"],
+                     "gather_pipe": gather_pipe(len(s["hop"][kf]["col"]), B, fwd_hops[dom_f])},
         "cpu_baseline": cpu_f,
         "train": {"value": round(sps, 1), "unit": "samples/s", "ms_per_step": round(ms_train, 4),
                   "workload": "fp32 teaching step: forward, KL(teacher||student) over 90 actions, fused backward, "
@@ -421,7 +437,8 @@ def main() -> int:
                                "algorithmic_bytes_per_launch": ab["hop_bwd"][kb],
                                "mean_launch_ms": round(bwd_hops[dom_b], 4),
                                "whole_step_frac": round(ab["train"] / (t_train / K) / PEAK_HBM, 4),
-                               "whole_step_algorithmic_bytes": ab["train"]},
+                               "whole_step_algorithmic_bytes": ab["train"],
+                               "gather_pipe": gather_pipe(len(s["hop"][kb]["col"]), B, bwd_hops[dom_b])},
                   "cpu_baseline": cpu_t},
         "trainer": trainer,
         "config5": config5,
