@@ -81,9 +81,6 @@ struct Core {
     long long adam_t = 0;
     int B = 0;
     hipStream_t st = nullptr;
-    hipStream_t st2 = nullptr;       // the gradient reductions, beside the backward kernels (default priority)
-    hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};   // hand-offs between the two streams
-    float* gwpart2 = nullptr;        // a second buffer of weight-gradient partials: hops alternate between the two
     std::vector<void*> allocs;
     Prof prof;
     float* arr(int set, int i) const { return pm + (long long)set * PT + off[i]; }
@@ -93,13 +90,12 @@ struct Core {
 struct Timed {
     Core& c;
     int stage;
-    hipStream_t s;
-    Timed(Core& c_, int stg, hipStream_t on = nullptr) : c(c_), stage(stg), s(on ? on : c_.st) { mark(0); }
+    Timed(Core& c_, int s) : c(c_), stage(s) { mark(0); }
     ~Timed() { mark(1); }
     void mark(int end) {
         if (!c.prof.on) return;
         hipEvent_t e = c.prof.get();
-        if (e && hipEventRecord(e, s) == hipSuccess) c.prof.rec.push_back({e, stage * 2 + end});
+        if (e && hipEventRecord(e, c.st) == hipSuccess) c.prof.rec.push_back({e, stage * 2 + end});
     }
 };
 

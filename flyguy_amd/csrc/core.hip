@@ -120,10 +120,6 @@ static bool upload_plan(Core& c, const HostPlan& h, int rows, const std::vector<
 
 void release(Core* c) {
     if (!c) return;
-    if (c->st2) (void)hipStreamSynchronize(c->st2);
-    for (hipEvent_t e : c->ev)
-        if (e) (void)hipEventDestroy(e);
-    if (c->st2) (void)hipStreamDestroy(c->st2);
     for (auto& r : c->prof.rec) (void)hipEventDestroy(r.first);
     for (auto e : c->prof.pool) (void)hipEventDestroy(e);
     for (void* p : c->allocs) (void)hipFree(p);
@@ -339,25 +335,21 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     c->dl = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->part = dalloc<float>(*c, Tm * std::max<long long>(max_slot, 1) * S);
     c->gwpart = dalloc<float>(*c, Tm * max_pos);
-    c->gwpart2 = dalloc<float>(*c, Tm * max_pos);
     c->ggp0 = dalloc<float>(*c, Tm * c->n_s);
     c->gsp0 = dalloc<float>(*c, Tm * c->n_s);
     c->ginb = dalloc<float>(*c, Tm * c->n_s);
     c->ginw = dalloc<float>(*c, Tm * c->E_in);
     c->gow_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act * c->n_dn);
     c->gob_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act);
-    c->stats_part = dalloc<float>(*c, (size_t)2 * ((bm + 63) / 64));     // one pair per 64 samples (k_loss)
+    c->stats_part = dalloc<float>(*c, (size_t)2 * ((bm + 31) / 32));     // one pair per 32 samples (k_loss)
     c->stats = dalloc<float>(*c, 4);
     c->red = dalloc<float>(*c, 1024);
     c->nrm = dalloc<float>(*c, 1);
     c->owT = dalloc<float>(*c, (size_t)c->n_dn * readout_pad(c->n_act));
     if (!c->x || !c->drive || !c->h0 || !c->gdrive || !c->gz[0] || !c->gz[1] || !c->lg || !c->dl || !c->part ||
         !c->gwpart || !c->ggp0 || !c->gsp0 || !c->ginb || !c->ginw || !c->gow_p || !c->gob_p || !c->stats_part ||
-        !c->stats || !c->red || !c->nrm || !c->owT || !c->gwpart2)
+        !c->stats || !c->red || !c->nrm || !c->owT)
         return nullptr;
-    if (hipStreamCreateWithFlags(&c->st2, hipStreamNonBlocking) != hipSuccess) { set_error("stream"); return nullptr; }
-    for (hipEvent_t& e : c->ev)
-        if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) { set_error("event"); return nullptr; }
     if (hipDeviceSynchronize() != hipSuccess) { set_error("device error after set-up"); return nullptr; }
     return c.release();
 }
@@ -454,19 +446,13 @@ bool backward(Core& c, const float* dlogits, int B) {
         FG_CHECK(launch_readout_bwd_w_mfma(dlogits, top.h, false, top.rows, c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st),
                  false);
     }
-    // The reductions of the per-tile partials into the gradient run on the second stream, each after the kernel that
-    // wrote its partials, while the next hop's backward runs; they stay in one order on that stream (the sums are the
-    // same), and st waits for them at the end.  Hops alternate between two weight-gradient partial buffers.
-    hipStream_t s2 = c.st2;
-    FG_CHECK(hipEventRecord(c.ev[0], st), false);
-    FG_CHECK(hipStreamWaitEvent(s2, c.ev[0], 0), false);
     const int nch = readout_chunks(B);
     {
-        Timed t(c, ST_REDUCE, s2);
-        FG_CHECK(launch_reduce(c.gow_p, (long long)c.n_act * c.n_dn, (long long)c.n_act * c.n_dn, nch, nullptr, nullptr, G[5], s2), false);
-        FG_CHECK(launch_reduce(c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], s2), false);
-        FG_CHECK(launch_reduce(top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1], s2), false);
-        FG_CHECK(launch_reduce(top.gsp, top.rows, top.rows, T, top.nid, theta, G[2], s2), false);
+        Timed t(c, ST_REDUCE);
+        FG_CHECK(launch_reduce(c.gow_p, (long long)c.n_act * c.n_dn, (long long)c.n_act * c.n_dn, nch, nullptr, nullptr, G[5], st), false);
+        FG_CHECK(launch_reduce(c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], st), false);
+        FG_CHECK(launch_reduce(top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1], st), false);
+        FG_CHECK(launch_reduce(top.gsp, top.rows, top.rows, T, top.nid, theta, G[2], st), false);
     }
 
     int cur = 0;
@@ -496,30 +482,21 @@ bool backward(Core& c, const float* dlogits, int B) {
             hbelow = c.h0; rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
         }
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
-        float* gwp = (k & 1) ? c.gwpart : c.gwpart2;
-        if (k + 2 <= K) FG_CHECK(hipStreamWaitEvent(st, c.ev[1 + (k & 1)], 0), false);   // hop k+2's reductions read it
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
-            FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), gwp,
+            FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart,
                                 d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st), false);
         }
-        FG_CHECK(hipEventRecord(c.ev[0], st), false);
-        FG_CHECK(hipStreamWaitEvent(s2, c.ev[0], 0), false);
-        {
-            Timed t(c, ST_REDUCE, s2);
-            FG_CHECK(launch_reduce(gwp, d.bp.npos, d.bp.npos, T, d.bp.pidx, nullptr, G[0], s2), false);
-            FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], s2), false);
-            FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], s2), false);
-            if (k == 1) {
-                FG_CHECK(launch_reduce(c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], s2), false);
-                FG_CHECK(launch_reduce(c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], s2), false);
-            }
+        Timed t(c, ST_REDUCE);
+        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, T, d.bp.pidx, nullptr, G[0], st), false);
+        FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
+        FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
+        if (k == 1) {
+            FG_CHECK(launch_reduce(c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], st), false);
+            FG_CHECK(launch_reduce(c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], st), false);
         }
-        FG_CHECK(hipEventRecord(c.ev[1 + (k & 1)], s2), false);
         cur ^= 1;
     }
-    FG_CHECK(hipEventRecord(c.ev[3], s2), false);
-    FG_CHECK(hipStreamWaitEvent(st, c.ev[3], 0), false);
     return true;
 }
 
@@ -597,19 +574,13 @@ static bool backward16(Core& c, const float* dlogits, int B) {
         FG_CHECK(launch_readout_bwd_w_mfma(dlogits, top.h, true, top.rows, c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st),
                  false);
     }
-    // The reductions of the per-tile partials into the gradient run on the second stream, each after the kernel that
-    // wrote its partials, while the next hop's backward runs; they stay in one order on that stream (the sums are the
-    // same), and st waits for them at the end.  Hops alternate between two weight-gradient partial buffers.
-    hipStream_t s2 = c.st2;
-    FG_CHECK(hipEventRecord(c.ev[0], st), false);
-    FG_CHECK(hipStreamWaitEvent(s2, c.ev[0], 0), false);
     const int nch = readout_chunks(B);
     {
-        Timed t(c, ST_REDUCE, s2);
-        FG_CHECK(launch_reduce(c.gow_p, (long long)c.n_act * c.n_dn, (long long)c.n_act * c.n_dn, nch, nullptr, nullptr, G[5], s2), false);
-        FG_CHECK(launch_reduce(c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], s2), false);
-        FG_CHECK(launch_reduce(top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1], s2), false);
-        FG_CHECK(launch_reduce(top.gsp, top.rows, top.rows, T, top.nid, theta, G[2], s2), false);
+        Timed t(c, ST_REDUCE);
+        FG_CHECK(launch_reduce(c.gow_p, (long long)c.n_act * c.n_dn, (long long)c.n_act * c.n_dn, nch, nullptr, nullptr, G[5], st), false);
+        FG_CHECK(launch_reduce(c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], st), false);
+        FG_CHECK(launch_reduce(top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1], st), false);
+        FG_CHECK(launch_reduce(top.gsp, top.rows, top.rows, T, top.nid, theta, G[2], st), false);
     }
     int cur = 0;
     for (int k = K; k >= 1; --k) {
@@ -640,29 +611,20 @@ static bool backward16(Core& c, const float* dlogits, int B) {
             rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
         }
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
-        float* gwp = (k & 1) ? c.gwpart : c.gwpart2;
-        if (k + 2 <= K) FG_CHECK(hipStreamWaitEvent(st, c.ev[1 + (k & 1)], 0), false);   // hop k+2's reductions read it
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
-            FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, gwp, d.bp.npos, e, c.part, T, st), false);
+            FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, c.gwpart, d.bp.npos, e, c.part, T, st), false);
         }
-        FG_CHECK(hipEventRecord(c.ev[0], st), false);
-        FG_CHECK(hipStreamWaitEvent(s2, c.ev[0], 0), false);
-        {
-            Timed t(c, ST_REDUCE, s2);
-            FG_CHECK(launch_reduce(gwp, d.bp.npos, d.bp.npos, T, d.bp.pidx, nullptr, G[0], s2), false);
-            FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], s2), false);
-            FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], s2), false);
-            if (k == 1) {
-                FG_CHECK(launch_reduce(c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], s2), false);
-                FG_CHECK(launch_reduce(c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], s2), false);
-            }
+        Timed t(c, ST_REDUCE);
+        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, T, d.bp.pidx, nullptr, G[0], st), false);
+        FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
+        FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
+        if (k == 1) {
+            FG_CHECK(launch_reduce(c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], st), false);
+            FG_CHECK(launch_reduce(c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], st), false);
         }
-        FG_CHECK(hipEventRecord(c.ev[1 + (k & 1)], s2), false);
         cur ^= 1;
     }
-    FG_CHECK(hipEventRecord(c.ev[3], s2), false);
-    FG_CHECK(hipStreamWaitEvent(st, c.ev[3], 0), false);
     return true;
 }
 

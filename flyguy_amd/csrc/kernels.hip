@@ -341,57 +341,81 @@ __global__ void k_reduce(const float* __restrict__ part, long long ld, long long
     G[o] += s;
 }
 
-// KL(teacher || student) per sample, dl = d(mean loss)/d logits (flyguy_train.cu:104-123).  One wave per 64 samples:
-// the samples' logits are staged through LDS with coalesced loads (and dl leaves the same way); each lane then does
-// one sample's softmax arithmetic.  Per-block sums of KL and argmax agreement go to stats_part.
-constexpr int LOSS_S = 64;
-__global__ __launch_bounds__(LOSS_S) void k_loss(const float* __restrict__ lg, const float* __restrict__ tl,
-                                                 float* __restrict__ dl, float* __restrict__ stats_part, int n_act,
-                                                 int B, float it) {
+// KL(teacher || student) per sample, dl = d(mean loss)/d logits (flyguy_train.cu:104-123).  Eight lanes per sample,
+// a workgroup of 256 threads per 32 samples: the samples' logits are staged through LDS with coalesced loads (and dl
+// leaves the same way).  Lane k of a sample's group takes actions k, k + 8, ...; the group then combines its maxima
+// (the larger value, on equal values the smaller action: the first maximum wins, as the reference's strict > does),
+// its sums of exponentials and its KL terms over the 8 lanes.  Per-block sums of KL and argmax agreement go to
+// stats_part.
+constexpr int LOSS_S = 32;
+__global__ __launch_bounds__(256) void k_loss(const float* __restrict__ lg, const float* __restrict__ tl,
+                                              float* __restrict__ dl, float* __restrict__ stats_part, int n_act, int B,
+                                              float it) {
     extern __shared__ float sm[];
     float* S = sm;                              // [LOSS_S][n_act] student logits, then dl
     float* Tt = sm + (size_t)LOSS_S * n_act;    // [LOSS_S][n_act] teacher logits * (1 / temperature)
+    __shared__ float red[2][4];
     const int b0 = blockIdx.x * LOSS_S, nb = min(LOSS_S, B - b0);
     const size_t base = (size_t)b0 * n_act;
-    for (int i = threadIdx.x; i < nb * n_act; i += LOSS_S) {
+    for (int i = threadIdx.x; i < nb * n_act; i += 256) {
         S[i] = lg[base + i];
         Tt[i] = tl[base + i] * it;
     }
     __syncthreads();
+    const int smp = threadIdx.x >> 3, sub = threadIdx.x & 7;
     float kl = 0.f, agree = 0.f;
-    if ((int)threadIdx.x < nb) {
-        float* s = S + (size_t)threadIdx.x * n_act;
-        const float* t = Tt + (size_t)threadIdx.x * n_act;
+    if (smp < nb) {                             // (whole 8-lane groups)
+        float* s = S + (size_t)smp * n_act;
+        const float* t = Tt + (size_t)smp * n_act;
         float ms = -1e30f, mt = -1e30f;
-        int as = 0, at = 0;
-        for (int a = 0; a < n_act; ++a) {
+        int as = n_act, at = n_act;
+        for (int a = sub; a < n_act; a += 8) {
             const float sv = s[a], tv = t[a];
             if (sv > ms) { ms = sv; as = a; }
             if (tv > mt) { mt = tv; at = a; }
         }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            const float vs = __shfl_xor(ms, o, 8), vt = __shfl_xor(mt, o, 8);
+            const int is = __shfl_xor(as, o, 8), jt = __shfl_xor(at, o, 8);
+            if (vs > ms || (vs == ms && is < as)) { ms = vs; as = is; }
+            if (vt > mt || (vt == mt && jt < at)) { mt = vt; at = jt; }
+        }
+        if (as == n_act) as = 0;                // (no logit above -1e30: the reference keeps action 0)
+        if (at == n_act) at = 0;
         float zs = 0.f, zt = 0.f;
-        for (int a = 0; a < n_act; ++a) {
+        for (int a = sub; a < n_act; a += 8) {
             zs += expf(s[a] - ms);
             zt += expf(t[a] - mt);
         }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            zs += __shfl_xor(zs, o, 8);
+            zt += __shfl_xor(zt, o, 8);
+        }
         const float ls = ms + logf(zs), lt = mt + logf(zt);
-        for (int a = 0; a < n_act; ++a) {
+        for (int a = sub; a < n_act; a += 8) {
             const float lps = s[a] - ls, lpt = t[a] - lt, pt = expf(lpt);
             kl += pt * (lpt - lps);
             s[a] = (expf(lps) - pt) / (float)B;
         }
-        agree = as == at ? 1.f : 0.f;
+        agree = (sub == 0 && as == at) ? 1.f : 0.f;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < nb * n_act; i += LOSS_S) dl[base + i] = S[i];
+    for (int i = threadIdx.x; i < nb * n_act; i += 256) dl[base + i] = S[i];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         kl += __shfl_xor(kl, o, 64);
         agree += __shfl_xor(agree, o, 64);
     }
-    if (threadIdx.x == 0) {
-        stats_part[2 * blockIdx.x] = kl;
-        stats_part[2 * blockIdx.x + 1] = agree;
+    if ((threadIdx.x & 63) == 0) {
+        red[0][threadIdx.x >> 6] = kl;
+        red[1][threadIdx.x >> 6] = agree;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {                     // the 4 waves' sums in wave order
+        stats_part[2 * blockIdx.x] = ((red[0][0] + red[0][1]) + red[0][2]) + red[0][3];
+        stats_part[2 * blockIdx.x + 1] = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
     }
 }
 __global__ void k_sum_pairs(const float* __restrict__ part, int n, float* __restrict__ out, int acc) {
@@ -551,7 +575,7 @@ hipError_t launch_loss(const float* lg, const float* tl, float* dl, float* stats
                        float it, hipStream_t st, bool accumulate) {
     if (n_act > 128) return hipErrorInvalidValue;       // the staged logits must fit the LDS
     const unsigned nb = blocks(B, LOSS_S);
-    k_loss<<<nb, LOSS_S, (size_t)2 * LOSS_S * n_act * sizeof(float), st>>>(lg, tl, dl, stats_part, n_act, B, it);
+    k_loss<<<nb, 256, (size_t)2 * LOSS_S * n_act * sizeof(float), st>>>(lg, tl, dl, stats_part, n_act, B, it);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     k_sum_pairs<<<1, 64, 0, st>>>(stats_part, (int)nb, stats, accumulate ? 1 : 0);
