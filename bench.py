@@ -73,6 +73,19 @@ def gather_pipe(E: int, B: int, ms: float) -> dict:
                     "pipe; the peak is a probe measurement, not a published figure"}
 
 
+def host_info() -> dict:
+    """The host the CPU baselines ran on: CPU model, logical CPUs, the CPUs this process may use, torch's threads."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            model = next((l.split(":", 1)[1].strip() for l in fh if l.startswith("model name")), "")
+    except OSError:
+        pass
+    import torch
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "torch_threads": torch.get_num_threads(), "pinning": "none (threads scheduled by the OS)"}
+
+
 def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None, dict | None]:
     import numpy as np
     from oracle import refinfer
@@ -88,6 +101,24 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
         fwd = {"value": sample / dt, "unit": "decisions/s", "cores": 1, "kind": "reference",
                "sample": f"{sample} batch-1 decisions of the same network through fly_infer.cpp (compiled from the "
                          f"reference), {dt:.1f} s"}
+        # configuration 1: batch-1 decisions one call at a time, median latency over 300 (as the bot times them), of
+        # the reference's compiled CPU forward and of this package's CPU decision library (include/fly_infer.h)
+        from flyguy_amd.cpu_decisions import CpuDecisions
+        ours = CpuDecisions(s, params)
+        one = rng.standard_normal((300, s["obs_dim"])).astype(np.float32)
+        c1 = {}
+        for who, f in (("reference", ref), ("ours", ours)):
+            f.forward(one[:5])
+            lat = []
+            for i in range(300):
+                t0 = time.perf_counter()
+                f.forward(one[i:i + 1])
+                lat.append(time.perf_counter() - t0)
+            c1[who] = {"median_ms": round(1e3 * float(np.median(lat)), 4), "p90_ms": round(1e3 * float(np.percentile(lat, 90)), 4)}
+        c1["decisions"] = 300
+        c1["workload"] = "batch-1 fp32 decision (plug, 3 hops pushing only firing neurons, read-out), one call each, 1 core"
+        fwd["config1"] = c1
+        del ours
         # the same on every host core this process may use (at most 16, a GPU's share of the host): one handle per
         # thread (a handle is not thread-safe; ctypes releases the GIL during the call), sample / 4 decisions each
         n_thr = max(1, min(16, len(os.sched_getaffinity(0))))
@@ -108,6 +139,7 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
             fwd["all_cores"] = {"value": n_thr * per / dt, "unit": "decisions/s", "cores": n_thr,
                                 "sample": f"{n_thr} threads x {per} batch-1 decisions, {dt:.1f} s"}
             del refs
+        fwd["host"] = host_info()
     train = None
     if train_batch > 0:
         from flyguy_amd.export import net_bytes

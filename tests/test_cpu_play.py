@@ -93,3 +93,28 @@ def test_viz_tap(tmp_path, monkeypatch):
     body2 = np.frombuffer(path.read_bytes()[512:], np.uint8)
     assert np.abs(body2.astype(int) - first.astype(int)).max() <= 1
     tap.close()
+
+
+@pytest.mark.skipif(not refinfer.available(), reason="the reference's CPU forward is not built here")
+@pytest.mark.parametrize("name,hops,fan", [("a", 3, 5), ("c", 4, 6)])
+def test_cpu_decisions_from_a_network_file(tmp_path, name, hops, fan):
+    """flyguy_amd.cpu_decisions.CpuDecisions on NET.bin / PARAMS.bin: the reference's compiled CPU forward's logits and
+    firing bytes, bit for bit, and the float64 oracle's logits within 1e-5."""
+    from flyguy_amd.cpu_decisions import CpuDecisions
+    from flyguy_amd.export import read_net, read_params, write_params
+    f = _actor(name, hops, fan)
+    s = structure(f)
+    P = params_from_torch(f, s)
+    (tmp_path / "net.bin").write_bytes(net_bytes(s))
+    write_params(P, tmp_path / "p.bin", 7)
+    s2 = read_net(tmp_path / "net.bin")
+    step, P2 = read_params(tmp_path / "p.bin", s2)
+    assert step == 7
+    obs = np.random.default_rng(2).standard_normal((9, 517)).astype(np.float32)
+    tap_ours, tap_ref = (np.zeros(int(sum(s["sizes"])), np.uint8) for _ in range(2))
+    got = CpuDecisions(s2, P2).forward(obs, tap_ours)
+    want = refinfer.RefInfer(s, P).forward(obs, tap_ref)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(tap_ours, tap_ref)
+    o = Oracle(net_bytes(s), P, "f64").forward(obs)
+    assert np.abs(got - o).max() <= 1e-5 * max(np.abs(o).max(), 1.0)
