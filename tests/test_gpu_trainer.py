@@ -257,6 +257,56 @@ def test_revive_matches_oracle(gpu_lib):
     assert f"| {want['still']} still silent" in report
 
 
+def test_bf16_revive_keeps_the_output(gpu_lib):
+    """fc_revive on a bfloat16-state handle: the network's output is bit-identical before and after, the silent
+    neurons are those of the library's own stored states, and every connection the surgery touches gets what the
+    rules say (a new sign into a silent neuron, zero from a silent one into a live one, gain 1 and threshold -4)."""
+    s, params, forced = _dead_case(2)
+    B, nb = 64, 2
+    core = Core(s, params, max_batch=B, flags=1)
+    rng = np.random.default_rng(6)
+    obs = rng.standard_normal((nb * B, OD)).astype(np.float32)
+    tl = (2 * rng.standard_normal((nb * B, NA))).astype(np.float32)
+    d_obs, d_tl = torch.as_tensor(obs).cuda(), torch.as_tensor(tl).cuda()
+    # the silent neurons, from the library's own stored states over the same batches
+    fired = np.zeros(s["n_neurons"], np.int64)
+    play = np.zeros(s["n_neurons"], bool)
+    sens = np.zeros(s["n_neurons"], bool)
+    sens[np.asarray(s["n0"])] = True
+    for i in range(nb):
+        core.forward(obs[i * B:(i + 1) * B])
+        for k, h in enumerate(s["hop"], start=1):
+            nid = np.asarray(h["nid"])
+            play[nid] = True
+            np.add.at(fired, nid, (core.state(k, 0, len(nid), B) > 0).sum(1))
+    dead = play & ~sens & (fired == 0)
+    before = core.forward(obs[:B])
+    rep = ctypes.create_string_buffer(1024)
+    say("bf16 fc_revive", len(forced))
+    n = call("fc_revive", core.h, d_obs.data_ptr(), d_tl.data_ptr(), B, nb, 0.4, 99991 * 5 + 3, 5, rep, 1024)
+    report = rep.value.decode()
+    say(report)
+    after = core.forward(obs[:B])
+    assert np.array_equal(before.view(np.uint32), after.view(np.uint32))
+    assert n == int(dead.sum()) and n >= len(forced)
+    W = core.get(0)[0]
+    pre, post = np.full(s["n_w"], -1), np.full(s["n_w"], -1)
+    below = np.asarray(s["n0"])
+    for h in s["hop"]:
+        nid = np.asarray(h["nid"])
+        tgt = np.repeat(np.arange(len(nid)), np.diff(h["crow"]))
+        pre[np.asarray(h["widx"])] = below[np.asarray(h["col"])]
+        post[np.asarray(h["widx"])] = nid[tgt]
+        below = nid
+    into = dead[post]
+    out_of = dead[pre] & ~into
+    assert (W[out_of] == 0).all()
+    assert np.array_equal(W[~into & ~out_of], params[0][~into & ~out_of])
+    assert (np.abs(W[into]) > 0).all()
+    gain, theta = core.get(0)[1], core.get(0)[2]
+    assert (gain[dead] == 1).all() and (theta[dead] == -4).all()
+
+
 # ---------------------------------------------------------------------------------------------------- whole runs
 def _setup(tmp_path, s, params, sizes=(50, 70, 90), seed=11):
     d = tmp_path / "data"
