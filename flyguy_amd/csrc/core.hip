@@ -488,7 +488,8 @@ bool backward(Core& c, const float* dlogits, int B) {
                                 d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st), false);
         }
         Timed t(c, ST_REDUCE);
-        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, T, d.bp.pidx, nullptr, G[0], st), false);
+        // (the float32 hop backward stores one weight-gradient partial per pair of tiles)
+        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, (T + 1) / 2, d.bp.pidx, nullptr, G[0], st), false);
         FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
         FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
         if (k == 1) {

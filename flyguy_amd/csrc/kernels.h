@@ -96,6 +96,9 @@ hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* c
 // src_rows / gz_rows: rows of the gathered state (a gather of a row outside it reads zeros)
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st);
+// gwpart: the per-position weight-gradient partials, gw_ld apart: one row per tile for the raw product (mode 0), one
+// per pair of tiles (tiles 2p and 2p + 1 summed) for the tiled layer backward (modes 1 and 2, whose hsrc must be
+// epi.h: the layer's own output)
 hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
                       float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st);
 hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStream_t st);

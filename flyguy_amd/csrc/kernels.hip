@@ -1,6 +1,7 @@
 // Kernels of the flyguy MI355X library.
 //
-// The hot loops are the gather SpMM of a hop (k_fwd) and the fused transposed pass of its backward (k_bwd).
+// The hot loops are the gather SpMM of a hop (k_fwd) and the fused transposed pass of its backward (k_bwd2, two tiles
+// per workgroup, for the library core's tiled layers; k_bwd, one tile, for the raw product of the row-major boundary).
 // Both follow a row plan (kernels.h): segments of at most seg_cap edges of one row, sorted longest first, 8 to a
 // wave.  A segment's 8 lanes each hold a float4 of the 32-sample tile and sum its edges in CSR (CSC) order, so a row
 // that is not split is summed exactly as flyguy_train.cu:88 / :171 sum it.  The (source, weight) pairs of a wave's
@@ -138,18 +139,24 @@ struct BwdIn {
 };
 // MODE (the epilogue's kind, a compile-time constant so that each kernel is straight-line code for its own case):
 // 0 the raw product, 1 a hop layer (d: the row's re-drive row), 2 the sensory layer
+// (the row's h given: a kernel that has loaded it already, from the same layer, hands it over)
 template <int MODE>
-__device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int tile, int sub) {
+__device__ __forceinline__ BwdIn bwd_inputs_h(const BwdEpi& e, int j, int d, int tile, int sub, float4 h) {
     BwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f, -1};
     if constexpr (MODE == 0) return in;
     in.d = MODE == 2 ? j : d;                              // the sensory layer's own drive gradient is complete now:
     if (in.d >= 0) in.gd = *at4u(e.gdrive, e.lgd, tile, in.d, sub);    //   every hop above has added its share
-    in.h = *at4u(e.h, e.lh, tile, j, sub);
+    in.h = h;
     if constexpr (MODE == 2) in.z = *at4u(e.z, e.lz, tile, j, sub);
     const float4 r = e.info[j];
     in.gn = r.x;
     in.sp = r.y;
     return in;
+}
+template <int MODE>
+__device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int tile, int sub) {
+    if constexpr (MODE == 0) return bwd_inputs_h<0>(e, j, d, tile, sub, splat(0.f));
+    return bwd_inputs_h<MODE>(e, j, d, tile, sub, *at4u(e.h, e.lh, tile, j, sub));
 }
 
 // gh: the gradient of this layer's output h for (row j, tile); every lane of the 8-lane group calls this
@@ -265,6 +272,81 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
         return;
     }
     bwd_finish<MODE>(epi, sg.x, tile, sub, acc, in);
+}
+
+// The same over two tiles at once, tiles 2 pr and 2 pr + 1 of a pair pr (the second may not exist): a step gathers
+// the source lines of both tiles for the same (source, weight) pairs, and the weight-gradient partial of a position is
+// summed over both tiles (tile 2 pr first) and stored once per pair: gwpart [ceil(T / 2)][gw_ld]
+template <int MODE>
+__global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw, const float* __restrict__ gz, Lay lg,
+                                             int gz_rows, const float* __restrict__ hs, Lay lhs, float* __restrict__ gwpart,
+                                             long long gw_ld, BwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB) {
+    __shared__ __align__(16) int2 slots[WG / LPR][LPR];
+    int rb;
+    const int pr = tile_of(blockIdx.x, RB, (T + 1) / 2, rb);
+    const int ta = 2 * pr, tb = 2 * pr + 1;
+    const bool hasb = tb < T;
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
+    int2 wv;
+    const bool wok = load_wave(p, w, wv);
+    const int2* q = cw + wv.x + lane;
+    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    int4 sg;
+    const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
+    float4 hja = splat(0.f), hjb = splat(0.f);
+    const Slab<true> sa(gz + (size_t)ta * lg.tile, lg.row, gz_rows, sub);
+    const Slab<true> sb(gz + (size_t)(hasb ? tb : ta) * lg.tile, lg.row, gz_rows, sub);
+    float* gwp = gwpart ? gwpart + (size_t)pr * gw_ld + wv.x + lane : nullptr;
+    float4 acca = splat(0.f), accb = splat(0.f);
+    BwdIn ina{}, inb{};
+    const bool whole = live && sg.y < 0;
+    for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
+        int c[8];
+        float wt[8];
+        stage8(slots[grp], sub, nxt, c, wt);
+        float4 va[8], vb[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) va[s] = s < left ? sa.get(c[s], sub) : splat(0.f);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) vb[s] = (hasb && s < left) ? sb.get(c[s], sub) : splat(0.f);
+        __builtin_amdgcn_sched_barrier(0);
+        if (left > 8) nxt = q[64 * (j + 1)];
+        if (j == 0) {
+            if (live) {
+                hja = *at4u(hs, lhs, ta, sg.x, sub);
+                if (hasb) hjb = *at4u(hs, lhs, tb, sg.x, sub);
+            }
+            if (whole) {                        // (hs is the layer's h: the core's launches hand over e.h)
+                ina = bwd_inputs_h<MODE>(epi, sg.x, sg.z, ta, sub, hja);
+                if (hasb) inb = bwd_inputs_h<MODE>(epi, sg.x, sg.z, tb, sub, hjb);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            fma4(wt[s], va[s], acca);
+            fma4(wt[s], vb[s], accb);
+        }
+        if (gwp) {
+            float d[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) d[s] = dot4(hja, va[s]) + dot4(hjb, vb[s]);
+            gwp[64 * j] = rs8(d, sub);
+        }
+    }
+    if (whole && !(wok && wv.y > 0)) {
+        ina = bwd_inputs<MODE>(epi, sg.x, sg.z, ta, sub);
+        if (hasb) inb = bwd_inputs<MODE>(epi, sg.x, sg.z, tb, sub);
+    }
+    if (!live) return;
+    if (sg.y >= 0) {
+        *at4w(part, lp, ta, sg.y, sub) = acca;
+        if (hasb) *at4w(part, lp, tb, sg.y, sub) = accb;
+        return;
+    }
+    bwd_finish<MODE>(epi, sg.x, ta, sub, acca, ina);
+    if (hasb) bwd_finish<MODE>(epi, sg.x, tb, sub, accb, inb);
 }
 
 template <int MODE>
@@ -521,8 +603,12 @@ static hipError_t launch_bwd_as(const Plan& p, const int2* cw, const float* gz, 
                                 hipStream_t st) {
     if (p.nwave > 0) {
         const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
-        k_bwd<TILED, MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld,
-                                                                         epi, part, lp, T, RB);
+        if constexpr (TILED && MODE != 0)       // a layer's backward: two tiles per workgroup
+            k_bwd2<MODE><<<(unsigned)((long long)((T + 1) / 2) * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs,
+                                                                                  gwpart, gw_ld, epi, part, lp, T, RB);
+        else
+            k_bwd<TILED, MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart,
+                                                                             gw_ld, epi, part, lp, T, RB);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
