@@ -24,6 +24,7 @@ struct HopD {
     int rows = 0, src = 0, E = 0;
     int *nid = nullptr, *drow = nullptr;
     bool has_drive = false;
+    bool pair_bwd = false;           // the layer's backward takes two tiles per workgroup (pair_tiles in core.hip)
     int2 *cw = nullptr, *tcw = nullptr;
     DevPlan fp, bp;
     float *h = nullptr, *ggp = nullptr, *gsp = nullptr;

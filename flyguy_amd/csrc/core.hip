@@ -13,6 +13,8 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <cstdlib>
+#include <functional>
 #include <memory>
 #include <numeric>
 #include <string>
@@ -176,6 +178,27 @@ static bool rowptr_ok(const std::vector<int>& rp, long long E) {
         if (rp[i] < rp[i - 1]) return false;
     return true;
 }
+// Whether a layer's backward takes two tiles per workgroup: it stores half the weight-gradient partials, but holds
+// two tiles' lines of the gathered gradient rows in the L2 at once.  That pays where the 16384 most gathered rows
+// (two tiles of their 128-byte lines fill an XCD's 4 MiB L2) take at least 3/4 of the gathers: 0.87-0.91 on the
+// lognormal fan-in of the benchmark networks (4% faster), 0.43-0.50 on an Erdos-Renyi control (5% slower).
+// FLYGUY_BWD_TILES=1 or 2 overrides the choice (for tests of both kernels).
+static bool pair_tiles(const std::vector<int>& crow, int rows) {
+    if (const char* f = std::getenv("FLYGUY_BWD_TILES")) {
+        if (f[0] == '1') return false;
+        if (f[0] == '2') return true;
+    }
+    const long long E = crow[rows];
+    if (E <= 0) return false;
+    std::vector<int> deg(rows);
+    for (int i = 0; i < rows; ++i) deg[i] = crow[i + 1] - crow[i];
+    const int top = std::min(rows, 16384);
+    std::nth_element(deg.begin(), deg.begin() + (top - 1), deg.end(), std::greater<int>());
+    long long s = 0;
+    for (int i = 0; i < top; ++i) s += deg[i];
+    return 4 * s >= 3 * E;
+}
+
 static bool distinct(const std::vector<int>& v, long long n, bool skip_negative) {
     std::vector<unsigned char> seen((size_t)std::max<long long>(n, 1), 0);
     for (int x : v) {
@@ -277,6 +300,7 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         if (!upload_plan(*c, f, d.rows, h.col, &h.widx, d.fp) || !upload_plan(*c, b, d.src, h.tcol, &h.twidx, d.bp))
             return nullptr;
         d.has_drive = std::any_of(h.drow.begin(), h.drow.end(), [](int v) { return v >= 0; });
+        d.pair_bwd = pair_tiles(h.crow, d.rows);
         d.nid = upload(*c, h.nid);
         d.drow = upload(*c, h.drow);
         d.cw = dalloc<int2>(*c, (size_t)d.fp.npos);
@@ -485,11 +509,11 @@ bool backward(Core& c, const float* dlogits, int B) {
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
             FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart,
-                                d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st), false);
+                                d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st, d.pair_bwd), false);
         }
         Timed t(c, ST_REDUCE);
-        // (the float32 hop backward stores one weight-gradient partial per pair of tiles)
-        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, (T + 1) / 2, d.bp.pidx, nullptr, G[0], st), false);
+        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, d.pair_bwd ? (T + 1) / 2 : T, d.bp.pidx, nullptr, G[0],
+                               st), false);
         FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
         FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
         if (k == 1) {
@@ -586,6 +610,7 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     int cur = 0;
     for (int k = K; k >= 1; --k) {
         HopD& d = c.hop[k - 1];
+        const bool pair = k >= 2 && d.pair_bwd;     // (the sensory layer's backward always takes one tile)
         BwdEpi16 e;
         e.gdrive = c.gdrive;
         e.n_s = c.n_s;
@@ -614,10 +639,12 @@ static bool backward16(Core& c, const float* dlogits, int B) {
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
-            FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, c.gwpart, d.bp.npos, e, c.part, T, st), false);
+            FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, c.gwpart, d.bp.npos, e, c.part, T, st,
+                                   pair), false);
         }
         Timed t(c, ST_REDUCE);
-        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, T, d.bp.pidx, nullptr, G[0], st), false);
+        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, pair ? (T + 1) / 2 : T, d.bp.pidx, nullptr, G[0], st),
+                 false);
         FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
         FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
         if (k == 1) {

@@ -326,6 +326,89 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
     bwd_finish16<MODE>(epi, sg.x, tile, sub, acc, in);
 }
 
+// The same over two tiles at once, tiles 2 pr and 2 pr + 1 of a pair pr (the second may not exist): a step gathers
+// the source lines of both tiles for the same (source, weight) pairs, and the weight-gradient partial of a position is
+// summed over both tiles (tile 2 pr first) and stored once per pair: gwpart [ceil(T / 2)][gw_ld]
+template <int MODE>
+__global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict__ cw, const bf16_t* __restrict__ gz,
+                                                 int gz_rows, float* __restrict__ gwpart, long long gw_ld, BwdEpi16 epi,
+                                                 float* __restrict__ part, int T, int RB) {
+    __shared__ __align__(16) int2 slots[WG / LPR][LPR];
+    int rb;
+    const int pr = tile_of(blockIdx.x, RB, (T + 1) / 2, rb);
+    const int ta = 2 * pr, tb = 2 * pr + 1;
+    const bool hasb = tb < T;
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
+    int2 wv;
+    const bool wok = load_wave(p, w, wv);
+    const int2* q = cw + wv.x + lane;
+    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    int4 sg;
+    const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(gz + (size_t)ta * gz_rows * TW16), (short)0, gz_rows * 128, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rbs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(gz + (size_t)(hasb ? tb : ta) * gz_rows * TW16), (short)0, hasb ? gz_rows * 128 : 0, 0x00020000);
+    float* gwp = gwpart ? gwpart + (size_t)pr * gw_ld + wv.x + lane : nullptr;
+    const bool whole = live && sg.y < 0;
+    u32x4 hja = {0u, 0u, 0u, 0u}, hjb = {0u, 0u, 0u, 0u};
+    float acca[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, accb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    BwdIn16 ina{}, inb{};
+    int j = 0, left = wok ? wv.y : 0;
+    auto step = [&](auto full) {
+        constexpr bool FULL = decltype(full)::value;
+        int c[8];
+        float wt[8];
+        stage8(slots[grp], sub, nxt, c, wt);
+        u32x4 va[8], vb[8];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) va[s] = (FULL || s < left) ? gather16(ra, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) vb[s] = (FULL || s < left) ? gather16(rbs, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (FULL) nxt = q[64 * (j + 1)];
+        if (j == 0) {
+            if (whole) {
+                bwd_inputs16<MODE>(epi, sg.x, sg.z, ta, sub, ina);
+                hja = ina.hr;
+                if (hasb) {
+                    bwd_inputs16<MODE>(epi, sg.x, sg.z, tb, sub, inb);
+                    hjb = inb.hr;
+                }
+            } else if (live) {
+                hja = ldr8(epi.h, epi.rows, ta, sg.x, sub);
+                if (hasb) hjb = ldr8(epi.h, epi.rows, tb, sg.x, sub);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float d[8];
+#pragma unroll
+        for (int s = 0; s < 8; s += 2)
+            if (FULL || s < left) {
+                fma_pair(wt[s], wt[s + 1], va[s], va[s + 1], acca);
+                fma_pair(wt[s], wt[s + 1], vb[s], vb[s + 1], accb);
+            }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) d[s] = (FULL || s < left) ? dot8(hja, va[s]) + dot8(hjb, vb[s]) : 0.f;
+        if (gwp) gwp[64 * j] = rs8(d, sub);
+    };
+    for (; left > 8; ++j, left -= 8) step(Full<true>{});
+    if (left > 0) step(Full<false>{});
+    if (whole && !(wok && wv.y > 0)) {
+        bwd_inputs16<MODE>(epi, sg.x, sg.z, ta, sub, ina);
+        if (hasb) bwd_inputs16<MODE>(epi, sg.x, sg.z, tb, sub, inb);
+    }
+    if (!live) return;
+    if (sg.y >= 0) {
+        store8(part + ((size_t)ta * p.nslot + sg.y) * TW16 + sub * 8, acca);
+        if (hasb) store8(part + ((size_t)tb * p.nslot + sg.y) * TW16 + sub * 8, accb);
+        return;
+    }
+    bwd_finish16<MODE>(epi, sg.x, ta, sub, acca, ina);
+    if (hasb) bwd_finish16<MODE>(epi, sg.x, tb, sub, accb, inb);
+}
+
 template <int MODE>
 __global__ __launch_bounds__(WG) void k_cbwd16_combine(Plan p, const float* __restrict__ part, BwdEpi16 epi, int T) {
     long long q = ((long long)blockIdx.x * WG + threadIdx.x);
@@ -415,10 +498,16 @@ hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* sr
 
 template <int MODE>
 static hipError_t launch_bwd16c_as(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
-                                   long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st) {
+                                   long long gw_ld, const BwdEpi16& epi, float* part, int T, bool pair, hipStream_t st) {
     if (p.nwave > 0) {
         const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
-        k_cbwd16<MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, RB);
+        // a hop layer may take two tiles per workgroup; the sensory layer's epilogue leaves no VGPRs for a second
+        if (MODE == 1 && pair)
+            k_cbwd16x2<1><<<(unsigned)((long long)((T + 1) / 2) * RB), WG, 0, st>>>(p, cw, gz, gz_rows, gwpart, gw_ld,
+                                                                                    epi, part, T, RB);
+        else
+            k_cbwd16<MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T,
+                                                                         RB);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -430,9 +519,9 @@ static hipError_t launch_bwd16c_as(const Plan& p, const int2* cw, const unsigned
 }
 
 hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
-                         long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st) {
-    if (epi.mode == 1) return launch_bwd16c_as<1>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, st);
-    if (epi.mode == 2) return launch_bwd16c_as<2>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, st);
+                         long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st, bool pair) {
+    if (epi.mode == 1) return launch_bwd16c_as<1>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, pair, st);
+    if (epi.mode == 2) return launch_bwd16c_as<2>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, false, st);
     return hipErrorInvalidValue;
 }
 

@@ -96,11 +96,12 @@ hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* c
 // src_rows / gz_rows: rows of the gathered state (a gather of a row outside it reads zeros)
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st);
-// gwpart: the per-position weight-gradient partials, gw_ld apart: one row per tile for the raw product (mode 0), one
-// per pair of tiles (tiles 2p and 2p + 1 summed) for the tiled layer backward (modes 1 and 2, whose hsrc must be
-// epi.h: the layer's own output)
+// gwpart: the per-position weight-gradient partials, gw_ld apart, one row per tile; with pair (a tiled layer backward,
+// modes 1 and 2, whose hsrc must be epi.h: the layer's own output) one row per pair of tiles (tiles 2p and 2p + 1
+// summed), ceil(T / 2) rows
 hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
-                      float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st);
+                      float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st,
+                      bool pair = false);
 hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStream_t st);
 // the read-out on the matrix cores (readout.hip): owT, n_dn x readout_pad(n_act) floats of scratch for the
 // transposed weights; hK float32 tiles of 32 or (bf16_states) bfloat16 tiles of 64
@@ -151,8 +152,10 @@ struct BwdEpi16 {
 hipError_t launch_obs_in16(const float* obs, unsigned short* x, int obs_dim, int B, hipStream_t st);
 hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* src, int src_rows, const FwdEpi16& epi,
                          float* part, int T, hipStream_t st);
+// gwpart: per-position weight-gradient partials, gw_ld apart, one row per tile; with pair (a hop layer, mode 1) one
+// row per pair of tiles, ceil(T / 2) rows (the sensory layer, mode 2, always takes one tile per workgroup)
 hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
-                         long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st);
+                         long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st, bool pair = false);
 hipError_t launch_export16(const unsigned short* src, int rows, float* dst, int B, hipStream_t st);
 hipError_t launch_readout_bwd_h16_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
                                        const BwdEpi16& epi, int B, hipStream_t st);

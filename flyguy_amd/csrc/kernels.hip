@@ -1,7 +1,8 @@
 // Kernels of the flyguy MI355X library.
 //
-// The hot loops are the gather SpMM of a hop (k_fwd) and the fused transposed pass of its backward (k_bwd2, two tiles
-// per workgroup, for the library core's tiled layers; k_bwd, one tile, for the raw product of the row-major boundary).
+// The hot loops are the gather SpMM of a hop (k_fwd) and the fused transposed pass of its backward (k_bwd, one tile
+// per workgroup; k_bwd2, two tiles, for a layer whose gathered rows are used unevenly enough that two tiles' worth of
+// the most used lines stay in the L2).
 // Both follow a row plan (kernels.h): segments of at most seg_cap edges of one row, sorted longest first, 8 to a
 // wave.  A segment's 8 lanes each hold a float4 of the 32-sample tile and sum its edges in CSR (CSC) order, so a row
 // that is not split is summed exactly as flyguy_train.cu:88 / :171 sum it.  The (source, weight) pairs of a wave's
@@ -600,15 +601,20 @@ hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, i
 template <bool TILED, int MODE>
 static hipError_t launch_bwd_as(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc,
                                 Lay lhs, float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T,
-                                hipStream_t st) {
+                                bool pair, hipStream_t st) {
     if (p.nwave > 0) {
         const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
-        if constexpr (TILED && MODE != 0)       // a layer's backward: two tiles per workgroup
-            k_bwd2<MODE><<<(unsigned)((long long)((T + 1) / 2) * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs,
-                                                                                  gwpart, gw_ld, epi, part, lp, T, RB);
-        else
+        if constexpr (TILED && MODE != 0) {
+            if (pair)                           // two tiles per workgroup
+                k_bwd2<MODE><<<(unsigned)((long long)((T + 1) / 2) * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs,
+                                                                                      gwpart, gw_ld, epi, part, lp, T, RB);
+            else
+                k_bwd<TILED, MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs,
+                                                                                 gwpart, gw_ld, epi, part, lp, T, RB);
+        } else {
             k_bwd<TILED, MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart,
                                                                              gw_ld, epi, part, lp, T, RB);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -620,18 +626,21 @@ static hipError_t launch_bwd_as(const Plan& p, const int2* cw, const float* gz, 
 }
 
 hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
-                      float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st) {
+                      float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st,
+                      bool pair) {
     const bool tiled_ = lg.row == TW;
     switch (epi.mode) {
         case 0:
-            return tiled_ ? launch_bwd_as<true, 0>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, st)
-                          : launch_bwd_as<false, 0>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, st);
+            return tiled_ ? launch_bwd_as<true, 0>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T,
+                                                   false, st)
+                          : launch_bwd_as<false, 0>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T,
+                                                    false, st);
         case 1:
             if (!tiled_) return hipErrorInvalidValue;
-            return launch_bwd_as<true, 1>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, st);
+            return launch_bwd_as<true, 1>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, pair, st);
         case 2:
             if (!tiled_) return hipErrorInvalidValue;
-            return launch_bwd_as<true, 2>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, st);
+            return launch_bwd_as<true, 2>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, pair, st);
         default:
             return hipErrorInvalidValue;
     }

@@ -95,6 +95,30 @@ def test_exact_forward_backward(gpu_lib, name, hops, fan):
         assert np.array_equal(g, w.astype(np.float32)), (n, rel(g, w))
 
 
+@pytest.mark.parametrize("tiles", ["1", "2"])
+def test_exact_one_and_two_tile_backward(gpu_lib, monkeypatch, tiles):
+    """Both hop backward kernels (one tile per workgroup, two: chosen per layer from how unevenly the gathered rows
+    are used, forced here), bit-exact at B = 192: three tiles, so the two-tile kernel also meets a lone last tile."""
+    monkeypatch.setenv("FLYGUY_BWD_TILES", tiles)
+    s, P, obs = _exact_case("b", 3, 8, 4)
+    rng = np.random.default_rng(50)
+    for i in (0, 3):                                            # denser strengths and plug weights: most gradients move
+        P[i] = (rng.choice([-1.0, 1.0, 1.0], P[i].size) * (rng.random(P[i].size) < 0.5)).astype(np.float32)
+    obs = np.concatenate([obs, -obs[::-1], np.roll(obs, 7, axis=1)])
+    say(f"bf16 exact b hops 3 fan 8, B 192, {tiles} tile(s) per backward workgroup")
+    o = Core16(s, P)
+    want = o.forward(obs)
+    for layer, (h, _) in enumerate(o.states):
+        assert np.array_equal(bf16(h), h) and np.abs(h).max() < 256, layer
+    core = Core(s, P, max_batch=192, flags=BF16)
+    assert np.array_equal(core.forward(obs), want.astype(np.float32))
+    dl = np.random.default_rng(10).choice([-1.0, 0.0, 1.0], want.shape).astype(np.float32)
+    core.zero_grad()
+    core.backward(dl)
+    for n, g, w in zip(NAMES, core.get(4), o.backward(dl)):
+        assert np.array_equal(g, w.astype(np.float32)), (n, rel(g, w))
+
+
 def test_weights_are_rounded_to_bfloat16(gpu_lib):
     """The sparse products use the strengths and plug weights rounded to bfloat16 (nearest even); the masters keep
     their float32 values.  Weights 1 + 2^-9, 1 + 2^-8 (a tie, to even: 1) and 1 - 2^-10 all round to 1, so the case

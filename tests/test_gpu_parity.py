@@ -104,6 +104,18 @@ def test_scaled_synthetic(gpu_lib, B):
     check_backward(core, o64, s, got)
 
 
+@pytest.mark.parametrize("tiles", ["1", "2"])
+def test_one_and_two_tile_backward(gpu_lib, monkeypatch, tiles):
+    """Both layer backward kernels (one tile per workgroup, two: chosen per layer from how unevenly the gathered
+    rows are used, forced here), at B = 160: five tiles, so the two-tile kernel also meets a lone last tile."""
+    monkeypatch.setenv("FLYGUY_BWD_TILES", tiles)
+    say(f"scaled synthetic 1/16, B 160, {tiles} tile(s) per backward workgroup")
+    s, params = scaled_3hop(16)
+    obs = np.random.default_rng(160).standard_normal((160, 517)).astype(np.float32)
+    core, o64, got, _ = check_forward(s, params, obs, states=False)
+    check_backward(core, o64, s, got)
+
+
 @pytest.fixture(scope="module")
 def full():
     return synth_3hop()
