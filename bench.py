@@ -334,7 +334,7 @@ def main() -> int:
 
     import numpy as np
     import torch
-    from flyguy_amd._lib import call, lib, profile_read
+    from flyguy_amd._lib import bwd_pairs, call, lib, profile_read
     from flyguy_amd.export import net_bytes
     from flyguy_amd.synth import synth_3hop
 
@@ -464,7 +464,8 @@ def main() -> int:
                   "workload": "fp32 teaching step: forward, KL(teacher||student) over 90 actions, fused backward, "
                               "Adam (lr 1e-4, betas 0.9/0.999) + running average over 2,992,734 strengths, gains, "
                               "thresholds and plugs, B=4096",
-                  "roofline": {"bound": "hbm", "kernel": "k_bwd " + dom_b, "achieved": round(ach_b / 1e9, 1),
+                  "roofline": {"bound": "hbm", "kernel": ("k_bwd2 " if bwd_pairs(s["hop"][kb]["crow"]) else "k_bwd ")
+                                                         + dom_b, "achieved": round(ach_b / 1e9, 1),
                                "peak": 8000.0, "unit": "GB/s", "frac": round(ach_b / PEAK_HBM, 4),
                                "algorithmic_bytes_per_launch": ab["hop_bwd"][kb],
                                "mean_launch_ms": round(bwd_hops[dom_b], 4),

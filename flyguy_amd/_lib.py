@@ -98,6 +98,19 @@ def seg_cap(n_edges: int) -> int:
     return int(min(256, max(16, -(-int(n_edges) // 4096))))
 
 
+def bwd_pairs(crow) -> bool:
+    """Whether the library's backward of a layer with this CSR row pointer (gathered rows: the layer's own) takes two
+    tiles per workgroup: when its 16384 most gathered rows take at least 3/4 of the gathers (core.hip:pair_tiles,
+    without its FLYGUY_BWD_TILES override)."""
+    import numpy as np
+    deg = np.diff(np.asarray(crow, np.int64))
+    E = int(deg.sum())
+    if E <= 0:
+        return False
+    top = int(np.sort(deg)[::-1][:16384].sum())
+    return 4 * top >= 3 * E
+
+
 def plan_rows(rowptr, seg_max: int | None = None) -> dict:
     """Row plan of a CSR row pointer (host only, fc_plan_rows): {"wave": int32 [nwave, 2], "seg": int32 [nseg, 4],
     "split": int32 [nsplit, 4], "nslot": int, "pos": int32 [npos]} (pos: the CSR edge of each plan position, -1 none).
