@@ -102,19 +102,22 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
                "sample": f"{sample} batch-1 decisions of the same network through fly_infer.cpp (compiled from the "
                          f"reference), {dt:.1f} s"}
         # configuration 1: batch-1 decisions one call at a time, median latency over 300 (as the bot times them), of
-        # the reference's compiled CPU forward and of this package's CPU decision library (include/fly_infer.h)
+        # the reference's compiled CPU forward and of this package's CPU decision library (include/fly_infer.h),
+        # alternating decision by decision so that both meet the same clock and cache conditions
         from flyguy_amd.cpu_decisions import CpuDecisions
         ours = CpuDecisions(s, params)
         one = rng.standard_normal((300, s["obs_dim"])).astype(np.float32)
-        c1 = {}
-        for who, f in (("reference", ref), ("ours", ours)):
+        fs = (("reference", ref), ("ours", ours))
+        lat = {who: [] for who, _ in fs}
+        for _, f in fs:
             f.forward(one[:5])
-            lat = []
-            for i in range(300):
+        for i in range(300):
+            for who, f in (fs if i % 2 == 0 else fs[::-1]):
                 t0 = time.perf_counter()
                 f.forward(one[i:i + 1])
-                lat.append(time.perf_counter() - t0)
-            c1[who] = {"median_ms": round(1e3 * float(np.median(lat)), 4), "p90_ms": round(1e3 * float(np.percentile(lat, 90)), 4)}
+                lat[who].append(time.perf_counter() - t0)
+        c1 = {who: {"median_ms": round(1e3 * float(np.median(v)), 4), "p90_ms": round(1e3 * float(np.percentile(v, 90)), 4)}
+              for who, v in lat.items()}
         c1["decisions"] = 300
         c1["workload"] = "batch-1 fp32 decision (plug, 3 hops pushing only firing neurons, read-out), one call each, 1 core"
         fwd["config1"] = c1
