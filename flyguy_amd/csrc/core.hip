@@ -473,10 +473,12 @@ bool backward(Core& c, const float* dlogits, int B) {
     const int nch = readout_chunks(B);
     {
         Timed t(c, ST_REDUCE);
-        FG_CHECK(launch_reduce(c.gow_p, (long long)c.n_act * c.n_dn, (long long)c.n_act * c.n_dn, nch, nullptr, nullptr, G[5], st), false);
-        FG_CHECK(launch_reduce(c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], st), false);
-        FG_CHECK(launch_reduce(top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1], st), false);
-        FG_CHECK(launch_reduce(top.gsp, top.rows, top.rows, T, top.nid, theta, G[2], st), false);
+        const long long now = (long long)c.n_act * c.n_dn;
+        const RedJob jobs[4] = {{c.gow_p, now, now, nch, nullptr, nullptr, G[5]},
+                                {c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6]},
+                                {top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1]},
+                                {top.gsp, top.rows, top.rows, T, top.nid, theta, G[2]}};
+        FG_CHECK(launch_reduce_n(jobs, 4, st), false);
     }
 
     int cur = 0;
@@ -512,14 +514,13 @@ bool backward(Core& c, const float* dlogits, int B) {
                                 d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st, d.pair_bwd), false);
         }
         Timed t(c, ST_REDUCE);
-        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, d.pair_bwd ? (T + 1) / 2 : T, d.bp.pidx, nullptr, G[0],
-                               st), false);
-        FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
-        FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
-        if (k == 1) {
-            FG_CHECK(launch_reduce(c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], st), false);
-            FG_CHECK(launch_reduce(c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], st), false);
-        }
+        // the layer's sums in one launch: each writes its own gradient array
+        const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, d.pair_bwd ? (T + 1) / 2 : T, d.bp.pidx, nullptr, G[0]},
+                                {ggp, rows_below, rows_below, T, nid_below, nullptr, G[1]},
+                                {gsp, rows_below, rows_below, T, nid_below, theta, G[2]},
+                                {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4]},
+                                {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3]}};
+        FG_CHECK(launch_reduce_n(jobs, k == 1 ? 5 : 3, st), false);
         cur ^= 1;
     }
     return true;
@@ -602,10 +603,12 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     const int nch = readout_chunks(B);
     {
         Timed t(c, ST_REDUCE);
-        FG_CHECK(launch_reduce(c.gow_p, (long long)c.n_act * c.n_dn, (long long)c.n_act * c.n_dn, nch, nullptr, nullptr, G[5], st), false);
-        FG_CHECK(launch_reduce(c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], st), false);
-        FG_CHECK(launch_reduce(top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1], st), false);
-        FG_CHECK(launch_reduce(top.gsp, top.rows, top.rows, T, top.nid, theta, G[2], st), false);
+        const long long now = (long long)c.n_act * c.n_dn;
+        const RedJob jobs[4] = {{c.gow_p, now, now, nch, nullptr, nullptr, G[5]},
+                                {c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6]},
+                                {top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1]},
+                                {top.gsp, top.rows, top.rows, T, top.nid, theta, G[2]}};
+        FG_CHECK(launch_reduce_n(jobs, 4, st), false);
     }
     int cur = 0;
     for (int k = K; k >= 1; --k) {
@@ -643,14 +646,13 @@ static bool backward16(Core& c, const float* dlogits, int B) {
                                    pair), false);
         }
         Timed t(c, ST_REDUCE);
-        FG_CHECK(launch_reduce(c.gwpart, d.bp.npos, d.bp.npos, pair ? (T + 1) / 2 : T, d.bp.pidx, nullptr, G[0], st),
-                 false);
-        FG_CHECK(launch_reduce(ggp, rows_below, rows_below, T, nid_below, nullptr, G[1], st), false);
-        FG_CHECK(launch_reduce(gsp, rows_below, rows_below, T, nid_below, theta, G[2], st), false);
-        if (k == 1) {
-            FG_CHECK(launch_reduce(c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], st), false);
-            FG_CHECK(launch_reduce(c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], st), false);
-        }
+        // the layer's sums in one launch: each writes its own gradient array
+        const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, pair ? (T + 1) / 2 : T, d.bp.pidx, nullptr, G[0]},
+                                {ggp, rows_below, rows_below, T, nid_below, nullptr, G[1]},
+                                {gsp, rows_below, rows_below, T, nid_below, theta, G[2]},
+                                {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4]},
+                                {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3]}};
+        FG_CHECK(launch_reduce_n(jobs, k == 1 ? 5 : 3, st), false);
         cur ^= 1;
     }
     return true;

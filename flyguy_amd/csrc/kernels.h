@@ -118,6 +118,19 @@ int readout_chunks(int B);
 // idx == nullptr: i itself.  The indices a launch names are distinct, so no two threads add to one entry.
 hipError_t launch_reduce(const float* part, long long ld, long long n, int nt, const int* idx, const float* theta,
                          float* G, hipStream_t st);
+// The same for up to RED_JOBS sums in one launch (a layer's weight, gain and threshold gradients, say).  The jobs of
+// a launch write different arrays, or different entries of one, so their order does not matter; each entry's sum is
+// the one launch_reduce forms.
+struct RedJob {
+    const float* part = nullptr;
+    long long ld = 0, n = 0;
+    int nt = 0;
+    const int* idx = nullptr;
+    const float* theta = nullptr;
+    float* G = nullptr;
+};
+constexpr int RED_JOBS = 5;
+hipError_t launch_reduce_n(const RedJob* jobs, int n, hipStream_t st);
 // The core with bfloat16 states (core16.hip): the epilogues of FwdEpi / BwdEpi on [T = B/64][rows][64] tiles, with
 // float32 tensors (partials, the drive's gradient) in the same tiling.
 struct FwdEpi16 {

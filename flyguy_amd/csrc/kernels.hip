@@ -404,24 +404,35 @@ int readout_chunks(int B) { return (B / TW + RO_CHUNK - 1) / RO_CHUNK; }
 // ------------------------------------------------------------------------------------------------ reductions
 // G[idx[i]] += sum_t part[t * ld + i]  (times -sigmoid(theta[idx[i]]) when theta is given: the threshold's gradient);
 // idx[i] < 0 (a plan position no edge uses) adds nothing
-__global__ void k_reduce(const float* __restrict__ part, long long ld, long long n, int nt, const int* __restrict__ idx,
-                         const float* __restrict__ theta, float* __restrict__ G) {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const long long o = idx ? idx[i] : i;
+struct RedJobs {
+    RedJob j[RED_JOBS];
+    long long first[RED_JOBS];       // the job's first block
+    int n;
+};
+__global__ __launch_bounds__(WG) void k_reduce(RedJobs J) {
+    const long long b = blockIdx.x;
+    RedJob r = J.j[0];
+    long long b0 = 0;
+#pragma unroll
+    for (int k = 1; k < RED_JOBS; ++k)       // (constant indices: the job table stays in the kernel arguments)
+        if (k < J.n && b >= J.first[k]) { r = J.j[k]; b0 = J.first[k]; }
+    const long long i = (b - b0) * WG + threadIdx.x;
+    if (i >= r.n) return;
+    const long long o = r.idx ? r.idx[i] : i;
     if (o < 0) return;
+    const float* __restrict__ part = r.part;
     float s = 0.f;
     int t = 0;
-    for (; t + 8 <= nt; t += 8) {              // 8 loads in flight, added in tile order
+    for (; t + 8 <= r.nt; t += 8) {          // 8 loads in flight, added in tile order
         float v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = part[(size_t)(t + k) * ld + i];
+        for (int k = 0; k < 8; ++k) v[k] = part[(size_t)(t + k) * r.ld + i];
 #pragma unroll
         for (int k = 0; k < 8; ++k) s += v[k];
     }
-    for (; t < nt; ++t) s += part[(size_t)t * ld + i];
-    if (theta) s *= -sigmoid_f(theta[o]);
-    G[o] += s;
+    for (; t < r.nt; ++t) s += part[(size_t)t * r.ld + i];
+    if (r.theta) s *= -sigmoid_f(r.theta[o]);
+    r.G[o] += s;
 }
 
 // KL(teacher || student) per sample, dl = d(mean loss)/d logits (flyguy_train.cu:104-123).  Eight lanes per sample,
@@ -659,11 +670,30 @@ hipError_t launch_readout_bwd_h_mfma(const float* dl, const float* owT, const in
     return hipGetLastError();
 }
 
+hipError_t launch_reduce_n(const RedJob* jobs, int n, hipStream_t st) {
+    if (n < 0 || n > RED_JOBS || (n > 0 && !jobs)) return hipErrorInvalidValue;
+    RedJobs J{};
+    long long nb = 0;
+    int m = 0;
+    for (int k = 0; k < n; ++k) {
+        if (jobs[k].n <= 0) continue;
+        if (!jobs[k].part || !jobs[k].G || jobs[k].nt < 0 || jobs[k].ld < jobs[k].n) return hipErrorInvalidValue;
+        J.j[m] = jobs[k];
+        J.first[m] = nb;
+        nb += blocks(jobs[k].n);
+        ++m;
+    }
+    J.n = m;
+    if (m == 0) return hipSuccess;
+    if (nb > 0xFFFFFFFFLL) return hipErrorInvalidValue;
+    k_reduce<<<(unsigned)nb, WG, 0, st>>>(J);
+    return hipGetLastError();
+}
+
 hipError_t launch_reduce(const float* part, long long ld, long long n, int nt, const int* idx, const float* theta,
                          float* G, hipStream_t st) {
-    if (n <= 0) return hipSuccess;
-    k_reduce<<<blocks(n), WG, 0, st>>>(part, ld, n, nt, idx, theta, G);
-    return hipGetLastError();
+    const RedJob j{part, ld, n, nt, idx, theta, G};
+    return launch_reduce_n(&j, 1, st);
 }
 
 hipError_t launch_loss(const float* lg, const float* tl, float* dl, float* stats_part, float* stats, int n_act, int B,
