@@ -392,9 +392,27 @@ bool check_batch(const Core* c, int B) {
 // ------------------------------------------------------------------------------------------------ passes
 // the per-row neuron records of every layer from this set's gain and theta
 static hipError_t rowinfo(Core& c, const float* gain, const float* theta) {
-    hipError_t e = launch_rowinfo(c.n0, nullptr, gain, theta, c.info0, c.n_s, c.st);
+    std::vector<RowJob> j;
+    j.push_back({c.n0, nullptr, c.info0, c.n_s});
+    for (auto& d : c.hop) j.push_back({d.nid, d.has_drive ? d.drow : nullptr, d.info, d.rows});
+    hipError_t e = hipSuccess;
+    for (size_t k = 0; k < j.size() && e == hipSuccess; k += ROW_JOBS)
+        e = launch_rowinfo_n(j.data() + k, (int)std::min<size_t>(ROW_JOBS, j.size() - k), gain, theta, c.st);
+    return e;
+}
+
+// the packed (source, weight) pairs of the forward plans (plug and hops) or of the hops' transposed plans, in launches
+// of up to PACK_JOBS plans
+static hipError_t pack(Core& c, int set, bool transposed, bool bf16w) {
+    std::vector<PackJob> j;
+    const float* W = c.arr(set, 0);
+    if (!transposed) j.push_back({c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos});
     for (auto& d : c.hop)
-        if (e == hipSuccess) e = launch_rowinfo(d.nid, d.has_drive ? d.drow : nullptr, gain, theta, d.info, d.rows, c.st);
+        j.push_back(transposed ? PackJob{d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos}
+                               : PackJob{d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos});
+    hipError_t e = hipSuccess;
+    for (size_t k = 0; k < j.size() && e == hipSuccess; k += PACK_JOBS)
+        e = launch_pack_n(j.data() + k, (int)std::min<size_t>(PACK_JOBS, j.size() - k), c.st, bf16w);
     return e;
 }
 
@@ -409,8 +427,7 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
     {
         Timed t(c, ST_PACK);
-        FG_CHECK(launch_pack(c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos, st), false);
-        for (auto& d : c.hop) FG_CHECK(launch_pack(d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos, st), false);
+        FG_CHECK(pack(c, set, false, false), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
     FwdEpi e0;
@@ -450,7 +467,7 @@ bool backward(Core& c, const float* dlogits, int B) {
     { Timed t(c, ST_ZERO); FG_CHECK(launch_fill(c.gdrive, 0.f, (long long)T * c.n_s * TW, st), false); }
     {
         Timed t(c, ST_PACK);
-        for (auto& d : c.hop) FG_CHECK(launch_pack(d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos, st), false);
+        FG_CHECK(pack(c, SET_P, true, false), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
 
@@ -537,8 +554,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
     {
         Timed t(c, ST_PACK);
-        FG_CHECK(launch_pack(c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos, st, true), false);
-        for (auto& d : c.hop) FG_CHECK(launch_pack(d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos, st, true), false);
+        FG_CHECK(pack(c, set, false, true), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
     FwdEpi16 e0;
@@ -579,7 +595,7 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     { Timed t(c, ST_ZERO); FG_CHECK(launch_fill(c.gdrive, 0.f, (long long)B * c.n_s, st), false); }
     {
         Timed t(c, ST_PACK);
-        for (auto& d : c.hop) FG_CHECK(launch_pack(d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos, st, true), false);
+        FG_CHECK(pack(c, SET_P, true, true), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
     HopD& top = c.hop[K - 1];

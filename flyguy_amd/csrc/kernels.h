@@ -93,6 +93,15 @@ struct BwdEpi {
 // rounded to bfloat16 (nearest even), as the float32 of that value (the bfloat16-state core's products)
 hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* cw, long long npos, hipStream_t st,
                        bool bf16w = false);
+// the same for up to PACK_JOBS plans in one launch
+struct PackJob {
+    const int *pcol = nullptr, *pidx = nullptr;
+    const float* w = nullptr;
+    int2* cw = nullptr;
+    long long n = 0;
+};
+constexpr int PACK_JOBS = 4;
+hipError_t launch_pack_n(const PackJob* jobs, int n, hipStream_t st, bool bf16w = false);
 // src_rows / gz_rows: rows of the gathered state (a gather of a row outside it reads zeros)
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st);
@@ -188,5 +197,13 @@ hipError_t launch_adam(float* P, const float* G, float* M, float* V, float* EMA,
 hipError_t launch_export(const float* src, Lay ls, float* dst, int rows, int B, hipStream_t st);
 hipError_t launch_rowinfo(const int* nid, const int* drow, const float* gain, const float* theta, float4* info, int rows,
                           hipStream_t st);
+// the same for up to ROW_JOBS layers in one launch
+struct RowJob {
+    const int *nid = nullptr, *drow = nullptr;
+    float4* info = nullptr;
+    int rows = 0;
+};
+constexpr int ROW_JOBS = 8;
+hipError_t launch_rowinfo_n(const RowJob* jobs, int n, const float* gain, const float* theta, hipStream_t st);
 
 }  // namespace fg

@@ -15,17 +15,52 @@
 namespace fg {
 
 // ------------------------------------------------------------------------------------------------ packing
+// Several small element-wise jobs in one launch: job k takes blocks first[k] .. first[k + 1] - 1.
+template <class J, int N>
+struct JobTable {
+    J j[N];
+    long long first[N];
+    int n;
+};
+// the job of block b and its first block (constant indices, so the table stays in the kernel arguments)
+template <class J, int N>
+__device__ __forceinline__ J job_of(const JobTable<J, N>& t, long long b, long long& b0) {
+    J r = t.j[0];
+    b0 = 0;
+#pragma unroll
+    for (int k = 1; k < N; ++k)
+        if (k < t.n && b >= t.first[k]) { r = t.j[k]; b0 = t.first[k]; }
+    return r;
+}
+// fill a table from jobs[0 .. n) (those of no elements left out); nb: the launch's blocks
+template <class J, int N, class Elems>
+static bool fill_table(JobTable<J, N>& t, const J* jobs, int n, Elems elems, long long& nb) {
+    t = JobTable<J, N>{};
+    nb = 0;
+    if (n < 0 || n > N || (n > 0 && !jobs)) return false;
+    for (int k = 0; k < n; ++k) {
+        const long long m = elems(jobs[k]);
+        if (m <= 0) continue;
+        t.j[t.n] = jobs[k];
+        t.first[t.n] = nb;
+        nb += (m + WG - 1) / WG;
+        ++t.n;
+    }
+    return nb <= 0xFFFFFFFFLL;
+}
+
 // the (source, weight) pair of every plan position, from the current weights; BF16W: the weight rounded to bfloat16
 // (nearest even), kept as the float32 of that value (low 16 bits zero)
 template <bool BF16W>
-__global__ void k_pack(const int* __restrict__ pcol, const int* __restrict__ pidx, const float* __restrict__ w,
-                       int2* __restrict__ cw, long long n) {
-    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= n) return;
-    const int i = pidx[p];
-    float v = i >= 0 ? w[i] : 0.f;
+__global__ __launch_bounds__(WG) void k_pack(JobTable<PackJob, PACK_JOBS> t) {
+    long long b0;
+    const PackJob J = job_of(t, blockIdx.x, b0);
+    const long long p = ((long long)blockIdx.x - b0) * WG + threadIdx.x;
+    if (p >= J.n) return;
+    const int i = J.pidx[p];
+    float v = i >= 0 ? J.w[i] : 0.f;
     if (BF16W) v = (float)(__bf16)v;
-    cw[p] = i >= 0 ? make_int2(pcol[p], __float_as_int(v)) : make_int2(NO_ROW, 0);
+    J.cw[p] = i >= 0 ? make_int2(J.pcol[p], __float_as_int(v)) : make_int2(NO_ROW, 0);
 }
 
 // ------------------------------------------------------------------------------------------------ forward
@@ -404,19 +439,10 @@ int readout_chunks(int B) { return (B / TW + RO_CHUNK - 1) / RO_CHUNK; }
 // ------------------------------------------------------------------------------------------------ reductions
 // G[idx[i]] += sum_t part[t * ld + i]  (times -sigmoid(theta[idx[i]]) when theta is given: the threshold's gradient);
 // idx[i] < 0 (a plan position no edge uses) adds nothing
-struct RedJobs {
-    RedJob j[RED_JOBS];
-    long long first[RED_JOBS];       // the job's first block
-    int n;
-};
-__global__ __launch_bounds__(WG) void k_reduce(RedJobs J) {
-    const long long b = blockIdx.x;
-    RedJob r = J.j[0];
-    long long b0 = 0;
-#pragma unroll
-    for (int k = 1; k < RED_JOBS; ++k)       // (constant indices: the job table stays in the kernel arguments)
-        if (k < J.n && b >= J.first[k]) { r = J.j[k]; b0 = J.first[k]; }
-    const long long i = (b - b0) * WG + threadIdx.x;
+__global__ __launch_bounds__(WG) void k_reduce(JobTable<RedJob, RED_JOBS> jt) {
+    long long b0;
+    const RedJob r = job_of(jt, blockIdx.x, b0);
+    const long long i = ((long long)blockIdx.x - b0) * WG + threadIdx.x;
     if (i >= r.n) return;
     const long long o = r.idx ? r.idx[i] : i;
     if (o < 0) return;
@@ -562,12 +588,14 @@ __global__ void k_adam(float* __restrict__ P, const float* __restrict__ G, float
 }
 
 // per row of a layer: {gain[nid], softplus(theta[nid]), re-drive row (int bits, -1 none), 0}
-__global__ void k_rowinfo(const int* __restrict__ nid, const int* __restrict__ drow, const float* __restrict__ gain,
-                          const float* __restrict__ theta, float4* __restrict__ info, int rows) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= rows) return;
-    const int n = nid[t];
-    info[t] = make_float4(gain[n], softplus_f(theta[n]), __int_as_float(drow ? drow[t] : -1), 0.f);
+__global__ __launch_bounds__(WG) void k_rowinfo(JobTable<RowJob, ROW_JOBS> t, const float* __restrict__ gain,
+                                                const float* __restrict__ theta) {
+    long long b0;
+    const RowJob J = job_of(t, blockIdx.x, b0);
+    const long long r = ((long long)blockIdx.x - b0) * WG + threadIdx.x;
+    if (r >= J.rows) return;
+    const int n = J.nid[r];
+    J.info[r] = make_float4(gain[n], softplus_f(theta[n]), __int_as_float(J.drow ? J.drow[r] : -1), 0.f);
 }
 
 // a state tensor (tiled) -> [rows][B] (tests and diagnostics)
@@ -581,14 +609,24 @@ __global__ void k_export(const float* __restrict__ src, Lay ls, float* __restric
 // ------------------------------------------------------------------------------------------------ launchers
 static inline unsigned blocks(long long n, int per = WG) { return (unsigned)((n + per - 1) / per); }
 
+hipError_t launch_pack_n(const PackJob* jobs, int n, hipStream_t st, bool bf16w) {
+    JobTable<PackJob, PACK_JOBS> t;
+    long long nb;
+    if (!fill_table(t, jobs, n, [](const PackJob& j) { return j.n; }, nb)) return hipErrorInvalidValue;
+    for (int k = 0; k < t.n; ++k)
+        if (!t.j[k].pcol || !t.j[k].pidx || !t.j[k].w || !t.j[k].cw) return hipErrorInvalidValue;
+    if (nb == 0) return hipSuccess;
+    if (bf16w)
+        k_pack<true><<<(unsigned)nb, WG, 0, st>>>(t);
+    else
+        k_pack<false><<<(unsigned)nb, WG, 0, st>>>(t);
+    return hipGetLastError();
+}
+
 hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* cw, long long npos, hipStream_t st,
                        bool bf16w) {
-    if (npos <= 0) return hipSuccess;
-    if (bf16w)
-        k_pack<true><<<blocks(npos), WG, 0, st>>>(pcol, pidx, w, cw, npos);
-    else
-        k_pack<false><<<blocks(npos), WG, 0, st>>>(pcol, pidx, w, cw, npos);
-    return hipGetLastError();
+    const PackJob j{pcol, pidx, w, cw, npos};
+    return launch_pack_n(&j, 1, st, bf16w);
 }
 
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
@@ -671,22 +709,13 @@ hipError_t launch_readout_bwd_h_mfma(const float* dl, const float* owT, const in
 }
 
 hipError_t launch_reduce_n(const RedJob* jobs, int n, hipStream_t st) {
-    if (n < 0 || n > RED_JOBS || (n > 0 && !jobs)) return hipErrorInvalidValue;
-    RedJobs J{};
-    long long nb = 0;
-    int m = 0;
-    for (int k = 0; k < n; ++k) {
-        if (jobs[k].n <= 0) continue;
-        if (!jobs[k].part || !jobs[k].G || jobs[k].nt < 0 || jobs[k].ld < jobs[k].n) return hipErrorInvalidValue;
-        J.j[m] = jobs[k];
-        J.first[m] = nb;
-        nb += blocks(jobs[k].n);
-        ++m;
-    }
-    J.n = m;
-    if (m == 0) return hipSuccess;
-    if (nb > 0xFFFFFFFFLL) return hipErrorInvalidValue;
-    k_reduce<<<(unsigned)nb, WG, 0, st>>>(J);
+    JobTable<RedJob, RED_JOBS> t;
+    long long nb;
+    if (!fill_table(t, jobs, n, [](const RedJob& j) { return j.n; }, nb)) return hipErrorInvalidValue;
+    for (int k = 0; k < t.n; ++k)
+        if (!t.j[k].part || !t.j[k].G || t.j[k].nt < 0 || t.j[k].ld < t.j[k].n) return hipErrorInvalidValue;
+    if (nb == 0) return hipSuccess;
+    k_reduce<<<(unsigned)nb, WG, 0, st>>>(t);
     return hipGetLastError();
 }
 
@@ -729,11 +758,21 @@ hipError_t launch_adam(float* P, const float* G, float* M, float* V, float* EMA,
     return hipGetLastError();
 }
 
+hipError_t launch_rowinfo_n(const RowJob* jobs, int n, const float* gain, const float* theta, hipStream_t st) {
+    JobTable<RowJob, ROW_JOBS> t;
+    long long nb;
+    if (!fill_table(t, jobs, n, [](const RowJob& j) { return (long long)j.rows; }, nb)) return hipErrorInvalidValue;
+    for (int k = 0; k < t.n; ++k)
+        if (!t.j[k].nid || !t.j[k].info) return hipErrorInvalidValue;
+    if (nb == 0) return hipSuccess;
+    k_rowinfo<<<(unsigned)nb, WG, 0, st>>>(t, gain, theta);
+    return hipGetLastError();
+}
+
 hipError_t launch_rowinfo(const int* nid, const int* drow, const float* gain, const float* theta, float4* info, int rows,
                           hipStream_t st) {
-    if (rows <= 0) return hipSuccess;
-    k_rowinfo<<<blocks(rows), WG, 0, st>>>(nid, drow, gain, theta, info, rows);
-    return hipGetLastError();
+    const RowJob j{nid, drow, info, rows};
+    return launch_rowinfo_n(&j, 1, gain, theta, st);
 }
 
 hipError_t launch_export(const float* src, Lay ls, float* dst, int rows, int B, hipStream_t st) {
