@@ -71,6 +71,7 @@ struct Core {
     float *ginb = nullptr, *ginw = nullptr, *gow_p = nullptr, *gob_p = nullptr, *stats_part = nullptr;
     float *stats = nullptr, *red = nullptr, *nrm = nullptr;
     float* owT = nullptr;            // the read-out weights transposed for the matrix cores, n_dn x readout_pad(n_act)
+    float* lpart = nullptr;          // the logits' sums over the RO_SPLIT ranges of read-out rows, RO_SPLIT x maxB x n_act
     std::vector<int> h_n0, h_dn;     // host copies: the sensory rows' neurons, the read-out rows
     bool keep_z = false;             // forward passes store every hop layer's pre-activation (surveys)
     int* scnt = nullptr;             // survey sums per row of every layer (sensory rows, then each hop's rows):

@@ -370,9 +370,10 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     c->red = dalloc<float>(*c, 1024);
     c->nrm = dalloc<float>(*c, 1);
     c->owT = dalloc<float>(*c, (size_t)c->n_dn * readout_pad(c->n_act));
+    c->lpart = dalloc<float>(*c, (size_t)RO_SPLIT * bm * c->n_act);
     if (!c->x || !c->drive || !c->h0 || !c->gdrive || !c->gz[0] || !c->gz[1] || !c->lg || !c->dl || !c->part ||
         !c->gwpart || !c->ggp0 || !c->gsp0 || !c->ginb || !c->ginw || !c->gow_p || !c->gob_p || !c->stats_part ||
-        !c->stats || !c->red || !c->nrm || !c->owT)
+        !c->stats || !c->red || !c->nrm || !c->owT || !c->lpart)
         return nullptr;
     if (hipDeviceSynchronize() != hipSuccess) { set_error("device error after set-up"); return nullptr; }
     return c.release();
@@ -451,7 +452,7 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     {
         Timed t(c, ST_LOGITS);
         FG_CHECK(launch_logits_mfma(hp, false, c.sizes[c.hops], c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, c.owT,
-                                    logits, B, st), false);
+                                    c.lpart, logits, B, st), false);
     }
     c.B = B;
     return true;
@@ -580,7 +581,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     {
         Timed t(c, ST_LOGITS);
         FG_CHECK(launch_logits_mfma(hp, true, c.sizes[c.hops], c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, c.owT,
-                                    logits, B, st), false);
+                                    c.lpart, logits, B, st), false);
     }
     c.B = B;
     return true;

@@ -527,6 +527,7 @@ hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz
 
 hipError_t launch_readout_bwd_h16_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
                                        const BwdEpi16& epi, int B, hipStream_t st) {
+    if (readout_pad(n_act) > 8 * GH_STEPS) return hipErrorInvalidValue;
     dim3 grid((unsigned)((rows + RPG - 1) / RPG), (unsigned)(B / TW16));
     k_rbwd_h16_mfma<<<grid, WG, 0, st>>>(dl, owT, readout_pad(n_act), dn_inv, n_act, rows, epi);
     return hipGetLastError();

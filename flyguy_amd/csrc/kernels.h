@@ -120,8 +120,13 @@ hipError_t launch_readout_bwd_w_mfma(const float* dl, const void* hK, bool bf16_
                                      int n_dn, int n_act, float* gow_part, float* gob_part, int B, hipStream_t st);
 hipError_t launch_readout_bwd_h_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
                                      const BwdEpi& epi, int B, hipStream_t st);
+// lpart: RO_SPLIT x B x n_act floats of scratch (the sums over each split of the read-out rows)
+constexpr int RO_SPLIT = 8;
 hipError_t launch_logits_mfma(const void* hK, bool bf16_states, int rows, const int* dn, int n_dn, const float* ow,
-                              const float* ob, int n_act, float* owT, float* logits, int B, hipStream_t st);
+                              const float* ob, int n_act, float* owT, float* lpart, float* logits, int B,
+                              hipStream_t st);
+// the read-out weights' gradient partials come per chunk of RO_CHUNK_S samples: readout_chunks(B) of them
+constexpr int RO_CHUNK_S = 128;
 int readout_chunks(int B);
 // G[idx[i]] += sum over nt tiles of part[t * ld + i] (times -sigmoid(theta[idx[i]]) if theta); idx[i] < 0: skipped,
 // idx == nullptr: i itself.  The indices a launch names are distinct, so no two threads add to one entry.

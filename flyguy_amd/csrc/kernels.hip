@@ -432,9 +432,8 @@ __global__ __launch_bounds__(WG) void k_readout_bwd_h_mfma(const float* __restri
     bwd_finish<1>(epi, t, tile, sub, acc, bwd_inputs<1>(epi, t, epi.drow ? epi.drow[t] : -1, tile, sub));
 }
 
-// per chunk of 512 samples (16 tiles): the read-out weights' gradient partials (readout.hip)
-constexpr int RO_CHUNK = 16;
-int readout_chunks(int B) { return (B / TW + RO_CHUNK - 1) / RO_CHUNK; }
+// per chunk of RO_CHUNK_S samples: the read-out weights' gradient partials (readout.hip)
+int readout_chunks(int B) { return (B + RO_CHUNK_S - 1) / RO_CHUNK_S; }
 
 // ------------------------------------------------------------------------------------------------ reductions
 // G[idx[i]] += sum_t part[t * ld + i]  (times -sigmoid(theta[idx[i]]) when theta is given: the threshold's gradient);
@@ -703,6 +702,7 @@ hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStre
 
 hipError_t launch_readout_bwd_h_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
                                      const BwdEpi& epi, int B, hipStream_t st) {
+    if (readout_pad(n_act) > 8 * GH_STEPS) return hipErrorInvalidValue;
     dim3 grid((unsigned)((rows + RPG - 1) / RPG), (unsigned)(B / TW));
     k_readout_bwd_h_mfma<<<grid, WG, 0, st>>>(dl, owT, readout_pad(n_act), dn_inv, n_act, rows, epi);
     return hipGetLastError();

@@ -10,6 +10,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // A 32 x 32 output block of an MFMA (lane l, register r) holds row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
 __device__ __forceinline__ int mfma_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
+constexpr int GH_STEPS = 16;     // MFMA steps per wave of readout_gh_block at most: 4 waves x 16 x 2 = 128 actions
 // gh of 32 rows (r0 ..) of the top layer for 32 samples (s0 ..): gh[t][c] = sum_a ow[a][j(t)] dl[s0 + c][a] with
 // j(t) = dn_inv[t] (rows without a read-out column: 0), summed over the actions on the matrix cores, the 4 waves of
 // the workgroup taking a quarter of the (padded) actions each; their partials are added in wave order into out[t][c].
@@ -21,15 +22,20 @@ __device__ __forceinline__ void readout_gh_block(const float* __restrict__ dl, c
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 31, kk = lane >> 5;
     const int t = r0 + i;
     const int j = t < rows ? dn_inv[t] : -1;
-    const int steps = ma / 2, per = (steps + 3) / 4;                 // MFMA steps (2 actions each) per wave
+    const int steps = ma / 2, per = (steps + 3) / 4;                 // MFMA steps (2 actions each) per wave: <= 16
     const int k0 = wave * per, k1 = min(steps, k0 + per);
-    f32x16 acc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int k = k0; k < k1; ++k) {
-        const int a = 2 * k + kk;
-        const float av = (j >= 0 && a < n_act) ? owT[(size_t)j * ma + a] : 0.f;
-        const float bv = a < n_act ? dl[(size_t)(s0 + i) * n_act + a] : 0.f;
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+    float av[GH_STEPS], bv[GH_STEPS];
+#pragma unroll
+    for (int u = 0; u < GH_STEPS; ++u) {                              // every load first: their latencies overlap
+        const int a = 2 * (k0 + u) + kk;
+        const bool ok = k0 + u < k1 && a < n_act;
+        av[u] = (ok && j >= 0) ? owT[(size_t)j * ma + a] : 0.f;
+        bv[u] = ok ? dl[(size_t)(s0 + i) * n_act + a] : 0.f;
     }
+    f32x16 acc = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < GH_STEPS; ++u)
+        if (k0 + u < k1) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u], bv[u], acc, 0, 0, 0);
     float* pw = part + (size_t)wave * 32 * 33;
 #pragma unroll
     for (int r = 0; r < 16; ++r) pw[mfma_row(r, lane) * 33 + i] = acc[r];

@@ -23,27 +23,31 @@ __device__ __forceinline__ float state_at(const void* hK, size_t i) {
     return reinterpret_cast<const float*>(hK)[i];
 }
 
-// grid B / 32, 512 threads (8 waves).  hK: the top layer's states, tiles of tw samples ([T][rows][tw]).  Wave w sums
-// read-out rows [w * per, (w + 1) * per) for every action block; a gathered state value feeds the 3 (ma / 32) blocks.
+// grid (B / 32, RO_SPLIT), 512 threads (8 waves).  hK: the top layer's states, tiles of tw samples ([T][rows][tw]).
+// Workgroup (b, s) takes the s-th of RO_SPLIT equal (even) ranges of the read-out rows for samples 32 b ..; wave w
+// sums the w-th eighth of that range for every action block (a gathered state value feeds the ma / 32 blocks), so a
+// wave walks about 21 rows: its chain of dependent loads stays short.  The split is fixed, so a sample's sums do not
+// depend on the batch.  lpart[s][B][n_act]: the workgroup's sum (no bias), added up by k_logits_sum.
 constexpr int RO_WAVES = 8;
 constexpr int RO_MAXB = 4;                   // action blocks of 32 a workgroup holds (n_act <= 128)
 template <bool BF16S>
 __global__ __launch_bounds__(64 * RO_WAVES) void k_logits_mfma(const void* __restrict__ hK, int rows, int tw,
                                                              const int* __restrict__ dn, int n_dn,
-                                                             const float* __restrict__ owT, int ma,
-                                                             const float* __restrict__ ob, int n_act,
-                                                             float* __restrict__ logits) {
+                                                             const float* __restrict__ owT, int ma, int n_act,
+                                                             float* __restrict__ lpart) {
     extern __shared__ int sm_dn[];                          // dn, then the partial blocks [RO_WAVES][32][33]
     float* part = reinterpret_cast<float*>(sm_dn + ((n_dn + 3) & ~3));
-    const int sb = blockIdx.x;
+    const int sb = blockIdx.x, sp = blockIdx.y, B = gridDim.x * 32;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int tile = sb * 32 / tw, col = sb * 32 % tw + (lane & 31);
     const int i = lane & 31, kk = lane >> 5;
     const int nb = ma / 32;
     for (int j = threadIdx.x; j < n_dn; j += 64 * RO_WAVES) sm_dn[j] = dn[j];
     __syncthreads();
-    const int per = ((n_dn + RO_WAVES - 1) / RO_WAVES + 1) & ~1;   // read-out rows per wave (even)
-    const int j0 = min(n_dn, wave * per), j1 = min(n_dn, j0 + per);
+    const int ps = ((n_dn + RO_SPLIT - 1) / RO_SPLIT + 1) & ~1;     // read-out rows per workgroup (even)
+    const int s0 = min(n_dn, sp * ps), s1 = min(n_dn, s0 + ps);
+    const int per = ((s1 - s0 + RO_WAVES - 1) / RO_WAVES + 1) & ~1; // ... per wave (even)
+    const int j0 = min(s1, s0 + wave * per), j1 = min(s1, j0 + per);
     const size_t base = (size_t)tile * rows * tw + col;
     f32x16 acc[RO_MAXB];
 #pragma unroll
@@ -66,7 +70,8 @@ __global__ __launch_bounds__(64 * RO_WAVES) void k_logits_mfma(const void* __res
                 if (m < nb) acc[m] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u][m], bv[u], acc[m], 0, 0, 0);
     }
     // per action block: the waves' partial blocks through LDS (lane l, register r holds action 8 (r / 4) + 4 (l / 32)
-    // + r % 4 of the block, sample l % 32), added in wave order, then the bias
+    // + r % 4 of the block, sample l % 32), added in wave order
+    float* out = lpart + (size_t)sp * B * n_act;
 #pragma unroll
     for (int m = 0; m < RO_MAXB; ++m) {
         if (m >= nb) break;
@@ -79,17 +84,29 @@ __global__ __launch_bounds__(64 * RO_WAVES) void k_logits_mfma(const void* __res
             if (a < n_act) {
                 float v = part[ai * 33 + c];
                 for (int w = 1; w < RO_WAVES; ++w) v += part[(size_t)w * 32 * 33 + ai * 33 + c];
-                logits[(size_t)(sb * 32 + c) * n_act + a] = ob[a] + v;
+                out[(size_t)(sb * 32 + c) * n_act + a] = v;
             }
         }
         __syncthreads();
     }
 }
 
-// The read-out weights' gradient per chunk of 512 samples (flyguy_train.cu:125-135):
+// logits[b][a] = ob[a] + the RO_SPLIT partial sums of k_logits_mfma, added in split order
+__global__ __launch_bounds__(WG) void k_logits_sum(const float* __restrict__ lpart, const float* __restrict__ ob,
+                                                   int n_act, long long n, float* __restrict__ logits) {
+    const long long i = (long long)blockIdx.x * WG + threadIdx.x;
+    if (i >= n) return;
+    float v = lpart[i];
+#pragma unroll
+    for (int s = 1; s < RO_SPLIT; ++s) v += lpart[(size_t)s * n + i];
+    logits[i] = ob[i % n_act] + v;
+}
+
+// The read-out weights' gradient per chunk of RO_CHUNK_S samples (flyguy_train.cu:125-135):
 //   gow_part[chunk][a][j] = sum_b dl[b][a] hK[dn[j]][b],  gob_part[chunk][a] = sum_b dl[b][a]  (b in the chunk)
-// Grid (n_dn / 32 blocks of read-out rows, chunks), 256 threads: the 4 waves each take 128 of the chunk's samples for
-// every block of 32 actions (M = actions, N = read-out rows, K = samples); partials added through LDS in wave order.
+// Grid (n_dn / 32 blocks of read-out rows, chunks), 256 threads: the 4 waves each take a quarter of the chunk's
+// samples for every block of 32 actions (M = actions, N = read-out rows, K = samples); partials added through LDS in
+// wave order.  Short chunks keep each wave's chain of dependent loads short (4 steps of 8 samples).
 template <bool BF16S>
 __global__ __launch_bounds__(WG) void k_readout_bwd_w_mfma(const float* __restrict__ dl, const void* __restrict__ hK,
                                                            int rows, int tw, const int* __restrict__ dn, int n_dn,
@@ -100,7 +117,7 @@ __global__ __launch_bounds__(WG) void k_readout_bwd_w_mfma(const float* __restri
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 31, kk = lane >> 5;
     const int nb = (n_act + 31) / 32;
     const int row = j0 + i < n_dn ? dn[j0 + i] : -1;
-    const int bs = min(B, chunk * 512 + wave * 128), be = min(B, bs + 128);
+    const int bs = min(B, chunk * RO_CHUNK_S + wave * (RO_CHUNK_S / 4)), be = min(B, bs + RO_CHUNK_S / 4);
     f32x16 acc[RO_MAXB];
 #pragma unroll
     for (int m = 0; m < RO_MAXB; ++m)
@@ -141,7 +158,8 @@ __global__ __launch_bounds__(WG) void k_readout_bwd_w_mfma(const float* __restri
     }
     if (blockIdx.x == 0 && (int)threadIdx.x < n_act) {
         float sb = 0.f;
-        for (int b = min(B, chunk * 512); b < min(B, chunk * 512 + 512); ++b) sb += dl[(size_t)b * n_act + threadIdx.x];
+        for (int b = min(B, chunk * RO_CHUNK_S); b < min(B, (chunk + 1) * RO_CHUNK_S); ++b)
+            sb += dl[(size_t)b * n_act + threadIdx.x];
         gob_part[(size_t)chunk * n_act + threadIdx.x] = sb;
     }
 }
@@ -167,20 +185,26 @@ hipError_t launch_readout_bwd_w_mfma(const float* dl, const void* hK, bool bf16_
 }
 
 hipError_t launch_logits_mfma(const void* hK, bool bf16_states, int rows, const int* dn, int n_dn, const float* ow,
-                              const float* ob, int n_act, float* owT, float* logits, int B, hipStream_t st) {
+                              const float* ob, int n_act, float* owT, float* lpart, float* logits, int B,
+                              hipStream_t st) {
     const int ma = readout_pad(n_act);
+    if (ma > 32 * RO_MAXB || B % 32 != 0) return hipErrorInvalidValue;
+    const size_t sm = (size_t)((n_dn + 3) & ~3) * sizeof(int) + (size_t)RO_WAVES * 32 * 33 * sizeof(float);
+    if (sm > 64 * 1024) return hipErrorInvalidValue;
     const long long n = (long long)n_dn * ma;
     k_owT<<<(unsigned)((n + WG - 1) / WG), WG, 0, st>>>(ow, n_act, n_dn, ma, owT);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    if (ma > 32 * RO_MAXB) return hipErrorInvalidValue;
-    const size_t sm = (size_t)((n_dn + 3) & ~3) * sizeof(int) + (size_t)RO_WAVES * 32 * 33 * sizeof(float);
-    if (sm > 64 * 1024) return hipErrorInvalidValue;
-    const unsigned grid = (unsigned)(B / 32), threads = 64 * RO_WAVES;
+    if (e != hipSuccess || B == 0) return e;
+    const dim3 grid((unsigned)(B / 32), RO_SPLIT);
+    const unsigned threads = 64 * RO_WAVES;
     if (bf16_states)
-        k_logits_mfma<true><<<grid, threads, sm, st>>>(hK, rows, TW16, dn, n_dn, owT, ma, ob, n_act, logits);
+        k_logits_mfma<true><<<grid, threads, sm, st>>>(hK, rows, TW16, dn, n_dn, owT, ma, n_act, lpart);
     else
-        k_logits_mfma<false><<<grid, threads, sm, st>>>(hK, rows, TW, dn, n_dn, owT, ma, ob, n_act, logits);
+        k_logits_mfma<false><<<grid, threads, sm, st>>>(hK, rows, TW, dn, n_dn, owT, ma, n_act, lpart);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const long long nl = (long long)B * n_act;
+    k_logits_sum<<<(unsigned)((nl + WG - 1) / WG), WG, 0, st>>>(lpart, ob, n_act, nl, logits);
     return hipGetLastError();
 }
 
