@@ -120,6 +120,23 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
               for who, v in lat.items()}
         c1["decisions"] = 300
         c1["workload"] = "batch-1 fp32 decision (plug, 3 hops pushing only firing neurons, read-out), one call each, 1 core"
+        # one decision on several host cores (fly_set_threads: bit-identical answers), up to every core this process
+        # may use (at most 16, a GPU's share of the host)
+        n_max = max(1, min(16, len(os.sched_getaffinity(0))))
+        c1["ours_threads"] = {}
+        for n_thr in sorted({n for n in (2, 4, 8, 16) if n <= n_max} | {n_max}):
+            if n_thr < 2:
+                continue
+            f = CpuDecisions(s, params, threads=n_thr)
+            f.forward(one[:20])
+            lat = []
+            for i in range(300):
+                t0 = time.perf_counter()
+                f.forward(one[i:i + 1])
+                lat.append(time.perf_counter() - t0)
+            c1["ours_threads"][str(n_thr)] = {"median_ms": round(1e3 * float(np.median(lat)), 4),
+                                              "p90_ms": round(1e3 * float(np.percentile(lat, 90)), 4)}
+            del f
         fwd["config1"] = c1
         del ours
         # the same on every host core this process may use (at most 16, a GPU's share of the host): one handle per

@@ -69,7 +69,8 @@ def build(verbose: bool = False) -> Path:
     os.replace(tmp, EXE)
     tmp = CPU_LIB.with_suffix(".so.tmp")
     # float32 sums as written: no multiply-add contraction
-    cmd = ["g++", "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall", "-ffp-contract=off", str(PKG / "csrc" / "infer_cpu.cpp"),
+    cmd = ["g++", "-O3", "-std=c++17", "-fPIC", "-shared", "-pthread", "-Wall", "-ffp-contract=off",
+           str(PKG / "csrc" / "infer_cpu.cpp"),
            "-o", str(tmp)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

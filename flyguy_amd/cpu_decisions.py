@@ -7,8 +7,8 @@ library, as flyguy/fly.py:186-241 drives it).
     logits = CpuDecisions(s, P).forward(obs)          # obs [B][obs_dim] float32 -> [B][n_act]
 
 The library is flyguy_amd/libfly_infer.so (include/fly_infer.h): the plug in CSR form, every hop by source (a hop
-pushes only the neurons that fire), thresholds softplus(theta), the read-out.  One handle per thread: a handle is not
-thread-safe.
+pushes only the neurons that fire), thresholds softplus(theta), the read-out.  threads > 1 decides each car on that
+many threads (bit-identical answers).  One handle per calling thread: a handle is not thread-safe.
 """
 from __future__ import annotations
 
@@ -31,7 +31,7 @@ class CpuDecisions:
     """The CPU decision library on a structure dict (flyguy_amd.export.structure / read_net) and the seven weight
     arrays (W, gain, theta, in_w, in_b, out_w, out_b)."""
 
-    def __init__(self, s: dict, params: list[np.ndarray], lib_path: Path | None = None):
+    def __init__(self, s: dict, params: list[np.ndarray], lib_path: Path | None = None, threads: int = 1):
         path = Path(lib_path or LIB)
         if not path.exists():
             raise FileNotFoundError(f"{path} is not built (python -c 'import __graft_entry__ as g; g.build()')")
@@ -42,6 +42,8 @@ class CpuDecisions:
         L.fly_set_out.restype, L.fly_set_out.argtypes = None, [_vp, _ci, _vp, _vp, _vp]
         L.fly_forward.restype, L.fly_forward.argtypes = None, [_vp, _vp, _ci, _vp, _vp]
         L.fly_free.restype, L.fly_free.argtypes = None, [_vp]
+        if threads != 1:
+            L.fly_set_threads.restype, L.fly_set_threads.argtypes = None, [_vp, _ci]
         self.L = L
         W, gain, theta, in_w, in_b, out_w, out_b = [np.asarray(p, np.float32).reshape(-1) for p in params]
         thr = _softplus32(theta)
@@ -64,6 +66,8 @@ class CpuDecisions:
                           ptr(gain[nid], np.float32), ptr(thr[nid], np.float32), ptr(hop["drow"], np.int32))
         L.fly_set_out(self.h, len(s["dn_rows"]), ptr(s["dn_rows"], np.int32), ptr(out_w, np.float32),
                       ptr(out_b, np.float32))
+        if threads != 1:
+            L.fly_set_threads(self.h, int(threads))
 
     def __del__(self):
         if getattr(self, "h", None):

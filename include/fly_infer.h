@@ -30,6 +30,12 @@ void fly_set_out(void* net, int n_dn, const int* dn, const float* w, const float
  * the first car, layer after layer (sensory first), 255 * tanh(1.5 * firing). */
 void fly_forward(void* net, const float* obs, int batch, float* logits, unsigned char* tap);
 
+/* An addition with no counterpart in the reference: decide each car on `threads` threads (<= 0: one per hardware
+ * thread; default 1), the calling thread among them.  Each thread owns a range of every layer's rows; the answers
+ * and tap bytes are bit-identical to one thread's.  The other threads wait for the next car, spinning for about a
+ * millisecond and then asleep; fly_free ends them. */
+void fly_set_threads(void* net, int threads);
+
 void fly_free(void* net);
 
 #ifdef __cplusplus

@@ -118,3 +118,25 @@ def test_cpu_decisions_from_a_network_file(tmp_path, name, hops, fan):
     assert np.array_equal(tap_ours, tap_ref)
     o = Oracle(net_bytes(s), P, "f64").forward(obs)
     assert np.abs(got - o).max() <= 1e-5 * max(np.abs(o).max(), 1.0)
+
+
+@pytest.mark.parametrize("name,hops,fan", [("a", 3, 5), ("c", 4, 6)])
+@pytest.mark.parametrize("threads", [2, 3, 8])
+def test_cpu_decisions_on_several_threads(name, hops, fan, threads):
+    """One car decided on several threads (fly_set_threads): the logits and firing bytes of one thread, bit for bit,
+    for several cars in a row and for batches (the threads wait between cars and between calls)."""
+    from flyguy_amd.cpu_decisions import CpuDecisions
+    f = _actor(name, hops, fan)
+    s = structure(f)
+    P = params_from_torch(f, s)
+    obs = np.random.default_rng(3).standard_normal((7, 517)).astype(np.float32)
+    one = CpuDecisions(s, P)
+    many = CpuDecisions(s, P, threads=threads)
+    for rep in range(3):
+        tap1, tapn = (np.zeros(int(sum(s["sizes"])), np.uint8) for _ in range(2))
+        want = one.forward(obs[rep:], tap1)
+        got = many.forward(obs[rep:], tapn)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rep
+        assert np.array_equal(tapn, tap1), rep
+    for i in range(len(obs)):
+        assert np.array_equal(many.forward(obs[i:i + 1]), one.forward(obs[i:i + 1]))

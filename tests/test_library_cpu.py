@@ -15,10 +15,12 @@ from flyguy_amd.fly import FlyActor
 
 
 def test_cpu_decision_library_exports():
-    """libfly_infer.so (no HIP) exports the six functions include/fly_infer.h declares (fly_infer.cpp's C-ABI)."""
+    """libfly_infer.so (no HIP) exports the functions include/fly_infer.h declares: fly_infer.cpp's six and
+    fly_set_threads (an addition)."""
     text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "fly_infer.h").read_text(), flags=re.S)
     names = sorted(set(re.findall(r"\b(fly_[a-z_]+)\s*\(", text)))
-    assert names == ["fly_create", "fly_forward", "fly_free", "fly_set_hop", "fly_set_out", "fly_set_plug"]
+    assert names == ["fly_create", "fly_forward", "fly_free", "fly_set_hop", "fly_set_out", "fly_set_plug",
+                     "fly_set_threads"]
     L = ctypes.CDLL(str(LIB_PATH.parent / "libfly_infer.so"))
     for n in names:
         assert hasattr(L, n), n
