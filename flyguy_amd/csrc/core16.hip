@@ -141,6 +141,28 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
     fwd_finish16(epi, sg.x, tile, sub, acc, in);
 }
 
+
+// acc[0..8) += the n partial sums (8 samples each, slot stride TW16 floats from p) of slots y .., in slot order, 4
+// slots' loads in flight
+__device__ __forceinline__ void add_parts16(const float* __restrict__ p, int y, int n, float acc[8]) {
+    int k = 0;
+    for (; k + 4 <= n; k += 4) {
+        float v[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ldf8(p + (size_t)(y + k + u) * TW16, v[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int m = 0; m < 8; ++m) acc[m] += v[u][m];
+    }
+    for (; k < n; ++k) {
+        float v[8];
+        ldf8(p + (size_t)(y + k) * TW16, v);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) acc[m] += v[m];
+    }
+}
+
 __global__ __launch_bounds__(WG) void k_cfwd16_combine(Plan p, const float* __restrict__ part, FwdEpi16 epi, int T) {
     long long q = ((long long)blockIdx.x * WG + threadIdx.x);
     const int sub = (int)(q & 7);
@@ -153,12 +175,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16_combine(Plan p, const float* __re
     float acc[8] = {b, b, b, b, b, b, b, b};
     FwdIn16 in{};
     fwd_inputs16(epi, s.x, s.w, tile, sub, in);
-    for (int k = 0; k < s.z; ++k) {
-        float v[8];
-        ldf8(part + ((size_t)tile * p.nslot + s.y + k) * TW16 + sub * 8, v);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) acc[m] += v[m];
-    }
+    add_parts16(part + (size_t)tile * p.nslot * TW16 + sub * 8, s.y, s.z, acc);
     fwd_finish16(epi, s.x, tile, sub, acc, in);
 }
 
@@ -421,12 +438,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16_combine(Plan p, const float* __re
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     BwdIn16 in{};
     bwd_inputs16<MODE>(epi, s.x, s.w, tile, sub, in);
-    for (int k = 0; k < s.z; ++k) {
-        float v[8];
-        ldf8(part + ((size_t)tile * p.nslot + s.y + k) * TW16 + sub * 8, v);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) acc[m] += v[m];
-    }
+    add_parts16(part + (size_t)tile * p.nslot * TW16 + sub * 8, s.y, s.z, acc);
     bwd_finish16<MODE>(epi, s.x, tile, sub, acc, in);
 }
 

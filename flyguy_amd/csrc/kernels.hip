@@ -151,6 +151,20 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
 }
 
 // split rows: partial sums in segment order, then the same finish
+// acc += the n partial sums of (slots y .., tile), in slot order, 8 loads in flight
+__device__ __forceinline__ void add_parts(const float* __restrict__ part, Lay lp, int tile, int y, int n, int sub,
+                                          float4& acc) {
+    int k = 0;
+    for (; k + 8 <= n; k += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = *at4(part, lp, tile, y + k + u, sub);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) add4(v[u], acc);
+    }
+    for (; k < n; ++k) add4(*at4(part, lp, tile, y + k, sub), acc);
+}
+
 __global__ __launch_bounds__(WG) void k_fwd_combine(Plan p, const float* __restrict__ part, Lay lp, FwdEpi epi, int T) {
     long long q = ((long long)blockIdx.x * WG + threadIdx.x);
     const int sub = (int)(q & 7);
@@ -161,7 +175,7 @@ __global__ __launch_bounds__(WG) void k_fwd_combine(Plan p, const float* __restr
     if (!load_split(p, i, s)) return;     // whole 8-lane groups leave together
     float4 acc = epi.bias ? splat(epi.bias[s.x]) : splat(0.f);
     const FwdIn in = fwd_inputs(epi, s.x, s.w, tile, sub);
-    for (int k = 0; k < s.z; ++k) add4(*at4(part, lp, tile, s.y + k, sub), acc);
+    add_parts(part, lp, tile, s.y, s.z, sub, acc);
     fwd_finish(epi, s.x, tile, sub, acc, in);
 }
 
@@ -396,7 +410,7 @@ __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restr
     if (!load_split(p, i, s)) return;     // whole 8-lane groups leave together
     float4 acc = splat(0.f);
     const BwdIn in = bwd_inputs<MODE>(epi, s.x, s.w, tile, sub);
-    for (int k = 0; k < s.z; ++k) add4(*at4(part, lp, tile, s.y + k, sub), acc);
+    add_parts(part, lp, tile, s.y, s.z, sub, acc);
     bwd_finish<MODE>(epi, s.x, tile, sub, acc, in);
 }
 
