@@ -2,7 +2,7 @@
 """Benchmark of the fly actor's batched inference and teaching step on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096]
-                    [--no-cpu] [--trainer-steps 60] [--config5-steps 10] [--config4-steps 0]
+                    [--no-cpu] [--trainer-steps 60] [--config5-steps 10] [--config4-steps 10]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -340,7 +340,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--trainer-steps", type=int, default=60, help="teaching-trainer loop steps at B=4096 (0: skip)")
     ap.add_argument("--config5-steps", type=int, default=10, help="timed bfloat16 B=16384 batches and steps (0: skip)")
-    ap.add_argument("--config4-steps", type=int, default=0,
+    ap.add_argument("--config4-steps", type=int, default=10,
                     help="timed whole-connectome B=1024 batches and steps (0: skip; its index build takes ~20 s)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 copies of 1 GiB (read 1 GiB, write 1 GiB each) so a counter run can scale "
