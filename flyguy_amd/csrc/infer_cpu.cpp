@@ -346,10 +346,17 @@ void fly_forward(void* p, const float* obs, int batch, float* logits, unsigned c
     CpuNet* n = (CpuNet*)p;
     if (!n || !n->ready() || !obs || !logits) return;
     if (n->threads > 1) {
-        if (!n->shares_ok) make_shares(*n);
-        if (!n->pool) {
-            n->pool = new Pool;
-            for (int t = 1; t < n->threads; ++t) n->pool->th.emplace_back(worker, n, t);
+        try {
+            if (!n->shares_ok) make_shares(*n);
+            if (!n->pool) {
+                n->pool = new Pool;
+                for (int t = 1; t < n->threads; ++t) n->pool->th.emplace_back(worker, n, t);
+            }
+        } catch (...) {                                    // no memory or no threads: decide on this thread alone
+            stop_pool(*n);
+            n->threads = 1;
+            n->shares_ok = false;
+            for (PushHop& h : n->hops) h.share.clear();
         }
     }
     unsigned local = n->pool ? n->pool->sense.load(std::memory_order_acquire) : 0;
