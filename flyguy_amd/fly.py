@@ -224,7 +224,8 @@ class FlyActor(nn.Module):
     def _native(self):
         """The CPU decision library (flyguy_amd/libfly_infer.so, include/fly_infer.h: a hop pushes only the neurons
         that fire), set up from the current weights (fly.py:186-241).  None when it is not built or FLYGUY_NATIVE=0:
-        then the sparse products below play."""
+        then the sparse products below play.  FLYGUY_CPU_THREADS=n decides each car on n threads (0: one per hardware
+        thread; unset: one, as the reference does), with bit-identical answers."""
         ver = (self.w._version, self.in_w._version, self.gain._version, self.theta._version, self.in_b._version,
                self.out.weight._version, self.out.bias._version, self.w.dtype)
         nat = getattr(self, "_nat", None)
@@ -270,6 +271,10 @@ class FlyActor(nn.Module):
                                 arr(drow, np.int32))
             lib.fly_set_out(h, len(self.dn_rows), arr(self.dn_rows, np.int32), arr(self.out.weight, np.float32),
                             arr(self.out.bias, np.float32))
+            threads = os.environ.get("FLYGUY_CPU_THREADS")
+            if threads is not None:
+                lib.fly_set_threads.restype, lib.fly_set_threads.argtypes = None, [vp, ci]
+                lib.fly_set_threads(h, int(threads))
         nat.update(h=h, lib=lib, shade=np.zeros(int(sum(self.sizes)), np.uint8))
         return nat
 

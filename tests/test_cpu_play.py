@@ -140,3 +140,16 @@ def test_cpu_decisions_on_several_threads(name, hops, fan, threads):
         assert np.array_equal(tapn, tap1), rep
     for i in range(len(obs)):
         assert np.array_equal(many.forward(obs[i:i + 1]), one.forward(obs[i:i + 1]))
+
+
+def test_actor_cpu_play_on_several_threads(monkeypatch):
+    """FLYGUY_CPU_THREADS: the actor's CPU play on 4 threads gives one thread's logits bit for bit."""
+    f = _actor("a", 3, 5)
+    obs = torch.as_tensor(np.random.default_rng(5).standard_normal((6, 517)).astype(np.float32))
+    with torch.no_grad():
+        one = f(obs).numpy()
+        monkeypatch.setenv("FLYGUY_CPU_THREADS", "4")
+        f.w.mul_(1.0)                                           # (a new weight version: set-up again, on 4 threads)
+        four = f(obs).numpy()
+        assert f._nat["h"]
+    assert np.array_equal(four.view(np.uint32), one.view(np.uint32))
