@@ -348,8 +348,9 @@ def main() -> int:
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
-        print(f"bench.py runs on one GPU only (asked for {max(args.gpus, world)}): this build measures the one-GPU "
-              f"share of the data-parallel path; how it shards is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for {max(args.gpus, world)}): it measures one GPU's share of "
+              f"the data-parallel path (a batch of samples); the gradient exchange between GPUs is not measured here",
+              file=sys.stderr)
         return 2
 
     import numpy as np
