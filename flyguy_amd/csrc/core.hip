@@ -284,13 +284,33 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     }
     c->in_cw = dalloc<int2>(*c, (size_t)c->pp.npos);
     long long max_slot = c->pp.nslot, max_pos = 1, max_rows = 1;
+    // The re-drive field of the transposed plans' segments, which is read by the backward only.  The backward writes
+    // the drive's gradient layer by layer from the top, so the top layer writes each of its re-drive rows first and
+    // a lower layer's row writes its re-drive row first when no layer above re-drives that row (a sensory row
+    // appears at most once per layer).  A first write starts from zero and reads nothing: its row is encoded as
+    // -(d + 3).  A sensory row that no layer re-drives reads zero: it is encoded -2 (others -1).  The gradient
+    // buffer then needs no clearing before a backward.
+    std::vector<std::vector<int>> bwd_drow(K);
+    std::vector<char> touched(c->n_s, 0);
+    for (int L = K; L >= 1; --L) {
+        const std::vector<int>& dr = hh[L - 1].drow;
+        if (L < K) {
+            bwd_drow[L - 1].resize(dr.size());
+            for (size_t r = 0; r < dr.size(); ++r)
+                bwd_drow[L - 1][r] = dr[r] >= 0 && !touched[dr[r]] ? -(dr[r] + 3) : dr[r];
+        }
+        for (int v : dr)
+            if (v >= 0) touched[v] = 1;
+    }
+    std::vector<int> sensory_drow(c->n_s);
+    for (int j = 0; j < c->n_s; ++j) sensory_drow[j] = touched[j] ? -1 : -2;
     c->hop.resize(K);
     for (int k = 0; k < K; ++k) {
         HopD& d = c->hop[k];
         HH& h = hh[k];
         d.rows = c->sizes[k + 1]; d.src = c->sizes[k]; d.E = c->E[k];
-        // the transposed plan's rows are the layer below: its re-drive rows (none for the sensory layer)
-        const int* below_drow = k >= 1 ? hh[k - 1].drow.data() : nullptr;
+        // the transposed plan's rows are the layer below, with their re-drive fields as above
+        const int* below_drow = k >= 1 ? bwd_drow[k - 1].data() : sensory_drow.data();
         HostPlan f, b;
         if (!make_plan(h.crow.data(), d.rows, seg_cap(d.E), h.drow.data(), f) ||
             !make_plan(h.tcrow.data(), d.src, seg_cap(d.E), below_drow, b)) {
@@ -465,7 +485,6 @@ bool backward(Core& c, const float* dlogits, int B) {
     const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
     float* G[7];
     for (int i = 0; i < 7; ++i) G[i] = c.arr(SET_G, i);
-    { Timed t(c, ST_ZERO); FG_CHECK(launch_fill(c.gdrive, 0.f, (long long)T * c.n_s * TW, st), false); }
     {
         Timed t(c, ST_PACK);
         FG_CHECK(pack(c, SET_P, true, false), false);
@@ -480,6 +499,7 @@ bool backward(Core& c, const float* dlogits, int B) {
     et.drow = top.has_drive ? top.drow : nullptr;
     et.gz_out = c.gz[0]; et.lgz = tiled(top.rows);
     et.gdrive = c.gdrive; et.lgd = tiled(c.n_s);
+    et.first = true;                                 // (the top layer writes each of its re-drive rows first)
     et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
     {
         Timed t(c, ST_RBWD);
@@ -593,7 +613,6 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
     float* G[7];
     for (int i = 0; i < 7; ++i) G[i] = c.arr(SET_G, i);
-    { Timed t(c, ST_ZERO); FG_CHECK(launch_fill(c.gdrive, 0.f, (long long)B * c.n_s, st), false); }
     {
         Timed t(c, ST_PACK);
         FG_CHECK(pack(c, SET_P, true, true), false);
@@ -608,6 +627,7 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     et.drow = top.has_drive ? top.drow : nullptr;
     et.gz_out = s16(c.gz[0]);
     et.gdrive = c.gdrive;
+    et.first = true;
     et.n_s = c.n_s;
     et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
     {

@@ -207,8 +207,15 @@ template <int MODE>
 __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, int tile, int sub, BwdIn16& in) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) in.z[k] = in.gd[k] = 0.f;
-    in.d = MODE == 2 ? j : d;
-    if (in.d >= 0) ldf8(f8p(e.gdrive, e.n_s, tile, in.d, sub), in.gd);
+    bool load;                               // (re-drive fields as in BwdEpi)
+    if constexpr (MODE == 2) {
+        in.d = j;
+        load = d != -2;
+    } else {
+        in.d = d <= -3 ? -d - 3 : d;
+        load = d >= 0 && !e.first;
+    }
+    if (load) ldf8(f8p(e.gdrive, e.n_s, tile, in.d, sub), in.gd);
     in.hr = ldr8(e.h, e.rows, tile, j, sub);
     if constexpr (MODE == 2) ld8(e.z, e.rows, tile, j, sub, in.z);
     const float4 r = e.info[j];

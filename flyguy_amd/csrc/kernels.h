@@ -71,8 +71,9 @@ struct BwdEpi {
     const int* drow = nullptr;    // per row: the re-drive row (-1: none), for kernels that do not follow a row plan
     float* gz_out = nullptr;      // mode 1
     Lay lgz{};
-    float* gdrive = nullptr;
-    Lay lgd{};
+    float* gdrive = nullptr;      // the drive's gradient: a re-drive row d >= 0 adds into it; -(d + 3): writes it
+    Lay lgd{};                    //   first (no load); a sensory row of re-drive field -2 reads 0 from it
+    bool first = false;           // mode 1: every re-drive row of the rows writes first (the top layer)
     float* ggain_part = nullptr;  // [T][rows]: sum over the tile of g * z
     float* gsum_part = nullptr;   // [T][rows]: sum over the tile of g
     long long gp_ld = 0;
@@ -164,7 +165,8 @@ struct BwdEpi16 {
     const float4* info = nullptr;
     const int* drow = nullptr;               // per row: re-drive row (read-out kernel only)
     unsigned short* gz_out = nullptr;        // mode 1: the layer's gz, gathered by the next backward
-    float* gdrive = nullptr;                 // float32 [T][n_s][64]
+    float* gdrive = nullptr;                 // float32 [T][n_s][64], re-drive fields as in BwdEpi
+    bool first = false;                      // as in BwdEpi
     int n_s = 0;
     float *ggain_part = nullptr, *gsum_part = nullptr;
     long long gp_ld = 0;

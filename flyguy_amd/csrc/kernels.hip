@@ -194,8 +194,17 @@ template <int MODE>
 __device__ __forceinline__ BwdIn bwd_inputs_h(const BwdEpi& e, int j, int d, int tile, int sub, float4 h) {
     BwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f, -1};
     if constexpr (MODE == 0) return in;
-    in.d = MODE == 2 ? j : d;                              // the sensory layer's own drive gradient is complete now:
-    if (in.d >= 0) in.gd = *at4u(e.gdrive, e.lgd, tile, in.d, sub);    //   every hop above has added its share
+    // the row's drive gradient so far (see BwdEpi): a first write starts from zero; the sensory layer's own is
+    // complete now (every hop above has added its share), or zero where no hop re-drives the row
+    bool load;
+    if constexpr (MODE == 2) {
+        in.d = j;
+        load = d != -2;
+    } else {
+        in.d = d <= -3 ? -d - 3 : d;
+        load = d >= 0 && !e.first;
+    }
+    if (load) in.gd = *at4u(e.gdrive, e.lgd, tile, in.d, sub);
     in.h = h;
     if constexpr (MODE == 2) in.z = *at4u(e.z, e.lz, tile, j, sub);
     const float4 r = e.info[j];
