@@ -108,7 +108,7 @@ hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, i
                       float* part, Lay lp, int T, hipStream_t st);
 // gwpart: the per-position weight-gradient partials, gw_ld apart, one row per tile; with pair (a tiled layer backward,
 // modes 1 and 2, whose hsrc must be epi.h: the layer's own output) one row per pair of tiles (tiles 2p and 2p + 1
-// summed), ceil(T / 2) rows
+// summed), ceil(T / 2) rows, and so are the rows' gain and threshold partials (epi.ggain_part, epi.gsum_part)
 hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc, Lay lhs,
                       float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T, hipStream_t st,
                       bool pair = false);

@@ -220,7 +220,10 @@ __device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int t
 
 // gh: the gradient of this layer's output h for (row j, tile); every lane of the 8-lane group calls this
 template <int MODE>
-__device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int sub, float4 gh, const BwdIn& in) {
+// keep (optional): the row's gain and threshold partials of the tile are returned there instead of stored (a kernel
+// that sums them over two tiles first)
+__device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int sub, float4 gh, const BwdIn& in,
+                                           float2* keep = nullptr) {
     if constexpr (MODE == 0) {
         *at4w(e.gh_out, e.lgh, tile, j, sub) = gh;
         return;
@@ -240,7 +243,9 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     } else {
         pg = gsum8(dot4(g, in.z));              // the sensory layer keeps its pre-activation (the drive)
     }
-    if (sub == 0) {
+    if (keep) {
+        *keep = make_float2(pg, ps);
+    } else if (sub == 0) {
         e.ggain_part[(size_t)tile * e.gp_ld + j] = pg;
         e.gsum_part[(size_t)tile * e.gp_ld + j] = ps;
     }
@@ -404,23 +409,46 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
         if (hasb) *at4w(part, lp, tb, sg.y, sub) = accb;
         return;
     }
-    bwd_finish<MODE>(epi, sg.x, ta, sub, acca, ina);
-    if (hasb) bwd_finish<MODE>(epi, sg.x, tb, sub, accb, inb);
+    float2 ka, kb = make_float2(0.f, 0.f);
+    bwd_finish<MODE>(epi, sg.x, ta, sub, acca, ina, &ka);
+    if (hasb) bwd_finish<MODE>(epi, sg.x, tb, sub, accb, inb, &kb);
+    if (sub == 0) {                             // the row's gain and threshold partials, one per pair of tiles
+        epi.ggain_part[(size_t)pr * epi.gp_ld + sg.x] = ka.x + kb.x;
+        epi.gsum_part[(size_t)pr * epi.gp_ld + sg.x] = ka.y + kb.y;
+    }
 }
 
-template <int MODE>
+// PAIR: an 8-lane group finishes the split row for both tiles of a pair (tiles 2 q and 2 q + 1, the second may not
+// exist) and stores the row's gain and threshold partials once per pair, as k_bwd2 does
+template <int MODE, bool PAIR>
 __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restrict__ part, Lay lp, BwdEpi epi, int T) {
+    const int NT = PAIR ? (T + 1) / 2 : T;
     long long q = ((long long)blockIdx.x * WG + threadIdx.x);
     const int sub = (int)(q & 7);
     q >>= 3;
-    const int tile = (int)(q % T);
-    const long long i = q / T;
+    const int u = (int)(q % NT);
+    const long long i = q / NT;
     int4 s;
     if (!load_split(p, i, s)) return;     // whole 8-lane groups leave together
-    float4 acc = splat(0.f);
-    const BwdIn in = bwd_inputs<MODE>(epi, s.x, s.w, tile, sub);
-    add_parts(part, lp, tile, s.y, s.z, sub, acc);
-    bwd_finish<MODE>(epi, s.x, tile, sub, acc, in);
+    if constexpr (!PAIR) {
+        float4 acc = splat(0.f);
+        const BwdIn in = bwd_inputs<MODE>(epi, s.x, s.w, u, sub);
+        add_parts(part, lp, u, s.y, s.z, sub, acc);
+        bwd_finish<MODE>(epi, s.x, u, sub, acc, in);
+    } else {
+        float2 k2[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
+        for (int h = 0; h < 2 && 2 * u + h < T; ++h) {
+            const int tile = 2 * u + h;
+            float4 acc = splat(0.f);
+            const BwdIn in = bwd_inputs<MODE>(epi, s.x, s.w, tile, sub);
+            add_parts(part, lp, tile, s.y, s.z, sub, acc);
+            bwd_finish<MODE>(epi, s.x, tile, sub, acc, in, &k2[h]);
+        }
+        if (sub == 0) {
+            epi.ggain_part[(size_t)u * epi.gp_ld + s.x] = k2[0].x + k2[1].x;
+            epi.gsum_part[(size_t)u * epi.gp_ld + s.x] = k2[0].y + k2[1].y;
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ obs / logits
@@ -690,7 +718,14 @@ static hipError_t launch_bwd_as(const Plan& p, const int2* cw, const float* gz, 
         if (e != hipSuccess) return e;
     }
     if (p.nsplit > 0) {
-        k_bwd_combine<MODE><<<blocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, lp, epi, T);
+        if constexpr (TILED && MODE != 0) {
+            if (pair) {
+                k_bwd_combine<MODE, true><<<blocks((long long)p.nsplit * ((T + 1) / 2) * LPR), WG, 0, st>>>(p, part, lp,
+                                                                                                            epi, T);
+                return hipGetLastError();
+            }
+        }
+        k_bwd_combine<MODE, false><<<blocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, lp, epi, T);
         return hipGetLastError();
     }
     return hipSuccess;
