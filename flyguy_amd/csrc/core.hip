@@ -685,9 +685,10 @@ static bool backward16(Core& c, const float* dlogits, int B) {
         }
         Timed t(c, ST_REDUCE);
         // the layer's sums in one launch: each writes its own gradient array
-        const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, pair ? (T + 1) / 2 : T, d.bp.pidx, nullptr, G[0]},
-                                {ggp, rows_below, rows_below, T, nid_below, nullptr, G[1]},
-                                {gsp, rows_below, rows_below, T, nid_below, theta, G[2]},
+        const int np = pair ? (T + 1) / 2 : T;        // (a two-tile backward stores its partials per pair of tiles)
+        const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, np, d.bp.pidx, nullptr, G[0]},
+                                {ggp, rows_below, rows_below, np, nid_below, nullptr, G[1]},
+                                {gsp, rows_below, rows_below, np, nid_below, theta, G[2]},
                                 {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4]},
                                 {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3]}};
         FG_CHECK(launch_reduce_n(jobs, k == 1 ? 5 : 3, st), false);

@@ -224,8 +224,9 @@ __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, in
 }
 
 template <int MODE>
+// keep (optional): the row's gain and threshold partials of the tile are returned there instead of stored
 __device__ __forceinline__ void bwd_finish16(const BwdEpi16& e, int j, int tile, int sub, const float (&gh)[8],
-                                             const BwdIn16& in) {
+                                             const BwdIn16& in, float2* keep = nullptr) {
     float g[8], gzv[8], h[8];
     float sg = 0.f, sgh = 0.f;
     unpack8<BF16>(in.hr, h);
@@ -240,7 +241,9 @@ __device__ __forceinline__ void bwd_finish16(const BwdEpi16& e, int j, int tile,
     float pg;
     if constexpr (MODE == 1) pg = in.gn != 0.f ? (gsum8(sgh) + in.sp * ps) / in.gn : 0.f;   // (see k_bwd)
     else pg = gsum8(sgh);
-    if (sub == 0) {
+    if (keep) {
+        *keep = make_float2(pg, ps);
+    } else if (sub == 0) {
         e.ggain_part[(size_t)tile * e.gp_ld + j] = pg;
         e.gsum_part[(size_t)tile * e.gp_ld + j] = ps;
     }
@@ -429,24 +432,40 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
         if (hasb) store8(part + ((size_t)tb * p.nslot + sg.y) * TW16 + sub * 8, accb);
         return;
     }
-    bwd_finish16<MODE>(epi, sg.x, ta, sub, acca, ina);
-    if (hasb) bwd_finish16<MODE>(epi, sg.x, tb, sub, accb, inb);
+    float2 ka, kb = make_float2(0.f, 0.f);
+    bwd_finish16<MODE>(epi, sg.x, ta, sub, acca, ina, &ka);
+    if (hasb) bwd_finish16<MODE>(epi, sg.x, tb, sub, accb, inb, &kb);
+    if (sub == 0) {                             // the row's gain and threshold partials, one per pair of tiles
+        epi.ggain_part[(size_t)pr * epi.gp_ld + sg.x] = ka.x + kb.x;
+        epi.gsum_part[(size_t)pr * epi.gp_ld + sg.x] = ka.y + kb.y;
+    }
 }
 
-template <int MODE>
+// PAIR: an 8-lane group finishes the split row for both tiles of a pair and stores the row's gain and threshold
+// partials once per pair, as k_cbwd16x2 does
+template <int MODE, bool PAIR>
 __global__ __launch_bounds__(WG) void k_cbwd16_combine(Plan p, const float* __restrict__ part, BwdEpi16 epi, int T) {
+    const int NT = PAIR ? (T + 1) / 2 : T;
     long long q = ((long long)blockIdx.x * WG + threadIdx.x);
     const int sub = (int)(q & 7);
     q >>= 3;
-    const int tile = (int)(q % T);
-    const long long i = q / T;
+    const int u = (int)(q % NT);
+    const long long i = q / NT;
     int4 s;
     if (!load_split(p, i, s)) return;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    BwdIn16 in{};
-    bwd_inputs16<MODE>(epi, s.x, s.w, tile, sub, in);
-    add_parts16(part + (size_t)tile * p.nslot * TW16 + sub * 8, s.y, s.z, acc);
-    bwd_finish16<MODE>(epi, s.x, tile, sub, acc, in);
+    float2 k2[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
+    for (int h = 0; h < (PAIR ? 2 : 1) && (PAIR ? 2 * u + h : u) < T; ++h) {
+        const int tile = PAIR ? 2 * u + h : u;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        BwdIn16 in{};
+        bwd_inputs16<MODE>(epi, s.x, s.w, tile, sub, in);
+        add_parts16(part + (size_t)tile * p.nslot * TW16 + sub * 8, s.y, s.z, acc);
+        bwd_finish16<MODE>(epi, s.x, tile, sub, acc, in, PAIR ? &k2[h] : nullptr);
+    }
+    if (PAIR && sub == 0) {
+        epi.ggain_part[(size_t)u * epi.gp_ld + s.x] = k2[0].x + k2[1].x;
+        epi.gsum_part[(size_t)u * epi.gp_ld + s.x] = k2[0].y + k2[1].y;
+    }
 }
 
 // ------------------------------------------------------------------------------------------------ x, read-out
@@ -531,7 +550,11 @@ static hipError_t launch_bwd16c_as(const Plan& p, const int2* cw, const unsigned
         if (e != hipSuccess) return e;
     }
     if (p.nsplit > 0) {
-        k_cbwd16_combine<MODE><<<nblocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, epi, T);
+        if (MODE == 1 && pair)
+            k_cbwd16_combine<MODE, true><<<nblocks((long long)p.nsplit * ((T + 1) / 2) * LPR), WG, 0, st>>>(p, part,
+                                                                                                          epi, T);
+        else
+            k_cbwd16_combine<MODE, false><<<nblocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, epi, T);
         return hipGetLastError();
     }
     return hipSuccess;
