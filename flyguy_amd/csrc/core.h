@@ -25,6 +25,8 @@ struct HopD {
     int *nid = nullptr, *drow = nullptr;
     bool has_drive = false;
     bool pair_bwd = false;           // the layer's backward takes two tiles per workgroup (pair_tiles in core.hip)
+    int gcols = 0;                   // the backward's gain / threshold partials of the layer below: plan columns
+    int* gidx = nullptr;             //   (segments, then split rows) and each column's neuron (-1: none)
     int2 *cw = nullptr, *tcw = nullptr;
     DevPlan fp, bp;
     float *h = nullptr, *ggp = nullptr, *gsp = nullptr;

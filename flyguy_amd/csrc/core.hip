@@ -319,6 +319,17 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         }
         if (!upload_plan(*c, f, d.rows, h.col, &h.widx, d.fp) || !upload_plan(*c, b, d.src, h.tcol, &h.twidx, d.bp))
             return nullptr;
+        {   // the backward stores the layer below's gain and threshold partials in plan columns: a whole row at its
+            // segment, split row i after the segments (coalesced stores); each column's neuron, for the reduction
+            const std::vector<int>& nid_below = k >= 1 ? c->hop[k - 1].h_nid : n0;
+            d.gcols = (int)(b.seg.size() + b.split.size());
+            std::vector<int> gidx((size_t)std::max(d.gcols, 1), -1);
+            for (size_t si = 0; si < b.seg.size(); ++si)
+                if (b.seg[si].y < 0) gidx[si] = nid_below[(size_t)b.seg[si].x];
+            for (size_t i = 0; i < b.split.size(); ++i) gidx[b.seg.size() + i] = nid_below[(size_t)b.split[i].x];
+            d.gidx = upload(*c, gidx);
+            if (!d.gidx) return nullptr;
+        }
         d.has_drive = std::any_of(h.drow.begin(), h.drow.end(), [](int v) { return v >= 0; });
         d.pair_bwd = pair_tiles(h.crow, d.rows);
         d.nid = upload(*c, h.nid);
@@ -368,8 +379,10 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     c->gz[1] = state(max_rows);
     for (auto& d : c->hop) {
         d.h = state(d.rows);
-        d.ggp = dalloc<float>(*c, Tm * d.rows);
-        d.gsp = dalloc<float>(*c, Tm * d.rows);
+        // (its partials' columns: the plan of the hop above, or the rows themselves for the top layer's read-out)
+        const size_t gc = &d != &c->hop.back() ? (size_t)std::max(d.rows, (&d + 1)->gcols) : (size_t)d.rows;
+        d.ggp = dalloc<float>(*c, Tm * gc);
+        d.gsp = dalloc<float>(*c, Tm * gc);
         d.info = dalloc<float4>(*c, d.rows);
         if (!d.h || !d.ggp || !d.gsp || !d.info) return nullptr;
     }
@@ -379,8 +392,8 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     c->dl = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->part = dalloc<float>(*c, Tm * std::max<long long>(max_slot, 1) * S);
     c->gwpart = dalloc<float>(*c, Tm * max_pos);
-    c->ggp0 = dalloc<float>(*c, Tm * c->n_s);
-    c->gsp0 = dalloc<float>(*c, Tm * c->n_s);
+    c->ggp0 = dalloc<float>(*c, Tm * (size_t)std::max(c->n_s, c->hop[0].gcols));
+    c->gsp0 = dalloc<float>(*c, Tm * (size_t)std::max(c->n_s, c->hop[0].gcols));
     c->ginb = dalloc<float>(*c, Tm * c->n_s);
     c->ginw = dalloc<float>(*c, Tm * c->E_in);
     c->gow_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act * c->n_dn);
@@ -545,7 +558,7 @@ bool backward(Core& c, const float* dlogits, int B) {
             e.ginw_part = c.ginw; e.gw_ld = c.E_in;
             hbelow = c.h0; rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
         }
-        e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
+        e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = d.gcols;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
             FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart,
@@ -555,8 +568,8 @@ bool backward(Core& c, const float* dlogits, int B) {
         // the layer's sums in one launch: each writes its own gradient array
         const int np = d.pair_bwd ? (T + 1) / 2 : T;   // (a two-tile backward stores its partials per pair of tiles)
         const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, np, d.bp.pidx, nullptr, G[0]},
-                                {ggp, rows_below, rows_below, np, nid_below, nullptr, G[1]},
-                                {gsp, rows_below, rows_below, np, nid_below, theta, G[2]},
+                                {ggp, d.gcols, d.gcols, np, d.gidx, nullptr, G[1]},
+                                {gsp, d.gcols, d.gcols, np, d.gidx, theta, G[2]},
                                 {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4]},
                                 {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3]}};
         FG_CHECK(launch_reduce_n(jobs, k == 1 ? 5 : 3, st), false);
@@ -677,7 +690,7 @@ static bool backward16(Core& c, const float* dlogits, int B) {
             e.ginw_part = c.ginw; e.gw_ld = c.E_in;
             rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
         }
-        e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = rows_below;
+        e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = d.gcols;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
             FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, c.gwpart, d.bp.npos, e, c.part, T, st,
@@ -687,8 +700,8 @@ static bool backward16(Core& c, const float* dlogits, int B) {
         // the layer's sums in one launch: each writes its own gradient array
         const int np = pair ? (T + 1) / 2 : T;        // (a two-tile backward stores its partials per pair of tiles)
         const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, np, d.bp.pidx, nullptr, G[0]},
-                                {ggp, rows_below, rows_below, np, nid_below, nullptr, G[1]},
-                                {gsp, rows_below, rows_below, np, nid_below, theta, G[2]},
+                                {ggp, d.gcols, d.gcols, np, d.gidx, nullptr, G[1]},
+                                {gsp, d.gcols, d.gcols, np, d.gidx, theta, G[2]},
                                 {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4]},
                                 {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3]}};
         FG_CHECK(launch_reduce_n(jobs, k == 1 ? 5 : 3, st), false);

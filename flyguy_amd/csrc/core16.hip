@@ -225,8 +225,9 @@ __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, in
 
 template <int MODE>
 // keep (optional): the row's gain and threshold partials of the tile are returned there instead of stored
+// gcol: as in bwd_finish
 __device__ __forceinline__ void bwd_finish16(const BwdEpi16& e, int j, int tile, int sub, const float (&gh)[8],
-                                             const BwdIn16& in, float2* keep = nullptr) {
+                                             const BwdIn16& in, float2* keep = nullptr, int gcol = -1) {
     float g[8], gzv[8], h[8];
     float sg = 0.f, sgh = 0.f;
     unpack8<BF16>(in.hr, h);
@@ -244,8 +245,9 @@ __device__ __forceinline__ void bwd_finish16(const BwdEpi16& e, int j, int tile,
     if (keep) {
         *keep = make_float2(pg, ps);
     } else if (sub == 0) {
-        e.ggain_part[(size_t)tile * e.gp_ld + j] = pg;
-        e.gsum_part[(size_t)tile * e.gp_ld + j] = ps;
+        const int col = gcol >= 0 ? gcol : j;
+        e.ggain_part[(size_t)tile * e.gp_ld + col] = pg;
+        e.gsum_part[(size_t)tile * e.gp_ld + col] = ps;
     }
     if constexpr (MODE == 1) {
         st8(e.gz_out, e.rows, tile, j, sub, gzv);
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
         store8(part + ((size_t)tile * p.nslot + sg.y) * TW16 + sub * 8, acc);
         return;
     }
-    bwd_finish16<MODE>(epi, sg.x, tile, sub, acc, in);
+    bwd_finish16<MODE>(epi, sg.x, tile, sub, acc, in, nullptr, w * 8 + (grp & 7));
 }
 
 // The same over two tiles at once, tiles 2 pr and 2 pr + 1 of a pair pr (the second may not exist): a step gathers
@@ -436,8 +438,9 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
     bwd_finish16<MODE>(epi, sg.x, ta, sub, acca, ina, &ka);
     if (hasb) bwd_finish16<MODE>(epi, sg.x, tb, sub, accb, inb, &kb);
     if (sub == 0) {                             // the row's gain and threshold partials, one per pair of tiles
-        epi.ggain_part[(size_t)pr * epi.gp_ld + sg.x] = ka.x + kb.x;
-        epi.gsum_part[(size_t)pr * epi.gp_ld + sg.x] = ka.y + kb.y;
+        const int col = w * 8 + (grp & 7);      // (the plan column of the row: its segment)
+        epi.ggain_part[(size_t)pr * epi.gp_ld + col] = ka.x + kb.x;
+        epi.gsum_part[(size_t)pr * epi.gp_ld + col] = ka.y + kb.y;
     }
 }
 
@@ -460,11 +463,11 @@ __global__ __launch_bounds__(WG) void k_cbwd16_combine(Plan p, const float* __re
         BwdIn16 in{};
         bwd_inputs16<MODE>(epi, s.x, s.w, tile, sub, in);
         add_parts16(part + (size_t)tile * p.nslot * TW16 + sub * 8, s.y, s.z, acc);
-        bwd_finish16<MODE>(epi, s.x, tile, sub, acc, in, PAIR ? &k2[h] : nullptr);
+        bwd_finish16<MODE>(epi, s.x, tile, sub, acc, in, PAIR ? &k2[h] : nullptr, (int)(p.nseg + i));
     }
     if (PAIR && sub == 0) {
-        epi.ggain_part[(size_t)u * epi.gp_ld + s.x] = k2[0].x + k2[1].x;
-        epi.gsum_part[(size_t)u * epi.gp_ld + s.x] = k2[0].y + k2[1].y;
+        epi.ggain_part[(size_t)u * epi.gp_ld + p.nseg + i] = k2[0].x + k2[1].x;
+        epi.gsum_part[(size_t)u * epi.gp_ld + p.nseg + i] = k2[0].y + k2[1].y;
     }
 }
 

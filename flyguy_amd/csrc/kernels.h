@@ -74,9 +74,9 @@ struct BwdEpi {
     float* gdrive = nullptr;      // the drive's gradient: a re-drive row d >= 0 adds into it; -(d + 3): writes it
     Lay lgd{};                    //   first (no load); a sensory row of re-drive field -2 reads 0 from it
     bool first = false;           // mode 1: every re-drive row of the rows writes first (the top layer)
-    float* ggain_part = nullptr;  // [T][rows]: sum over the tile of g * z
-    float* gsum_part = nullptr;   // [T][rows]: sum over the tile of g
-    long long gp_ld = 0;
+    float* ggain_part = nullptr;  // [T][gp_ld]: sum over the tile of g * z, in plan columns: a whole row at its
+    float* gsum_part = nullptr;   //   segment, split row i at nseg + i (the read-out kernel: the row itself);
+    long long gp_ld = 0;          //   [T][gp_ld]: sum over the tile of g
     // mode 2: the plug
     const int* in_crow = nullptr;     // the plug's CSR: connections in_crow[j] .. in_crow[j+1] of sensory row j
     const int* in_col = nullptr;      //   read observation rows in_col[f]

@@ -222,8 +222,9 @@ __device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int t
 template <int MODE>
 // keep (optional): the row's gain and threshold partials of the tile are returned there instead of stored (a kernel
 // that sums them over two tiles first)
+// gcol: the column of the row's gain and threshold partials (its plan column, see BwdEpi; -1: the row itself)
 __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int sub, float4 gh, const BwdIn& in,
-                                           float2* keep = nullptr) {
+                                           float2* keep = nullptr, int gcol = -1) {
     if constexpr (MODE == 0) {
         *at4w(e.gh_out, e.lgh, tile, j, sub) = gh;
         return;
@@ -246,8 +247,9 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     if (keep) {
         *keep = make_float2(pg, ps);
     } else if (sub == 0) {
-        e.ggain_part[(size_t)tile * e.gp_ld + j] = pg;
-        e.gsum_part[(size_t)tile * e.gp_ld + j] = ps;
+        const int col = gcol >= 0 ? gcol : j;
+        e.ggain_part[(size_t)tile * e.gp_ld + col] = pg;
+        e.gsum_part[(size_t)tile * e.gp_ld + col] = ps;
     }
     if constexpr (MODE == 1) {
         *at4uw(e.gz_out, e.lgz, tile, j, sub) = gzv;
@@ -335,7 +337,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
         *at4w(part, lp, tile, sg.y, sub) = acc;
         return;
     }
-    bwd_finish<MODE>(epi, sg.x, tile, sub, acc, in);
+    bwd_finish<MODE>(epi, sg.x, tile, sub, acc, in, nullptr, w * 8 + (grp & 7));
 }
 
 // The same over two tiles at once, tiles 2 pr and 2 pr + 1 of a pair pr (the second may not exist): a step gathers
@@ -413,8 +415,9 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
     bwd_finish<MODE>(epi, sg.x, ta, sub, acca, ina, &ka);
     if (hasb) bwd_finish<MODE>(epi, sg.x, tb, sub, accb, inb, &kb);
     if (sub == 0) {                             // the row's gain and threshold partials, one per pair of tiles
-        epi.ggain_part[(size_t)pr * epi.gp_ld + sg.x] = ka.x + kb.x;
-        epi.gsum_part[(size_t)pr * epi.gp_ld + sg.x] = ka.y + kb.y;
+        const int col = w * 8 + (grp & 7);      // (the plan column of the row: its segment)
+        epi.ggain_part[(size_t)pr * epi.gp_ld + col] = ka.x + kb.x;
+        epi.gsum_part[(size_t)pr * epi.gp_ld + col] = ka.y + kb.y;
     }
 }
 
@@ -434,7 +437,7 @@ __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restr
         float4 acc = splat(0.f);
         const BwdIn in = bwd_inputs<MODE>(epi, s.x, s.w, u, sub);
         add_parts(part, lp, u, s.y, s.z, sub, acc);
-        bwd_finish<MODE>(epi, s.x, u, sub, acc, in);
+        bwd_finish<MODE>(epi, s.x, u, sub, acc, in, nullptr, (int)(p.nseg + i));
     } else {
         float2 k2[2] = {make_float2(0.f, 0.f), make_float2(0.f, 0.f)};
         for (int h = 0; h < 2 && 2 * u + h < T; ++h) {
@@ -445,8 +448,8 @@ __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restr
             bwd_finish<MODE>(epi, s.x, tile, sub, acc, in, &k2[h]);
         }
         if (sub == 0) {
-            epi.ggain_part[(size_t)u * epi.gp_ld + s.x] = k2[0].x + k2[1].x;
-            epi.gsum_part[(size_t)u * epi.gp_ld + s.x] = k2[0].y + k2[1].y;
+            epi.ggain_part[(size_t)u * epi.gp_ld + p.nseg + i] = k2[0].x + k2[1].x;
+            epi.gsum_part[(size_t)u * epi.gp_ld + p.nseg + i] = k2[0].y + k2[1].y;
         }
     }
 }
