@@ -209,6 +209,29 @@ static bool distinct(const std::vector<int>& v, long long n, bool skip_negative)
     return true;
 }
 
+// Whether the by-source form of a hop (tcrow, tcol, twidx: per source row its connections' target rows and weight
+// indices) holds exactly the connections of its by-target form (crow, col, widx), as (target, source, weight index)
+// triples.  Both forms' weight indices are already known to be distinct and below n_w, and both hold E connections,
+// so it is enough that each by-source connection meets a by-target one of its weight index with the same target and
+// source.  The forward gathers through one form and the backward through the other: were they different graphs, the
+// gradients would belong to another network than the logits.  edge_of: scratch, n_w entries of -1 on return.
+static bool transposes(const std::vector<int>& crow, const std::vector<int>& col, const std::vector<int>& widx,
+                       const std::vector<int>& tcrow, const std::vector<int>& tcol, const std::vector<int>& twidx,
+                       int n_w, std::vector<int>& edge_of) {
+    if (edge_of.size() != (size_t)std::max(n_w, 0)) edge_of.assign((size_t)std::max(n_w, 0), -1);
+    const int srcs = (int)tcrow.size() - 1;
+    const long long E = (long long)col.size();
+    for (long long e = 0; e < E; ++e) edge_of[(size_t)widx[e]] = (int)e;      // weight index -> by-target connection
+    bool ok = tcol.size() == col.size();
+    for (int j = 0; j < srcs && ok; ++j)
+        for (int e = tcrow[j]; e < tcrow[j + 1] && ok; ++e) {
+            const int f = edge_of[(size_t)twidx[e]], r = tcol[e];           // (tcol is range-checked: a row)
+            ok = f >= 0 && col[f] == j && crow[r] <= f && f < crow[r + 1];
+        }
+    for (long long e = 0; e < E; ++e) edge_of[(size_t)widx[e]] = -1;
+    return ok;
+}
+
 Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) {
     clear_error();
     if (!bytes || len < 36 || std::memcmp(bytes, "FLY1", 4) != 0) {
@@ -255,6 +278,7 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     }
     struct HH { std::vector<int> nid, crow, col, widx, tcrow, tcol, twidx, drow; };
     std::vector<HH> hh(K);
+    std::vector<int> edge_of;                                       // (scratch of transposes())
     for (int k = 0; k < K; ++k) {
         HH& h = hh[k];
         const int rows = c->sizes[k + 1], src = c->sizes[k], E = c->E[k];
@@ -265,6 +289,11 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
                   distinct(h.widx, c->n_w, false) && rowptr_ok(h.tcrow, E) && in_range(h.tcol, 0, rows) &&
                   distinct(h.twidx, c->n_w, false) && in_range(h.drow, -1, c->n_s) && distinct(h.drow, c->n_s, true);
         if (!ok) { set_error("bad index arrays in hop " + std::to_string(k + 1)); return nullptr; }
+        if (!transposes(h.crow, h.col, h.widx, h.tcrow, h.tcol, h.twidx, c->n_w, edge_of)) {
+            set_error("hop " + std::to_string(k + 1) + ": the by-source form (tcrow, tcol, twidx) is not the transpose "
+                      "of the by-target form (crow, col, widx)");
+            return nullptr;
+        }
     }
     auto dn = r.ints(c->n_dn);
     r.ints(c->n_w);                                                 // wmap: the caller's business

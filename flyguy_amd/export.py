@@ -125,3 +125,139 @@ def read_params(path: Path, s: dict) -> tuple[int, list[np.ndarray]]:
         out.append(np.frombuffer(raw, np.float32, n, at).copy())
         at += 4 * n
     return step, out
+
+
+# ------------------------------------------------------------------------------------------------ command line
+USAGE = """python -m flyguy_amd.export COMMAND ...  (the converter of flyguy/native/export.py:91-147)
+
+  net GRAPH.npz NET.bin [--hops 3] [--fan 16] [--obs 517]
+        the network of a graph file as NET.bin, and its initial weights as NET.init.bin (a FLYP file)
+  params CKPT.pt PARAMS.bin [--graph GRAPH.npz]
+        a checkpoint's actor weights as a FLYP file (step counter 0: the trainer counts its own steps)
+  torch PARAMS.bin CKPT.pt OUT.pt [--graph GRAPH.npz]
+        a FLYP / FLYO file's weights put back into the checkpoint CKPT.pt (the strengths in play scattered into the
+        full strength array through wmap), written as OUT.pt
+  batch CKPT.pt BATCH.bin [--n 64] [--graph GRAPH.npz]
+        a fixed FLYB batch (n observations ~ 0.7 N(0,1), teacher logits ~ 2 N(0,1), torch seed 0) and the PyTorch
+        path's answer on it, printed as `flyguy_train --check NET PARAMS BATCH` prints the library's
+
+A checkpoint is read with torch.load(weights_only=True): its "model" holds the actor.* weights, and its
+config.model.fly_graph / fly_hops name the graph and hop count unless --graph / --hops are given."""
+
+ARRAY_NAMES = ("W", "gain", "theta", "in_w", "in_b", "out_w", "out_b")
+
+
+def _graph_path(p) -> str:
+    """A graph path as given on the command line: relative to the working directory when the file is there, else as
+    FlyActor resolves it (relative to the repository)."""
+    q = Path(p)
+    return str(q.resolve()) if q.exists() else str(p)
+
+
+def actor_of(ck: dict, graph: str | None = None, hops: int | None = None, fan: int = 16, obs_dim: int = 517):
+    """The FlyActor of a checkpoint dict: built on its graph, with its actor.* weights loaded."""
+    from .fly import FlyActor
+    cfg = (ck.get("config") or {}).get("model") or {}
+    g = graph or cfg.get("fly_graph")
+    if not g:
+        raise SystemExit("the checkpoint names no graph (config.model.fly_graph): give --graph")
+    weights = {k[len("actor."):]: v for k, v in ck["model"].items() if k.startswith("actor.")}
+    if "in_w" not in weights:
+        raise SystemExit("the checkpoint holds no fly actor (no actor.in_w)")
+    n_act = int(weights["out.bias"].numel()) if "out.bias" in weights else 90
+    f = FlyActor(_graph_path(g), obs_dim, n_act, hops=int(hops or cfg.get("fly_hops", 3)), fan=fan)
+    f.load_state_dict(weights, strict=False)
+    return f
+
+
+def _load(path) -> dict:
+    return torch.load(path, map_location="cpu", weights_only=True)
+
+
+def _cmd_net(a) -> str:
+    from .fly import FlyActor
+    f = FlyActor(_graph_path(a.args[0]), a.obs, 90, hops=a.hops or 3, fan=a.fan)
+    out = Path(a.args[1])
+    s = write_net(f, out)
+    write_params(params_from_torch(f, s), out.with_suffix(".init.bin"))
+    steps = sum(len(h["col"]) for h in s["hop"])
+    return (f"{out}: {s['n_w']:,} strengths in play, neurons per hop {s['sizes']}, {steps:,} connection steps; "
+            f"initial weights in {out.with_suffix('.init.bin')}")
+
+
+def _cmd_params(a) -> str:
+    ck = _load(a.args[0])
+    f = actor_of(ck, a.graph, a.hops, a.fan, a.obs)
+    write_params(params_from_torch(f, structure(f)), Path(a.args[1]), 0)
+    return f"{a.args[1]}: the weights of {a.args[0]} (trained {int(ck.get('steps', 0)):,} steps); step counter 0"
+
+
+def _cmd_torch(a) -> str:
+    params_path, ck_path, out = a.args[0], a.args[1], a.args[2]
+    ck = _load(ck_path)
+    f = actor_of(ck, a.graph, a.hops, a.fan, a.obs)
+    s = structure(f)
+    step, arrs = read_params(Path(params_path), s)
+    model = dict(ck["model"])
+    w = model["actor.w"].detach().clone()
+    w[torch.as_tensor(np.asarray(s["wmap"], np.int64))] = torch.as_tensor(arrs[0])
+    named = dict(zip(("w", "gain", "theta", "in_w", "in_b", "out.weight", "out.bias"), [w] + arrs[1:]))
+    named["out.weight"] = torch.as_tensor(named["out.weight"]).reshape(s["n_act"], s["n_dn"])
+    for k, v in named.items():
+        model["actor." + k] = torch.as_tensor(v).clone()
+    torch.save({"model": model, "steps": step, "config": ck.get("config"), "note": f"native weights of {params_path}"},
+               out)
+    return f"{out}: the weights of {params_path} (step {step:,}) in the checkpoint {ck_path}"
+
+
+def _cmd_batch(a) -> str:
+    f = actor_of(_load(a.args[0]), a.graph, a.hops, a.fan, a.obs)
+    n = a.n
+    torch.manual_seed(0)
+    x = 0.7 * torch.randn(n, f.obs_dim)
+    t = 2.0 * torch.randn(n, f.out.out_features)
+    f.zero_grad()
+    logits = f(x)
+    lt = torch.log_softmax(t, -1)
+    loss = (lt.exp() * (lt - torch.log_softmax(logits, -1))).sum(-1).mean()
+    loss.backward()
+    s = structure(f)
+    with open(a.args[1], "wb") as fh:
+        fh.write(b"FLYB" + struct.pack("<i", n) + x.numpy().astype(np.float32).tobytes() +
+                 t.numpy().astype(np.float32).tobytes())
+    grads = [f.w.grad.numpy()[np.asarray(s["wmap"], np.int64)], f.gain.grad.numpy(), f.theta.grad.numpy(),
+             f.in_w.grad.numpy(), f.in_b.grad.numpy(), f.out.weight.grad.numpy().reshape(-1), f.out.bias.grad.numpy()]
+    agree = float((logits.argmax(-1) == t.argmax(-1)).float().mean())
+    lines = [f"{a.args[1]}: {n} samples", f"torch: loss {float(loss.detach()):.6f} agree {agree:.4f}",
+             "   logits[0][:5] " + " ".join(f"{v:.6f}" for v in logits[0, :5].tolist())]
+    for name, g in zip(ARRAY_NAMES, grads):
+        g64 = g.astype(np.float64)
+        lines.append(f"   grad {name:6s} norm {float(np.sqrt((g64 * g64).sum())):.6e} sum {float(g64.sum()):+.6e}")
+    return "\n".join(lines)
+
+
+_COMMANDS = {"net": (_cmd_net, 2), "params": (_cmd_params, 2), "torch": (_cmd_torch, 3), "batch": (_cmd_batch, 2)}
+
+
+def main(argv=None) -> int:
+    import argparse
+    ap = argparse.ArgumentParser(prog="python -m flyguy_amd.export", description=USAGE,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("command", choices=sorted(_COMMANDS))
+    ap.add_argument("args", nargs="+")
+    ap.add_argument("--graph", default=None)
+    ap.add_argument("--hops", type=int, default=None)
+    ap.add_argument("--fan", type=int, default=16)
+    ap.add_argument("--obs", type=int, default=517)
+    ap.add_argument("--n", type=int, default=64)
+    a = ap.parse_args(argv)
+    fn, nargs = _COMMANDS[a.command]
+    if len(a.args) != nargs:
+        ap.error(f"{a.command} takes {nargs} paths")
+    print(fn(a), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    import sys
+    sys.exit(main())

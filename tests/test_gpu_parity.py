@@ -121,24 +121,6 @@ def full():
     return synth_3hop()
 
 
-def test_whole_connectome_against_oracle(gpu_lib):
-    """The whole-connectome case: a synthetic graph of 166,700 neurons and 15,283,167 connections (lognormal(1.8)
-    in-degree), indexed by FlyActor as the reference indexes a graph file (hops of 1.55M, 6.0M and 121k
-    connections, 6.76M strengths in play), its initial weights; B = 64."""
-    from flyguy_amd.synth import whole_connectome
-    say("whole connectome: graph and index")
-    torch.manual_seed(0)
-    f = FlyActor(whole_connectome(), 517, 90, hops=3, fan=16)
-    s = structure(f)
-    params = params_from_torch(f, s)
-    assert s["n_neurons"] == 166_700 and f.n_conn == 15_283_167
-    say(f"   hops {[len(h['col']) for h in s['hop']]}, strengths {s['n_w']:,}")
-    obs = np.random.default_rng(21).standard_normal((64, 517)).astype(np.float32)
-    core, o64, got, _ = check_forward(s, params, obs, states=True)
-    say("whole connectome: backward")
-    check_backward(core, o64, s, got)
-
-
 def test_full_size_against_oracle(gpu_lib, full):
     """The benchmark network (70k neurons in 3 hops, 2,992,734 strengths) at B = 64."""
     s, params = full

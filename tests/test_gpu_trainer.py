@@ -494,3 +494,44 @@ def test_check_mode_matches_oracle(gpu_lib, tmp_path):
         n0 = float(np.linalg.norm(g.astype(np.float64)))
         assert abs(norm - n0) <= 1e-4 * max(n0, 1e-12) + 1e-9, (name, norm, n0)
         assert abs(tot - float(g.astype(np.float64).sum())) <= 1e-4 * float(np.abs(g).sum()) + 1e-9, name
+
+
+def test_export_batch_then_check(gpu_lib, tmp_path):
+    """The reference's workflow for checking the library against PyTorch (export.py net / params / batch, then
+    flyguy_train --check NET PARAMS BATCH): the library's loss, first logits and gradient norms and sums agree with
+    the PyTorch path's, as the converter printed them."""
+    from conftest import GOLDEN
+    from flyguy_amd.export import main as export_main
+    graph = GOLDEN / "toy_b.npz"
+    torch.manual_seed(4)
+    f = lively(FlyActor(str(graph), OD, NA, hops=3, fan=16), 4)
+    ck = {"model": {"actor." + k: v.detach().clone() for k, v in f.state_dict().items()},
+          "config": {"model": {"fly_graph": str(graph), "fly_hops": 3}}}
+    torch.save(ck, tmp_path / "ck.pt")
+    net, p, b = tmp_path / "net.bin", tmp_path / "p.bin", tmp_path / "batch.bin"
+    import contextlib
+    import io
+    torch.manual_seed(4)
+    assert export_main(["net", str(graph), str(net), "--hops", "3", "--fan", "16"]) == 0
+    assert export_main(["params", str(tmp_path / "ck.pt"), str(p)]) == 0
+    out = io.StringIO()
+    with contextlib.redirect_stdout(out):
+        assert export_main(["batch", str(tmp_path / "ck.pt"), str(b), "--n", "64"]) == 0
+    ref = out.getvalue()
+    exe = lib()._name.replace("libflyguy_core.so", "flyguy_train")
+    say("export batch -> flyguy_train --check")
+    r = subprocess.run([exe, "--check", net, p, b], capture_output=True, text=True, timeout=120)
+    say(ref, r.stdout, r.stderr)
+    assert r.returncode == 0
+    lt = float(re.search(r"torch: loss ([-0-9.e+]+)", ref).group(1))
+    ln = float(re.search(r"native: loss ([-0-9.e+]+)", r.stdout).group(1))
+    assert abs(ln - lt) <= 1e-5 * max(1.0, abs(lt))
+    first_t = [float(v) for v in re.search(r"logits\[0\]\[:5\] (.*)", ref).group(1).split()]
+    first_n = [float(v) for v in re.search(r"logits\[0\]\[:5\] (.*)", r.stdout).group(1).split()]
+    assert np.allclose(first_n, first_t, atol=1e-5, rtol=1e-5)
+    for name in ("W", "gain", "theta", "in_w", "in_b", "out_w", "out_b"):
+        pat = rf"grad {name}\s+norm ([-0-9.e+]+) sum ([-+0-9.e]+)"
+        nt, st = (float(v) for v in re.search(pat, ref).groups())
+        nn, sn = (float(v) for v in re.search(pat, r.stdout).groups())
+        assert abs(nn - nt) <= 1e-4 * max(nt, 1e-12), (name, nn, nt)
+        assert abs(sn - st) <= 1e-4 * max(nt, 1e-12) * 64, (name, sn, st)

@@ -83,3 +83,16 @@ def test_malformed_networks_are_refused_on_the_host():
     d[0] = s["n_s"] + 1
     s4["hop"][0]["drow"] = d
     assert "hop 1" in _bad(net_bytes(s4))
+    # a by-source form that is not the transpose of the by-target form: two weight indices swapped (each still
+    # distinct and in range), and two connections' target rows swapped
+    s5 = structure(f)
+    tw = np.array(s5["hop"][1]["twidx"]).copy()
+    tw[[0, -1]] = tw[[-1, 0]]
+    s5["hop"][1]["twidx"] = tw
+    assert "not the transpose" in _bad(net_bytes(s5))
+    s6 = structure(f)
+    tc = np.array(s6["hop"][2]["tcol"]).copy()
+    i = int(np.flatnonzero(tc != tc[0])[0])
+    tc[[0, i]] = tc[[i, 0]]
+    s6["hop"][2]["tcol"] = tc
+    assert "not the transpose" in _bad(net_bytes(s6))
