@@ -36,6 +36,7 @@ _SIGS = {
     "fc_profile_read": (ci, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(cll), ci, ci]),
     "fc_plan_rows": (ci, [vp, ci, ci, vp, cll, vp, cll, vp, cll, vp, cll, ctypes.POINTER(cll)]),
     "fh_spmm": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp, vp, vp]),
+    "fh_spmm_static": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp]),
     "fh_spmm_bwd": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp, vp]),
     "fh_to_half": (None, [vp, ci, ci, vp, vp, vp]),
     "fh_absmax": (None, [vp, cll, vp, vp]),

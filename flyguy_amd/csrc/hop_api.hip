@@ -1,29 +1,106 @@
 // The HopCuda-style hop (flyguy/fly_cuda.py:78-115) on the library's kernels: states are [rows][B] row-major
 // (B contiguous), the connection weights come in per call, the caller owns every buffer (plans included).
+//
+// fh_spmm_static is fh_spmm for callers that cannot allocate device memory (code under HIP graph capture, serving
+// loops that forbid allocation): its two workspaces, the packed (source, weight) pairs and the split rows' partial
+// sums, live in `scratch`, a file-scope device array of FH_STATIC_BYTES.  Every GPU the library runs on holds its
+// own copy until the process ends.  Calls on one GPU share that copy, so calls that overlap on one GPU (two streams,
+// two threads) race; calls in one stream are ordered.  Nothing in it needs clearing: a call packs every pair it
+// reads and writes every partial sum before it reads it.
+#include <mutex>
+
 #include "../../include/flyguy_core.h"
 #include "kernels.h"
 
 using namespace fg;
 
-extern "C" {
+static __device__ __align__(256) unsigned char scratch[FH_STATIC_BYTES];
 
-void fh_spmm(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
-             const int* pcol, const int* pidx, long long npos, const float* w, const float* h, float* out, int n_rows,
-             int n_src, int B, void* cw, float* scratch, void* stream) {
-    clear_error();
-    if (B <= 0 || B % TW || n_rows <= 0 || n_src <= 0 || nwave < 0 || nseg < 0 || nseg > 8LL * nwave || npos < 0 ||
-        nslot < 0 || !w || !h || !out || (nwave > 0 && (!wave || !seg || !pcol || !pidx || !cw)) ||
-        (nsplit > 0 && (!split || !scratch))) {
-        set_error("fh_spmm: bad argument");
-        return;
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_static_mu;
+void* g_static_ptr[MAX_DEVICES] = {};      // per device: the device address of its copy of `scratch`
+
+// The device address of the current device's `scratch` (looked up once per device, with that device current).  In
+// host code the array's name is only a stand-in for the symbol: kernels and copies get this address instead.
+unsigned char* static_scratch() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        set_error("fh_spmm_static: no current device");
+        return nullptr;
     }
-    hipStream_t st = (hipStream_t)stream;
-    FG_CHECK(launch_pack(pcol, pidx, w, (int2*)cw, npos, st), );
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    if (!g_static_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            set_error(std::string("fh_spmm_static: hipGetSymbolAddress: ") + hipGetErrorString(e));
+            return nullptr;
+        }
+        g_static_ptr[dev] = p;
+    }
+    return static_cast<unsigned char*>(g_static_ptr[dev]);
+}
+
+bool spmm_args_ok(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                  const int* pcol, const int* pidx, long long npos, const float* w, const float* h, const float* out,
+                  int n_rows, int n_src, int B) {
+    return !(B <= 0 || B % TW || n_rows <= 0 || n_src <= 0 || nwave < 0 || nseg < 0 || nseg > 8LL * nwave ||
+             npos < 0 || nslot < 0 || !w || !h || !out || (nwave > 0 && (!wave || !seg || !pcol || !pidx)) ||
+             (nsplit > 0 && !split));
+}
+
+// pack the pairs into cw, then the product through the plan (split rows' partial sums in `partials`)
+void spmm_run(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+              const int* pcol, const int* pidx, long long npos, const float* w, const float* h, float* out, int n_rows,
+              int n_src, int B, int2* cw, float* partials, hipStream_t st) {
+    FG_CHECK(launch_pack(pcol, pidx, w, cw, npos, st), );
     FwdEpi e;
     e.z = out;
     e.lz = plain(B);
     Plan p{(const int2*)wave, nwave, (const int4*)seg, nseg, (const int4*)split, nsplit, n_rows, nslot, npos};
-    FG_CHECK(launch_fwd(p, (const int2*)cw, h, plain(B), n_src, e, scratch, tiled(nslot), B / TW, st), );
+    FG_CHECK(launch_fwd(p, cw, h, plain(B), n_src, e, partials, tiled(nslot), B / TW, st), );
+}
+
+}  // namespace
+
+extern "C" {
+
+void fh_spmm(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+             const int* pcol, const int* pidx, long long npos, const float* w, const float* h, float* out, int n_rows,
+             int n_src, int B, void* cw, float* partials, void* stream) {
+    clear_error();
+    if (!spmm_args_ok(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, h, out, n_rows, n_src, B) ||
+        (nwave > 0 && !cw) || (nsplit > 0 && !partials)) {
+        set_error("fh_spmm: bad argument");
+        return;
+    }
+    spmm_run(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, h, out, n_rows, n_src, B, (int2*)cw,
+             partials, (hipStream_t)stream);
+}
+
+void fh_spmm_static(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                    const int* pcol, const int* pidx, long long npos, const float* w, const float* h, float* out,
+                    int n_rows, int n_src, int B, void* stream) {
+    clear_error();
+    if (!spmm_args_ok(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, h, out, n_rows, n_src, B)) {
+        set_error("fh_spmm_static: bad argument");
+        return;
+    }
+    // layout of the workspace: the npos pairs (8 bytes each), then nslot x B partial sums, each at 256 bytes
+    const unsigned long long pair_bytes = ((unsigned long long)npos * 8ull + 255ull) & ~255ull;
+    const unsigned long long part_bytes = (unsigned long long)nslot * (unsigned long long)B * 4ull;
+    if (pair_bytes + part_bytes > FH_STATIC_BYTES) {
+        set_error("fh_spmm_static: the product needs " + std::to_string(pair_bytes + part_bytes) +
+                  " bytes of workspace (8 per plan position + 4 per split-row slot and sample), more than the " +
+                  std::to_string((unsigned long long)FH_STATIC_BYTES) + " of the static workspace; use fh_spmm");
+        return;
+    }
+    unsigned char* base = static_scratch();
+    if (!base) return;
+    spmm_run(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, h, out, n_rows, n_src, B,
+             reinterpret_cast<int2*>(base), reinterpret_cast<float*>(base + pair_bytes), (hipStream_t)stream);
 }
 
 void fh_spmm_bwd(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,

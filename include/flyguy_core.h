@@ -137,6 +137,17 @@ void fh_spmm(const int* wave, int nwave, const int* seg, int nseg, const int* sp
              const int* pcol, const int* pidx, long long npos, const float* w, const float* h, float* out, int n_rows,
              int n_src, int B, void* cw, float* scratch, void* stream);
 
+/* fh_spmm without the two workspace arguments, for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops that forbid allocation).  No counterpart in the reference: the pairs and the split rows'
+ * partial sums go to a static device workspace of FH_STATIC_BYTES per GPU (held until the process ends), so a call
+ * allocates nothing.  A product needs 8 bytes per plan position (rounded up to 256) + 4 * nslot * B bytes; a larger
+ * one is refused with an error (fc_last_error).  Calls on one GPU share its workspace: calls that overlap on one GPU
+ * (several streams or threads) race. */
+#define FH_STATIC_BYTES (32u << 20)
+void fh_spmm_static(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                    const int* pcol, const int* pidx, long long npos, const float* w, const float* h, float* out,
+                    int n_rows, int n_src, int B, void* stream);
+
 /* Backward of fh_spmm: gh[n_src][B] = A^T gz and gw[e] += sum_b gz[row_e][b] h[col_e][b] (gw is added to), through the
  * row plan of the transposed (CSC) row pointer: pcol / pidx per position the CSC column tcol[pos] (a row of gz) and
  * the CSR edge tperm[pos] it is.  gwpart: scratch of npos * B/32 floats (unused when gw is null); scratch: nslot * B
