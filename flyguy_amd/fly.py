@@ -11,16 +11,22 @@ read-out maps the descending neurons to the action logits.  Hop k only holds the
 signal after k hops AND still reach a descending neuron in the hops left (fly.py:91-100), so pruning changes
 nothing in the result.
 
-Execution paths of forward():
-  - on a GPU with kernel "cuda" / "cuda16" / "hip": the hops run as the MI355X library's sparse products
-    (flyguy_amd.fly_hip.HopHip, the HopCuda interface of fly_cuda.py) - the library must be built, else an error;
-  - otherwise the PyTorch formulation of the reference: gather / index_add for small batches, sparse products
-    with their own backward for large ones, and sparse CSR products for playing on the CPU (fly.py:252-305).
+One walk through the layers (_walk) serves every execution path of forward(); the paths differ in the layout of
+the states and in how a layer's sparse product is formed:
+  - on a GPU with kernel "cuda" / "cuda16" / "hip" and a batch that is a multiple of 32: states [neurons, batch],
+    products on the MI355X library (flyguy_amd.fly_hip.HopHip, the HopCuda interface of fly_cuda.py; the library
+    must be built, else an error).  The reference takes its kernels only above gather_limit; the library's products
+    are the faster ones at any batch, so here they are taken at any batch;
+  - with gradients, or on a GPU otherwise: states [batch, neurons], gather / index_add products for a few samples
+    (batch x connection steps up to gather_limit), sparse products with a backward of their own above;
+  - playing on the CPU (no gradients): the CPU decision library when it is built, else sparse CSR matrices of the
+    current weights, made once per weights (fly.py:186-284).
 NativeFlyActor (flyguy_amd.fly_native) runs the whole network, its backward and Adam in the library.
 """
 from __future__ import annotations
 
 from collections.abc import Mapping
+from typing import NamedTuple
 import struct
 from pathlib import Path
 
@@ -56,30 +62,6 @@ def _load_graph(graph) -> Mapping:
         return graph
     p = Path(graph)
     return np.load(p if p.is_absolute() else ROOT / p)
-
-
-class _SparseHop(torch.autograd.Function):
-    """z[b, target] = sum over connections of w * h[b, source], states [B, rows]; the backward is the transposed
-    product for h and the product sampled at the connections for w (fly.py:51-72)."""
-
-    @staticmethod
-    def forward(ctx, w, h, crow, col, tcrow, tcol, tperm):
-        a = torch.sparse_csr_tensor(crow, col, w, size=(crow.numel() - 1, h.shape[1]))
-        ctx.save_for_backward(w, h, crow, col, tcrow, tcol, tperm)
-        return torch.sparse.mm(a, h.t()).t()
-
-    @staticmethod
-    def backward(ctx, gz):
-        w, h, crow, col, tcrow, tcol, tperm = ctx.saved_tensors
-        n_rows = crow.numel() - 1
-        gw = gh = None
-        if ctx.needs_input_grad[0]:
-            pattern = torch.sparse_csr_tensor(crow, col, torch.zeros_like(w), size=(n_rows, h.shape[1]))
-            gw = torch.sparse.sampled_addmm(pattern, gz.t().contiguous(), h, beta=0.0, alpha=1.0).values()
-        if ctx.needs_input_grad[1]:
-            at = torch.sparse_csr_tensor(tcrow, tcol, w[tperm], size=(h.shape[1], n_rows))
-            gh = torch.sparse.mm(at, gz.t()).t()
-        return gw, gh, None, None, None, None, None
 
 
 class FlyActor(nn.Module):
@@ -189,222 +171,321 @@ class FlyActor(nn.Module):
                 f"{self.used:,} connection steps a decision; learned outside the fly: {plug:,} numbers (each sensory "
                 f"neuron hears {self.fan} observation values; {len(self.dn_rows):,} descending neurons -> actions)")
 
-    # ---- hop products, PyTorch formulation ([B, rows] states)
-    def _hop_buffers(self, k):
-        if k == "in_":
-            return self.in_r, self.in_c, self.in_crow, self.in_tcrow, self.in_tcol, self.in_tperm
-        return (getattr(self, f"r{k}"), getattr(self, f"c{k}"), getattr(self, f"crow{k}"), getattr(self, f"tcrow{k}"),
-                getattr(self, f"tcol{k}"), getattr(self, f"tperm{k}"))
 
-    def _product(self, k, w: torch.Tensor, h: torch.Tensor, n_rows: int, small: bool) -> torch.Tensor:
-        r, c, crow, tcrow, tcol, tperm = self._hop_buffers(k)
-        if small:                                               # gather / scatter: cheapest for a few samples
-            return torch.zeros(h.shape[0], n_rows, dtype=h.dtype, device=h.device).index_add_(1, r, h[:, c] * w)
-        return _SparseHop.apply(w, h, crow, c, tcrow, tcol, tperm)
-
-    def _forward_hip(self, obs: torch.Tensor) -> torch.Tensor:
-        """States [neurons, batch], every product on the MI355X library (fly.py:170-185 with HopHip)."""
-        from .fly_hip import HopHip
-        half = self.kernel == "cuda16"
-        x = obs.t().contiguous()
-        drive = HopHip.apply(self.in_w, x, self.in_crow, self.in_ci, self.in_tcrow, self.in_tci, self.in_tperm, False)
-        drive = drive + self.in_b[:, None]
-        thr = nn.functional.softplus(self.theta)
-        h = torch.relu(self.gain[self.n0][:, None] * drive - thr[self.n0][:, None])
+    # ---- the layers as the forward passes walk them
+    def _layers(self) -> list[_Layer]:
+        """The plug (layer 0, the sensory neurons) and every hop, each with its product's index buffers."""
+        def csr(pre: str, post: str, n_rows: int, n_src: int) -> _Csr:
+            b = lambda name: getattr(self, f"{pre}{name}{post}")            # noqa: E731
+            return _Csr(b("r"), b("c"), b("crow"), b("tcrow"), b("tcol"), b("tperm"), b("ci"), b("tci"), n_rows, n_src)
+        none = self.n0.new_zeros(0)
+        out = [_Layer(csr("in_", "", self.sizes[0], self.obs_dim), None, self.n0, none, none)]
         for k in range(1, self.hops + 1):
-            rows = getattr(self, f"n{k}")
-            z = HopHip.apply(self.w[getattr(self, f"e{k}")], h, getattr(self, f"crow{k}"), getattr(self, f"ci{k}"),
-                             getattr(self, f"tcrow{k}"), getattr(self, f"tci{k}"), getattr(self, f"tperm{k}"), half)
-            s_ = getattr(self, f"s{k}")
-            if len(s_):
-                z = z.index_add(0, s_, drive[getattr(self, f"d{k}")])
-            h = torch.relu(self.gain[rows][:, None] * z - thr[rows][:, None])
-        return self.out(h[self.dn_rows].t())
+            out.append(_Layer(csr("", str(k), self.sizes[k], self.sizes[k - 1]), getattr(self, f"e{k}"),
+                              getattr(self, f"n{k}"), getattr(self, f"s{k}"), getattr(self, f"d{k}")))
+        return out
 
-    def _native(self):
-        """The CPU decision library (flyguy_amd/libfly_infer.so, include/fly_infer.h: a hop pushes only the neurons
-        that fire), set up from the current weights (fly.py:186-241).  None when it is not built or FLYGUY_NATIVE=0:
-        then the sparse products below play.  FLYGUY_CPU_THREADS=n decides each car on n threads (0: one per hardware
-        thread; unset: one, as the reference does), with bit-identical answers."""
-        ver = (self.w._version, self.in_w._version, self.gain._version, self.theta._version, self.in_b._version,
-               self.out.weight._version, self.out.bias._version, self.w.dtype)
-        nat = getattr(self, "_nat", None)
-        if nat is not None and nat["ver"] == ver:
-            return nat if nat["h"] else None
-        import ctypes
+    def _walk(self, x: torch.Tensor, product, by_neuron: bool, watch=None) -> torch.Tensor:
+        """Logits of a batch: the plug's product plus bias gives the sensory drive, each hop's product (plus the
+        drive of its re-driven sensory rows) the next layer's input, every neuron fires relu(gain z - softplus
+        theta), and the read-out maps the descending rows to the actions (fly.py:286-305 / 170-185 / 252-284).
+        States are [rows, B] when by_neuron, else [B, rows]; product(k, layer, weights, states) is layer k's sparse
+        product (k = 0: the plug).  watch(h) sees every layer's firing."""
+        axis = 0 if by_neuron else 1
+        thr = nn.functional.softplus(self.theta)
+
+        def per_row(v):
+            return v[:, None] if by_neuron else v
+
+        def fire(z, nid):
+            return torch.relu(per_row(self.gain[nid]) * z - per_row(thr[nid]))
+
+        layers = self._layers()
+        drive = product(0, layers[0], self.in_w, x) + per_row(self.in_b)
+        h = fire(drive, layers[0].nid)
+        if watch is not None:
+            watch(h)
+        for k, layer in enumerate(layers[1:], start=1):
+            z = product(k, layer, self.w[layer.edges], h)
+            if len(layer.redriven):
+                z = z.index_add(axis, layer.redriven, drive.index_select(axis, layer.drive_rows))
+            h = fire(z, layer.nid)
+            if watch is not None:
+                watch(h)
+        top = h.index_select(axis, self.dn_rows)
+        return self.out(top.t() if by_neuron else top)
+
+    # ---- CPU play
+    def _host_decider(self) -> "_HostDecider | None":
+        """The CPU decision library loaded with the current weights (rebuilt when a weight changed), or None when it
+        is not built, FLYGUY_NATIVE=0 or the weights are not float32."""
         import os
-        if nat is not None and nat["h"]:
-            nat["lib"].fly_free(nat["h"])
-        nat = {"ver": ver, "h": None}
-        self._nat = nat
-        path = Path(__file__).resolve().parent / "libfly_infer.so"
-        if os.environ.get("FLYGUY_NATIVE", "1") == "0" or not path.exists() or self.w.dtype != torch.float32:
-            return None
-        lib = ctypes.CDLL(str(path))
-        vp, ci = ctypes.c_void_p, ctypes.c_int
-        lib.fly_create.restype, lib.fly_create.argtypes = vp, [ci, ci, ci]
-        lib.fly_set_plug.restype, lib.fly_set_plug.argtypes = None, [vp, ci, ci] + [vp] * 6
-        lib.fly_set_hop.restype, lib.fly_set_hop.argtypes = None, [vp, ci, ci, ci, ci] + [vp] * 6
-        lib.fly_set_out.restype, lib.fly_set_out.argtypes = None, [vp, ci, vp, vp, vp]
-        lib.fly_forward.restype, lib.fly_forward.argtypes = None, [vp, vp, ci, vp, vp]
-        lib.fly_free.restype, lib.fly_free.argtypes = None, [vp]
-        keep = []                      # the arrays handed over (the library copies them; kept until set-up ends)
+        stamp = _weights_stamp(self)
+        held = getattr(self, "_decider", None)
+        if held is not None and held[0] == stamp:
+            return held[1]
+        if held is not None and held[1] is not None:
+            held[1].close()
+        dec = None
+        if os.environ.get("FLYGUY_NATIVE", "1") != "0" and self.w.dtype == torch.float32 and _HostDecider.LIB.exists():
+            dec = _HostDecider(self, os.environ.get("FLYGUY_CPU_THREADS"))
+        self._decider = (stamp, dec)
+        return dec
 
-        def arr(t, dt):
-            a = np.ascontiguousarray(t.detach().cpu().numpy() if torch.is_tensor(t) else t, dtype=dt)
-            keep.append(a)
-            return a.ctypes.data_as(vp)
-        with torch.no_grad():
-            thr = nn.functional.softplus(self.theta)
-            h = lib.fly_create(self.obs_dim, self.out.out_features, self.hops)
-            lib.fly_set_plug(h, self.sizes[0], int(self.in_ci.numel()), arr(self.in_crow, np.int32),
-                             arr(self.in_ci, np.int32), arr(self.in_w, np.float32), arr(self.in_b, np.float32),
-                             arr(self.gain[self.n0], np.float32), arr(thr[self.n0], np.float32))
-            for k in range(1, self.hops + 1):
-                rows = getattr(self, f"n{k}")
-                drow = np.full(len(rows), -1, np.int32)
-                drow[getattr(self, f"s{k}").cpu().numpy()] = getattr(self, f"d{k}").cpu().numpy()
-                w_by_src = self.w[getattr(self, f"e{k}")[getattr(self, f"tperm{k}")]]
-                lib.fly_set_hop(h, k - 1, len(rows), self.sizes[k - 1], int(w_by_src.numel()),
-                                arr(getattr(self, f"tcrow{k}"), np.int32), arr(getattr(self, f"tci{k}"), np.int32),
-                                arr(w_by_src, np.float32), arr(self.gain[rows], np.float32), arr(thr[rows], np.float32),
-                                arr(drow, np.int32))
-            lib.fly_set_out(h, len(self.dn_rows), arr(self.dn_rows, np.int32), arr(self.out.weight, np.float32),
-                            arr(self.out.bias, np.float32))
-            threads = os.environ.get("FLYGUY_CPU_THREADS")
-            if threads is not None:
-                lib.fly_set_threads.restype, lib.fly_set_threads.argtypes = None, [vp, ci]
-                lib.fly_set_threads(h, int(threads))
-        nat.update(h=h, lib=lib, shade=np.zeros(int(sum(self.sizes)), np.uint8))
-        return nat
-
-    def _forward_native(self, obs: torch.Tensor, nat: dict) -> torch.Tensor:
-        import ctypes
-        x = np.ascontiguousarray(obs.detach().numpy(), dtype=np.float32)
-        out = np.empty((x.shape[0], self.out.out_features), np.float32)
-        tap = getattr(self, "tap", None)             # the visualizer: every neuron's firing for the first car
-        vp = ctypes.c_void_p
-        nat["lib"].fly_forward(nat["h"], x.ctypes.data_as(vp), x.shape[0], out.ctypes.data_as(vp),
-                               nat["shade"].ctypes.data_as(vp) if tap is not None else None)
-        if tap is not None:
-            tap(nat["shade"])
-        return torch.from_numpy(out)
+    def _host_matrices(self) -> list[torch.Tensor]:
+        """The products as sparse CSR matrices of the current weights ([rows, sources]), made once per weights."""
+        stamp = _weights_stamp(self)[:5]
+        held = getattr(self, "_host_csr", None)
+        if held is None or held[0] != stamp:
+            mats = []
+            for layer in self._layers():
+                p = layer.prod
+                w = (self.in_w if layer.edges is None else self.w[layer.edges]).detach().clone()
+                mats.append(torch.sparse_csr_tensor(p.crow, p.c, w, size=(p.n_rows, p.n_src)))
+            held = (stamp, mats)
+            self._host_csr = held
+        return held[1]
 
     @torch.no_grad()
-    def _forward_cpu(self, obs: torch.Tensor) -> torch.Tensor:
-        """Playing on the CPU (fly.py:252-284): the CPU decision library when it is built, else sparse CSR products
-        built once from the current weights."""
-        nat = self._native()
-        if nat is not None:
-            return self._forward_native(obs, nat)
-        ver = (self.w._version, self.in_w._version, self.gain._version, self.theta._version, self.in_b._version)
-        c = getattr(self, "_cpu", None)
-        if c is None or c["ver"] != ver:
-            thr = nn.functional.softplus(self.theta)
-            c = {"ver": ver, "hop": [],
-                 "a_in": torch.sparse_csr_tensor(self.in_crow, self.in_c, self.in_w.detach().clone(),
-                                                 size=(self.sizes[0], self.obs_dim)),
-                 "g0": self.gain[self.n0][:, None].clone(), "t0": thr[self.n0][:, None].clone()}
-            for k in range(1, self.hops + 1):
-                rows = getattr(self, f"n{k}")
-                a = torch.sparse_csr_tensor(getattr(self, f"crow{k}"), getattr(self, f"c{k}"),
-                                            self.w.detach()[getattr(self, f"e{k}")], size=(len(rows), self.sizes[k - 1]))
-                c["hop"].append((a, self.gain[rows][:, None].clone(), thr[rows][:, None].clone(),
-                                 getattr(self, f"s{k}"), getattr(self, f"d{k}")))
-            self._cpu = c
-        drive = torch.sparse.mm(c["a_in"], obs.t().contiguous()) + self.in_b[:, None]
-        h = torch.relu(c["g0"] * drive - c["t0"])
-        tap = getattr(self, "tap", None)             # the visualizer: every layer's firing for the first car
-        acts = [h[:, 0]] if tap is not None else None
-        for a, g, t, s_, d_ in c["hop"]:
-            z = torch.sparse.mm(a, h)
-            if len(s_):
-                z[s_] += drive[d_]
-            h = torch.relu(g * z - t)
-            if acts is not None:
-                acts.append(h[:, 0])
+    def _play(self, obs: torch.Tensor) -> torch.Tensor:
+        """A decision on the CPU (the bot): the CPU decision library when it is there, else sparse CSR products of
+        the current weights (fly.py:186-284).  A visualizer tap (self.tap) gets the first sample's firing."""
+        tap = getattr(self, "tap", None)
+        dec = self._host_decider()
+        if dec is not None:
+            return dec.decide(obs, tap)
+        mats = self._host_matrices()
+        first = [] if tap is not None else None
+        logits = self._walk(obs.t().contiguous(), lambda k, layer, w, h: torch.sparse.mm(mats[k], h),
+                            by_neuron=True, watch=(lambda h: first.append(h[:, 0])) if first is not None else None)
         if tap is not None:
-            tap(acts)
-        return self.out(h[self.dn_rows].t())
+            tap(first)
+        return logits
 
+    # ---- forward
     def forward(self, obs: torch.Tensor, extra: torch.Tensor | None = None) -> torch.Tensor:
         obs = obs.double() if self.w.dtype == torch.float64 else obs.float()    # (float64: an actor made .double())
         if not obs.is_cuda and not torch.is_grad_enabled():
-            return self._forward_cpu(obs)
-        small = obs.shape[0] * self.used <= self.gather_limit
-        if self.kernel != "torch" and obs.is_cuda and obs.shape[0] % 32 == 0:
-            return self._forward_hip(obs)
-        drive = self._product("in_", self.in_w, obs, self.sizes[0], small) + self.in_b
-        thr = nn.functional.softplus(self.theta)
-        h = torch.relu(self.gain[self.n0] * drive - thr[self.n0])
-        for k in range(1, self.hops + 1):
-            rows = getattr(self, f"n{k}")
-            z = self._product(str(k), self.w[getattr(self, f"e{k}")], h, len(rows), small)
-            s_ = getattr(self, f"s{k}")
-            if len(s_):
-                z = z.index_add(1, s_, drive[:, getattr(self, f"d{k}")])
-            h = torch.relu(self.gain[rows] * z - thr[rows])
-        return self.out(h[:, self.dn_rows])
+            return self._play(obs)
+        if self.kernel != "torch" and obs.is_cuda and obs.shape[0] % 32 == 0:      # (at any batch size)
+            from .fly_hip import HopHip
+            half = self.kernel == "cuda16"
+
+            def on_library(k, layer, w, h):
+                p = layer.prod
+                return HopHip.apply(w, h, p.crow, p.ci, p.tcrow, p.tci, p.tperm, half and k > 0)
+            return self._walk(obs.t().contiguous(), on_library, by_neuron=True)
+
+        few = obs.shape[0] * self.used <= self.gather_limit        # a few samples: gather / scatter products
+
+        def in_torch(k, layer, w, h):
+            p = layer.prod
+            if few:
+                return h.new_zeros(h.shape[0], p.n_rows).index_add_(1, p.r, h[:, p.c] * w)
+            return _RowProduct.apply(w, h, p.crow, p.c, p.tcrow, p.tcol, p.tperm)
+        return self._walk(obs, in_torch, by_neuron=False)
+
+
+class _Csr(NamedTuple):
+    """The index buffers of one sparse product: per connection its row (target) and column (source), CSR row
+    pointer, the by-source form (row pointer over sources, rows, and the permutation into CSR order) and int32 copies
+    of the columns / by-source rows."""
+    r: torch.Tensor
+    c: torch.Tensor
+    crow: torch.Tensor
+    tcrow: torch.Tensor
+    tcol: torch.Tensor
+    tperm: torch.Tensor
+    ci: torch.Tensor
+    tci: torch.Tensor
+    n_rows: int
+    n_src: int
+
+
+class _Layer(NamedTuple):
+    prod: _Csr
+    edges: torch.Tensor | None     # the connections' indices into w (None: the plug, whose weights are in_w)
+    nid: torch.Tensor              # the neuron of each row
+    redriven: torch.Tensor         # rows that are sensory neurons, kept driven by the observation ...
+    drive_rows: torch.Tensor       # ... and their rows in the sensory layer
+
+
+def _weights_stamp(f: FlyActor) -> tuple:
+    """Changes whenever a weight does (PyTorch bumps a tensor's version on every in-place change)."""
+    return (f.w._version, f.in_w._version, f.gain._version, f.theta._version, f.in_b._version,
+            f.out.weight._version, f.out.bias._version, f.w.dtype)
+
+
+class _RowProduct(torch.autograd.Function):
+    """z[b, i] = sum over the connections e of row i of w[e] h[b, col[e]] for states [B, sources] -> [B, rows],
+    with a backward of its own (fly.py:51-72): the transposed product for h, and for w the product sampled at the
+    connections only, instead of the dense rows x sources gradient PyTorch's sparse products would build."""
+
+    @staticmethod
+    def forward(ctx, w, h, crow, col, tcrow, tcol, tperm):
+        n_rows, n_src = crow.numel() - 1, h.shape[1]
+        ctx.save_for_backward(w, h, crow, col, tcrow, tcol, tperm)
+        return torch.sparse.mm(torch.sparse_csr_tensor(crow, col, w, size=(n_rows, n_src)), h.t()).t()
+
+    @staticmethod
+    def backward(ctx, gz):
+        w, h, crow, col, tcrow, tcol, tperm = ctx.saved_tensors
+        n_rows, n_src = crow.numel() - 1, h.shape[1]
+        want_w, want_h = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        gw = gh = None
+        if want_w:               # <gz[:, row], h[:, col]> at every connection, through a sampled dense product
+            mask = torch.sparse_csr_tensor(crow, col, torch.zeros_like(w), size=(n_rows, n_src))
+            gw = torch.sparse.sampled_addmm(mask, gz.t().contiguous(), h, beta=0.0, alpha=1.0).values()
+        if want_h:               # A^T gz through the by-source form (weights in by-source order)
+            at = torch.sparse_csr_tensor(tcrow, tcol, w[tperm], size=(n_src, n_rows))
+            gh = torch.sparse.mm(at, gz.t()).t()
+        return gw, gh, None, None, None, None, None
+
+
+class _HostDecider:
+    """The CPU decision library (flyguy_amd/libfly_infer.so, include/fly_infer.h: a hop pushes the neurons that fire
+    along their outgoing connections) with one version of an actor's weights (fly.py:186-250).  threads: None (one
+    thread, as the reference), or a count for fly_set_threads (0: one per hardware thread), with bit-identical
+    answers."""
+
+    LIB = Path(__file__).resolve().parent / "libfly_infer.so"
+    _lib = None
+
+    @classmethod
+    def library(cls):
+        import ctypes
+        if cls._lib is None:
+            L = ctypes.CDLL(str(cls.LIB))
+            vp, ci = ctypes.c_void_p, ctypes.c_int
+            sig = {"fly_create": (vp, [ci, ci, ci]), "fly_set_plug": (None, [vp, ci, ci] + [vp] * 6),
+                   "fly_set_hop": (None, [vp, ci, ci, ci, ci] + [vp] * 6), "fly_set_out": (None, [vp, ci, vp, vp, vp]),
+                   "fly_forward": (None, [vp, vp, ci, vp, vp]), "fly_free": (None, [vp]),
+                   "fly_set_threads": (None, [vp, ci])}
+            for name, (res, args) in sig.items():
+                fn = getattr(L, name)
+                fn.restype, fn.argtypes = res, args
+            cls._lib = L
+        return cls._lib
+
+    def __init__(self, f: FlyActor, threads: str | None):
+        L = self.library()
+        held = []                          # the arrays handed over (the library copies them during set-up)
+
+        def ptr(t, dtype):
+            a = np.ascontiguousarray(t.detach().cpu().numpy() if torch.is_tensor(t) else t, dtype=dtype)
+            held.append(a)
+            return a.ctypes.data
+
+        i32, f32 = np.int32, np.float32
+        self.n_act = f.out.out_features
+        with torch.no_grad():
+            thr = nn.functional.softplus(f.theta)
+            self.h = L.fly_create(f.obs_dim, self.n_act, f.hops)
+            plug = f._layers()[0]
+            L.fly_set_plug(self.h, f.sizes[0], int(plug.prod.ci.numel()), ptr(plug.prod.crow, i32), ptr(plug.prod.ci, i32),
+                           ptr(f.in_w, f32), ptr(f.in_b, f32), ptr(f.gain[f.n0], f32), ptr(thr[f.n0], f32))
+            for k, layer in enumerate(f._layers()[1:], start=1):
+                p = layer.prod
+                redrive = np.full(p.n_rows, -1, i32)
+                redrive[layer.redriven.cpu().numpy()] = layer.drive_rows.cpu().numpy()
+                by_source = f.w[layer.edges[p.tperm]]              # strengths in the by-source order
+                L.fly_set_hop(self.h, k - 1, p.n_rows, p.n_src, int(by_source.numel()), ptr(p.tcrow, i32), ptr(p.tci, i32),
+                              ptr(by_source, f32), ptr(f.gain[layer.nid], f32), ptr(thr[layer.nid], f32),
+                              ptr(redrive, i32))
+            L.fly_set_out(self.h, len(f.dn_rows), ptr(f.dn_rows, i32), ptr(f.out.weight, f32), ptr(f.out.bias, f32))
+            if threads is not None:
+                L.fly_set_threads(self.h, int(threads))
+        self.shade = np.zeros(int(sum(f.sizes)), np.uint8)
+
+    def decide(self, obs: torch.Tensor, tap=None) -> torch.Tensor:
+        x = np.ascontiguousarray(obs.detach().numpy(), dtype=np.float32)
+        out = np.empty((x.shape[0], self.n_act), np.float32)
+        self.library().fly_forward(self.h, x.ctypes.data, x.shape[0], out.ctypes.data,
+                                   self.shade.ctypes.data if tap is not None else None)
+        if tap is not None:
+            tap(self.shade)
+        return torch.from_numpy(out)
+
+    def close(self) -> None:
+        if self.h:
+            self.library().fly_free(self.h)
+            self.h = None
 
 
 class VizTap:
-    """The visualizer's window into a playing actor (fly.py:308-368): after every decision the firing of every neuron
-    in play, layer by layer, goes into a small shared file, one byte a neuron, with the chosen action; a reader
-    (the visualizer's server) maps the file, nothing waits for it.  Set `actor.tap = VizTap(actor.sizes)`.
+    """A live window for the visualizer into a playing actor (fly.py:308-368): after every decision the firing of
+    every neuron in play, layer by layer, one byte each, and the chosen action go into a small memory-mapped file;
+    readers (the visualizer's server) map it, and nothing waits for them.  Set `actor.tap = VizTap(actor.sizes)`.
 
-    File (little endian): "FLYV", version 1 (u32), seq (u32, odd while being written) at 8, tick (u32) at 12, time
-    (f64) at 16, action (i32) at 24, 8 controls (f32) at 28, layer count and 4 layer sizes (u32) at 60, 90 action
-    probabilities (f32) at 80, match clock (f32), frame (u32), overtime (i32) at 440; the firing bytes from 512,
-    the layers one after another (sensory first), 255 * tanh(1.5 * firing)."""
+    The file is a fixed layout (little endian): the header fields below at their byte offsets, the firing bytes from
+    byte 512 (sensory layer first), each 255 * tanh(1.5 * firing) truncated to a byte.  `seq` is odd while a
+    decision is being written, so a reader that sees the same even seq before and after its read has a whole one."""
 
-    HEADER = 512
+    FIRING = 512
+    _FIELDS = {                            # name: (offset, struct format)
+        "magic": (0, "<4sI"),              #   "FLYV", layout version 1
+        "seq": (8, "<I"),
+        "stamp": (12, "<Idi"),             #   decisions published, wall time, action
+        "controls": (28, "<8f"),
+        "layers": (60, "<5I"),             #   layer count, first 4 layer sizes
+        "probs": (80, "<90f"),
+        "clock": (440, "<fIi"),            #   match clock, game frame, overtime
+    }
 
     def __init__(self, sizes, path=None):
         import mmap
         import tempfile
         self.sizes = [int(v) for v in sizes]
         self.path = Path(path) if path else Path(tempfile.gettempdir()) / "flyguy_viz.bin"
-        total = self.HEADER + sum(self.sizes)
-        if not (self.path.exists() and self.path.stat().st_size == total):   # a file of the right size is reused
-            with open(self.path, "wb") as fh:
-                fh.write(bytes(total))
+        length = self.FIRING + sum(self.sizes)
+        # a file of the right length is used as it is: a reader may have it mapped, and replacing it would cut them off
+        if not (self.path.exists() and self.path.stat().st_size == length):
+            self.path.write_bytes(bytes(length))
         self.fh = open(self.path, "r+b")
-        self.mm = mmap.mmap(self.fh.fileno(), total)
-        self.mm[0:8] = b"FLYV" + struct.pack("<I", 1)
-        self.mm[60:80] = struct.pack("<5I", len(self.sizes), *(self.sizes + [0] * 4)[:4])
-        self.seq = 0
-        self.tick = 0
+        self.mm = mmap.mmap(self.fh.fileno(), length)
+        self._put("magic", b"FLYV", 1)
+        self._put("layers", len(self.sizes), *(self.sizes + [0, 0, 0, 0])[:4])
+        self.seq = self.tick = 0
         self.acts = None
 
+    def _put(self, field: str, *values) -> None:
+        at, fmt = self._FIELDS[field]
+        struct.pack_into(fmt, self.mm, at, *values)
+
     def __call__(self, acts) -> None:
-        """From the actor's forward pass: the first car's firing (a uint8 array from the CPU library, or one tensor
-        per layer from the sparse products)."""
+        """From the actor's forward pass: the first sample's firing (bytes from the CPU library, or one tensor per
+        layer from the sparse products)."""
         self.acts = acts
 
+    def _firing_bytes(self) -> bytes:
+        if isinstance(self.acts, np.ndarray):
+            return self.acts.astype(np.uint8).tobytes()
+        return b"".join((torch.tanh(1.5 * a.float()) * 255.0).to(torch.uint8).cpu().numpy().tobytes()
+                        for a in self.acts)
+
     def publish(self, action: int, controls, probs, clock: float = -1.0, frame: int = 0, overtime: bool = False) -> None:
+        """Write the last decision: its firing, the action, the 8 controls and the action probabilities; clock /
+        frame / overtime let a recording of the page be lined up with one of the game."""
         import time
         if self.acts is None:
             return
-        self.mm[440:452] = struct.pack("<fIi", float(clock), int(frame) & 0xFFFFFFFF, int(bool(overtime)))
-        self.seq += 1
-        self.mm[8:12] = struct.pack("<I", self.seq)
-        at = self.HEADER
-        if isinstance(self.acts, np.ndarray):
-            b = self.acts.astype(np.uint8).tobytes()
-            self.mm[at:at + len(b)] = b
-        else:
-            for a in self.acts:
-                b = (torch.tanh(a.float() * 1.5) * 255.0).to(torch.uint8).cpu().numpy().tobytes()
-                self.mm[at:at + len(b)] = b
-                at += len(b)
+        body = self._firing_bytes()
+        self.seq += 1                                   # odd: being written
+        self._put("seq", self.seq)
+        self.mm[self.FIRING:self.FIRING + len(body)] = body
         self.tick += 1
-        self.mm[12:28] = struct.pack("<Idi", self.tick, time.time(), int(action))
-        self.mm[28:60] = np.asarray(controls, np.float32)[:8].tobytes()
-        p = np.asarray(probs, np.float32)[:90]
-        self.mm[80:80 + 4 * len(p)] = p.tobytes()
-        self.seq += 1
-        self.mm[8:12] = struct.pack("<I", self.seq)
+        self._put("stamp", self.tick, time.time(), int(action))
+        self._put_floats("controls", np.asarray(controls, np.float32)[:8])
+        self._put_floats("probs", np.asarray(probs, np.float32)[:90])
+        self._put("clock", float(clock), int(frame) & 0xFFFFFFFF, int(bool(overtime)))
+        self.seq += 1                                   # even: whole
+        self._put("seq", self.seq)
         self.acts = None
+
+    def _put_floats(self, field: str, v: np.ndarray) -> None:
+        """The first len(v) floats of a field (a caller may give fewer than the field holds)."""
+        at = self._FIELDS[field][0]
+        self.mm[at:at + 4 * len(v)] = v.tobytes()
 
     def close(self) -> None:
         self.mm.close()

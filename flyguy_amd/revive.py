@@ -4,15 +4,20 @@ flyguy/native/revive.py; the trainer's own surgery is fc_revive in the library):
     python -m flyguy_amd.revive NET.bin PARAMS_IN.bin CHUNK.bin PARAMS_OUT.bin [--samples 512] [--seed 0]
                                 [--passes 3] [--target 0.4]
 
-NET.bin takes the place of the reference's TEMPLATE.pt and graph file: the sending and receiving neuron of every
-strength in play comes from the hop index arrays.  The first --samples moments of CHUNK.bin (a FLYD file with the
-teacher's answers) are surveyed: a neuron outside the sensory layer that fires for none of them in any hop is
-silent.  Its incoming strengths keep their sizes and get a random sign (numpy default_rng(--seed)), its gain and
-threshold return to 1 and -4, its strengths onto live neurons and its action weights become 0 (it sent nothing and
-still sends nothing, so the network's answers do not change), and then, --passes times, its incoming strengths are
-scaled so that its input's rms is --target (clipped to 0.02..200 times).  The KL to the teacher is checked to be
-unchanged after every pass.  Everything runs in float32 with PyTorch CPU tensors (revive.py:56-128); the GPU beside it
-belongs to the trainer.
+A neuron outside the sensory layer that fires for none of the first --samples moments of CHUNK.bin (a FLYD file with
+the teacher's answers) in any hop it takes part in is silent: it passes no gradient, so nothing would ever wake it.
+The surgery (revive.py:96-128):
+  - its incoming strengths keep their sizes and get random signs (numpy default_rng(--seed), one draw per strength
+    in weight-index order), so its input is positive about half the time;
+  - its gain and threshold return to their starting values 1 and -4;
+  - its outgoing strengths onto live neurons, and for a descending neuron its action weights, become 0: it sent
+    nothing before and sends nothing now, so the network's answers do not change (a connection between two silent
+    neurons keeps its new sign: its target is silent too);
+  - then, --passes times, its incoming strengths are scaled so that its input's rms over the samples comes to
+    --target (the factor clipped to 0.02..200).
+After every pass the KL to the teacher is checked to be unchanged.  NET.bin takes the place of the reference's
+TEMPLATE.pt and graph file: the sending and receiving neuron of every strength in play come from the hop index
+arrays.  Float32, PyTorch CPU tensors; the GPU beside it belongs to the trainer.
 """
 from __future__ import annotations
 
@@ -20,92 +25,138 @@ import argparse
 import struct
 import sys
 from pathlib import Path
+from typing import NamedTuple
 
 import numpy as np
 import torch
 
 from .export import read_net, read_params, write_params
 
+CHUNK = 64                                       # samples per pass of the survey
+
 
 def _chunk(path: Path, samples: int, obs_dim: int, n_act: int):
-    """The first `samples` moments of a FLYD file: observations and teacher logits, float32 (revive.py:51-56)."""
-    with open(path, "rb") as fh:
-        if fh.read(4) != b"FLYD":
-            raise SystemExit(f"{path}: not a FLYD file")
-        n, od, na = struct.unpack("<qii", fh.read(16))
-        if od != obs_dim or na != n_act:
-            raise SystemExit(f"{path}: moments of {od} numbers and {na} answers, the network reads {obs_dim} and scores {n_act}")
-        k = min(samples, n)
-        obs = np.frombuffer(fh.read(k * od * 2), np.float16).reshape(k, od).astype(np.float32)
-        fh.seek(20 + n * od * 2)
-        tl = np.frombuffer(fh.read(k * na * 2), np.float16).reshape(k, na).astype(np.float32)
-    return torch.from_numpy(obs), torch.from_numpy(tl)
+    """The first `samples` moments of a FLYD file: observations and teacher logits as float32 tensors."""
+    raw = Path(path).read_bytes()
+    if raw[:4] != b"FLYD":
+        raise SystemExit(f"{path}: not a FLYD file")
+    n, od, na = struct.unpack_from("<qii", raw, 4)
+    if od != obs_dim or na != n_act:
+        raise SystemExit(f"{path}: moments of {od} numbers and {na} answers, the network reads {obs_dim} and scores {n_act}")
+    k = min(samples, n)
+    obs = np.frombuffer(raw, np.float16, k * od, 20).reshape(k, od)
+    answers = np.frombuffer(raw, np.float16, k * na, 20 + 2 * n * od).reshape(k, na)
+    return torch.from_numpy(obs.astype(np.float32)), torch.from_numpy(answers.astype(np.float32))
+
+
+class Survey(NamedTuple):
+    fired: np.ndarray        # per neuron: (layer, sample) pairs in which it fires, over the hops it takes part in
+    seen: np.ndarray         # per neuron: whether it takes part in a hop
+    rms: np.ndarray          # per neuron: the largest rms of its input over the hops it takes part in
+    share: list[float]       # per layer (sensory first): the share of (row, sample) pairs that fire
+    kl: float                # mean KL(teacher || network) over the samples
 
 
 class Net:
-    """The network of a NET.bin with one set of weights, as PyTorch CPU tensors (index_add form, as revive.py's)."""
+    """The network of a NET.bin, evaluated with one set of weights on PyTorch CPU tensors (gather / index_add
+    products), and the sending (`pre`) and receiving (`post`) neuron of every strength in play."""
 
     def __init__(self, s: dict):
         self.s = s
-        L = torch.as_tensor
-        self.in_r = L(np.repeat(np.arange(s["n_s"]), np.diff(s["in_crow"])))
-        self.in_c = L(s["in_col"])
-        self.n0 = L(s["n0"])
-        self.hop = []
-        for h in s["hop"]:
-            rows = len(h["nid"])
-            drow = np.asarray(h["drow"])
-            keep = np.flatnonzero(drow >= 0)
-            self.hop.append({"r": L(np.repeat(np.arange(rows), np.diff(h["crow"]))), "c": L(h["col"]), "widx": L(h["widx"]),
-                             "nid": L(h["nid"]), "s": L(keep), "d": L(drow[keep]), "rows": rows})
-        self.dn = L(s["dn_rows"])
-        # the sending / receiving neuron of every strength in play
+        t = torch.as_tensor
+        counts = np.diff(np.asarray(s["in_crow"]))
+        self.plug = (t(np.repeat(np.arange(s["n_s"]), counts)), t(np.asarray(s["in_col"])))
+        self.n0 = t(np.asarray(s["n0"]))
+        self.layers = []
         self.pre = np.full(s["n_w"], -1, np.int64)
         self.post = np.full(s["n_w"], -1, np.int64)
         below = np.asarray(s["n0"])
         for h in s["hop"]:
-            nid = np.asarray(h["nid"])
-            tgt = np.repeat(np.arange(len(nid)), np.diff(h["crow"]))
-            self.pre[np.asarray(h["widx"])] = below[np.asarray(h["col"])]
-            self.post[np.asarray(h["widx"])] = nid[tgt]
+            nid, col, widx = np.asarray(h["nid"]), np.asarray(h["col"]), np.asarray(h["widx"])
+            target = np.repeat(np.arange(len(nid)), np.diff(np.asarray(h["crow"])))
+            drow = np.asarray(h["drow"])
+            redriven = np.flatnonzero(drow >= 0)
+            self.layers.append({"row": t(target), "col": t(col), "widx": t(widx), "nid": t(nid),
+                                "redriven": t(redriven), "drive_rows": t(drow[redriven])})
+            self.pre[widx] = below[col]
+            self.post[widx] = nid[target]
             below = nid
+        self.dn = t(np.asarray(s["dn_rows"]))
 
-    @torch.no_grad()
-    def survey(self, P, obs: torch.Tensor, tl: torch.Tensor):
-        """Firing counts per neuron over every hop it takes part in, neurons seen in a hop, the largest input rms over
-        those hops, the firing share per layer and the KL to the teacher (revive.py:61-95)."""
+    def _states(self, P, x: torch.Tensor):
+        """Per layer of a batch: (neurons, pre-activation, firing), sensory layer first; then the logits."""
         s = self.s
         W, gain, theta, in_w, in_b, ow, ob = (torch.as_tensor(p) for p in P)
-        ow = ow.view(s["n_act"], s["n_dn"])
-        N, K = s["n_neurons"], s["hops"]
+        thr = torch.nn.functional.softplus(theta)
+        rows, cols = self.plug
+        drive = torch.zeros(len(x), s["n_s"]).index_add_(1, rows, x[:, cols] * in_w) + in_b
+        h = torch.relu(gain[self.n0] * drive - thr[self.n0])
+        yield self.n0, drive, h
+        for L in self.layers:
+            z = torch.zeros(len(x), len(L["nid"])).index_add_(1, L["row"], h[:, L["col"]] * W[L["widx"]])
+            if len(L["redriven"]):
+                z = z.index_add(1, L["redriven"], drive[:, L["drive_rows"]])
+            h = torch.relu(gain[L["nid"]] * z - thr[L["nid"]])
+            yield L["nid"], z, h
+        yield None, None, h[:, self.dn] @ ow.view(s["n_act"], s["n_dn"]).t() + ob
+
+    @torch.no_grad()
+    def survey(self, P, obs: torch.Tensor, teacher: torch.Tensor) -> Survey:
+        """The Survey of the moments, in passes of CHUNK samples (revive.py:61-95)."""
+        N, layers = self.s["n_neurons"], len(self.layers) + 1
         fired = torch.zeros(N)
         seen = torch.zeros(N, dtype=torch.bool)
-        sq = [torch.zeros(h["rows"]) for h in self.hop]
-        share = [0.0] * (K + 1)
+        sq = [None] * layers
+        firing = [0.0] * layers
         kl = 0.0
-        thr = torch.nn.functional.softplus(theta)
-        n = obs.shape[0]
-        for i in range(0, n, 64):
-            x = obs[i:i + 64]
-            drive = torch.zeros(len(x), s["n_s"]).index_add_(1, self.in_r, x[:, self.in_c] * in_w) + in_b
-            h = torch.relu(gain[self.n0] * drive - thr[self.n0])
-            share[0] += float((h > 0).float().mean()) * len(x)
-            for k, hp in enumerate(self.hop):
-                z = torch.zeros(len(x), hp["rows"]).index_add_(1, hp["r"], h[:, hp["c"]] * W[hp["widx"]])
-                if len(hp["s"]):
-                    z = z.index_add(1, hp["s"], drive[:, hp["d"]])
-                sq[k] += z.pow(2).sum(0)
-                h = torch.relu(gain[hp["nid"]] * z - thr[hp["nid"]])
-                fired[hp["nid"]] += (h > 0).float().sum(0)
-                seen[hp["nid"]] = True
-                share[k + 1] += float((h > 0).float().mean()) * len(x)
-            lp = torch.log_softmax(h[:, self.dn] @ ow.t() + ob, -1)
-            tp = torch.log_softmax(tl[i:i + 64], -1)
-            kl += float((tp.exp() * (tp - lp)).sum())
+        n = len(obs)
+        for i in range(0, n, CHUNK):
+            x = obs[i:i + CHUNK]
+            for k, (nid, z, h) in enumerate(self._states(P, x)):
+                if nid is None:                                   # the logits
+                    lt = torch.log_softmax(teacher[i:i + CHUNK], -1)
+                    kl += float((lt.exp() * (lt - torch.log_softmax(h, -1))).sum())
+                    continue
+                on = h > 0
+                firing[k] += float(on.float().mean()) * len(x)
+                if k == 0:
+                    continue                                      # (the sensory layer is never revived)
+                fired[nid] += on.float().sum(0)
+                seen[nid] = True
+                sq[k] = z.pow(2).sum(0) if sq[k] is None else sq[k] + z.pow(2).sum(0)
         rms = torch.zeros(N)
-        for k, hp in enumerate(self.hop):
-            rms[hp["nid"]] = torch.maximum(rms[hp["nid"]], (sq[k] / n).sqrt())
-        return fired.numpy(), seen.numpy(), rms.numpy(), [v / n for v in share], kl / n
+        for k, L in enumerate(self.layers, start=1):
+            rms[L["nid"]] = torch.maximum(rms[L["nid"]], (sq[k] / n).sqrt())
+        return Survey(fired.numpy(), seen.numpy(), rms.numpy(), [v / n for v in firing], kl / n)
+
+
+class Revival:
+    """The surgery on one set of weights (the seven arrays, in the library's order)."""
+
+    def __init__(self, net: Net, P: list[np.ndarray], dead: np.ndarray, seed: int):
+        s = net.s
+        self.net, self.dead = net, dead
+        self.incoming = dead[net.post]                            # strengths into a silent neuron
+        outgoing = dead[net.pre] & ~self.incoming                 # strengths from a silent neuron onto a live one
+        w = P[0].copy()
+        signs = np.random.default_rng(seed).choice([-1.0, 1.0], int(self.incoming.sum())).astype(np.float32)
+        w[self.incoming] = np.abs(w[self.incoming]) * signs
+        w[outgoing] = 0.0
+        gain, theta = P[1].copy(), P[2].copy()
+        gain[dead], theta[dead] = 1.0, -4.0
+        actions = P[5].copy().reshape(s["n_act"], s["n_dn"])
+        descending = np.asarray(s["hop"][-1]["nid"])[np.asarray(s["dn_rows"])]
+        actions[:, dead[descending]] = 0.0
+        self.P = [w, gain, theta, P[3], P[4], actions.reshape(-1), P[6]]
+        self.counts = (int(self.incoming.sum()), int(outgoing.sum()), int(dead[descending].sum()))
+
+    def rescale(self, rms: np.ndarray, target: float) -> None:
+        """Bring every revived neuron's input rms to `target` (factors clipped to 0.02..200)."""
+        factor = np.ones(len(rms), np.float32)
+        m = self.dead & (rms > 0)
+        factor[m] = np.clip(target / rms[m], 0.02, 200.0)
+        w = self.P[0]
+        w[self.incoming] *= factor[self.net.post[self.incoming]]
 
 
 def main(argv=None) -> int:
@@ -122,42 +173,29 @@ def main(argv=None) -> int:
     s = read_net(Path(args.net))
     step, P = read_params(Path(args.params), s)
     net = Net(s)
-    obs, tl = _chunk(Path(args.chunk), args.samples, s["obs_dim"], s["n_act"])
-    fired, seen, _, share, kl0 = net.survey(P, obs, tl)
-    is_sens = np.zeros(s["n_neurons"], bool)
-    is_sens[np.asarray(s["n0"])] = True
-    dead = seen & (fired == 0) & ~is_sens
-    print(f"native step {step:,}, {len(obs)} samples: firing share per hop {[round(v, 3) for v in share]}; KL {kl0:.4f}")
-    print(f"silent neurons (never fire in any hop): {int(dead.sum()):,} of {int((seen & ~is_sens).sum()):,} in play "
+    obs, teacher = _chunk(Path(args.chunk), args.samples, s["obs_dim"], s["n_act"])
+    fired, seen, _, share, kl0 = net.survey(P, obs, teacher)
+    outside = np.ones(s["n_neurons"], bool)
+    outside[np.asarray(s["n0"])] = False                          # neurons outside the sensory layer
+    dead = seen & (fired == 0) & outside
+    n = len(obs)
+    print(f"native step {step:,}, {n} samples: firing share per hop {[round(v, 3) for v in share]}; KL {kl0:.4f}")
+    print(f"silent neurons (never fire in any hop): {int(dead.sum()):,} of {int((seen & outside).sum()):,} in play "
           f"outside the sensory layer")
-    rng = np.random.default_rng(args.seed)
-    w = P[0].copy()
-    inc, outg = dead[net.post], dead[net.pre]
-    w[inc] = np.abs(w[inc]) * rng.choice([-1.0, 1.0], int(inc.sum())).astype(np.float32)
-    w[outg & ~inc] = 0.0                       # silent -> live only: a connection between two silent neurons stays
-    gain, theta = P[1].copy(), P[2].copy()
-    gain[dead], theta[dead] = 1.0, -4.0
-    out_w = P[5].copy().reshape(s["n_act"], -1)
-    dn_ids = np.asarray(s["hop"][-1]["nid"])[np.asarray(s["dn_rows"])]
-    out_w[:, dead[dn_ids]] = 0.0               # a silent descending neuron sent nothing to the actions either
-    P2 = [w, gain, theta, P[3], P[4], out_w.reshape(P[5].shape), P[6]]
-    print(f"re-signed {int(inc.sum()):,} incoming strengths, zeroed {int((outg & ~inc).sum()):,} outgoing ones and the "
-          f"action weights of {int(dead[dn_ids].sum())} descending neurons")
-    for it in range(args.passes + 1):          # hop after hop: bring every revived neuron's input to the target size
-        fired2, _, rms, share2, kl1 = net.survey(P2, obs, tl)
-        dead2 = seen & (fired2 == 0) & ~is_sens
-        rate = (fired2[dead] / len(obs)).mean() if dead.any() else 0.0
-        print(f"   pass {it}: firing share per hop {[round(v, 3) for v in share2]}; still silent {int(dead2.sum()):,}; "
-              f"the revived fire {rate:.3f} of the time; KL {kl1:.4f}")
-        if abs(kl1 - kl0) >= 1e-4 * max(1.0, abs(kl0)):
+    rev = Revival(net, P, dead, args.seed)
+    print("re-signed {:,} incoming strengths, zeroed {:,} outgoing ones and the action weights of {} descending "
+          "neurons".format(*rev.counts))
+    for k in range(args.passes + 1):
+        fired2, _, rms, share2, kl = net.survey(rev.P, obs, teacher)
+        still = seen & (fired2 == 0) & outside
+        woke = float((fired2[dead] / n).mean()) if dead.any() else 0.0
+        print(f"   pass {k}: firing share per hop {[round(v, 3) for v in share2]}; still silent {int(still.sum()):,}; "
+              f"the revived fire {woke:.3f} of the time; KL {kl:.4f}")
+        if abs(kl - kl0) >= 1e-4 * max(1.0, abs(kl0)):
             raise SystemExit("the surgery changed the network's output")
-        if it == args.passes:
-            break
-        scale = np.ones(s["n_neurons"], np.float32)
-        m = dead & (rms > 0)
-        scale[m] = np.clip(args.target / rms[m], 0.02, 200.0)
-        w[inc] *= scale[net.post[inc]]
-    write_params(P2, Path(args.out), step)
+        if k < args.passes:
+            rev.rescale(rms, args.target)
+    write_params(rev.P, Path(args.out), step)
     print("wrote", args.out)
     return 0
 

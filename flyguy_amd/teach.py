@@ -1,21 +1,24 @@
-"""Teach a fly network to choose what a teacher chooses: the small, all-PyTorch loop of flyguy/teach.py.
+"""Teach a fly network to choose what a teacher chooses: the small, all-PyTorch teaching loop (flyguy/teach.py).
 
     python -m flyguy_amd.teach --data MOMENTS.bin [MORE.bin ...] --graph GRAPH.npz [--teacher TEACHER.pt]
         [--start fresh | CKPT.pt] [--hops 3] [--steps 3000] [--batch 128] [--lr 4e-4] [--temp 0.5] [--average 0.999]
         [--holdout 0.05] [--eval-every 250] [--out runs/teach/student.pt] [--device cuda] [--kernel torch|hip] [--seed 0]
 
-DATA: game moments, any mix of FLYD files (observations as 16-bit floats, and the teacher's answers when the file
-holds them) and FLYR recordings of the bot (teach.py:53-66).  The last --holdout share of every file is never
-learned from; "unseen" in the log is the share of those moments on which the student's first choice is the
-teacher's.  The teacher scores the 90 actions of a moment: a fly actor checkpoint (--teacher; its "model" holds the
-actor.* weights of a network on --teacher-graph, by default --graph), or, without --teacher, the answers stored in
-the FLYD files.  The reference builds any model its factory knows as the teacher; the factory and the other network
-kinds are outside this package.
+What is learned: a teacher scores the 90 actions of a game moment, and the student - a FlyActor on --graph - is
+moved toward the same answer: the loss is KL(teacher || student) with the teacher's logits sharpened by --temp.
+Teachers: a fly-actor checkpoint (--teacher; its "model" holds actor.* weights of a network on --teacher-graph, by
+default --graph), or, without --teacher, the answers stored in the FLYD files.  (The reference can build any network
+its model factory knows as the teacher; the factory and those networks are outside this package.)
 
-The student: a FlyActor on --graph, fresh (--start fresh: strengths from the synapse counts and transmitter signs) or
-from a checkpoint.  Adam with the neurons' gains and thresholds at 0.3 of the rate, the rate falling to a tenth by
-the end, the loss the distance from the teacher's answer sharpened by --temp, and a running average of the weights
-that is scored and saved (teach.py:96-165).  --kernel hip runs the hops on the MI355X library (HopHip).
+DATA: FLYD files (observations as binary16, and the teacher's answers when the file has them) and FLYR recordings
+of the bot, in any mix (teach.py:53-66).  The last --holdout share of every file is never learned from; the log's
+"unseen" figures are measured on (at most about 4,096 of) those held-out moments.
+
+Training (teach.py:96-165): Adam over three groups - the strengths and the plugs at --lr, the neurons' gains and
+thresholds at 0.3 of it - with every rate decaying geometrically to a tenth at the last step; batches are drawn
+uniformly with replacement (numpy default_rng(--seed)) and sorted.  A running average of the weights (decay
+--average, but never slower than step / (step + 9), so that a young average follows closely) is what is scored and
+saved.  --kernel hip runs the student's products on the MI355X library (HopHip).
 """
 from __future__ import annotations
 
@@ -31,27 +34,145 @@ import torch
 from .fly import FlyActor
 
 
+# ------------------------------------------------------------------------------------------------ data
 def moments(path: Path):
     """(observations [n, obs size] float16, teacher answers [n, n_act] float16 or None) of a FLYD file or a FLYR
-    recording (teach.py:53-66)."""
+    recording of the bot (teach.py:53-66)."""
     with open(path, "rb") as fh:
-        kind = fh.read(4)
-        if kind == b"FLYD":
-            n, od, na = struct.unpack("<qii", fh.read(16))
-            obs = np.memmap(path, np.float16, "r", 20, (n, od))
-            ans = np.memmap(path, np.float16, "r", 20 + 2 * n * od, (n, na)) if na > 0 else None
-            return obs, ans
-        if kind == b"FLYR":
-            od, extra = struct.unpack("<ii", fh.read(8))
-            rec = 8 + extra + 2 * od
-            n = (path.stat().st_size - 12) // rec
-            raw = np.memmap(path, np.uint8, "r", 12, (n, rec))
-            return np.ascontiguousarray(raw[:, 8 + extra:]).view(np.float16), None
+        tag = fh.read(4)
+        head = fh.read(16)
+    if tag == b"FLYD":
+        n, obs_dim, n_ans = struct.unpack("<qii", head)
+        obs = np.memmap(path, np.float16, "r", 20, (n, obs_dim))
+        ans = np.memmap(path, np.float16, "r", 20 + 2 * n * obs_dim, (n, n_ans)) if n_ans > 0 else None
+        return obs, ans
+    if tag == b"FLYR":
+        obs_dim, extra = struct.unpack("<ii", head[:8])
+        record = 8 + extra + 2 * obs_dim                 # each decision: 8 bytes, `extra` bytes, the observation
+        n = (Path(path).stat().st_size - 12) // record
+        rows = np.memmap(path, np.uint8, "r", 12, (n, record))
+        return np.ascontiguousarray(rows[:, record - 2 * obs_dim:]).view(np.float16), None
     raise SystemExit(f"{path}: neither a FLYD file nor a recording of the bot")
 
 
-def _actor_state(ck: dict) -> dict:
+class Moments:
+    """The moments of all data files, cut into the part learned from and the held-out part (the last `holdout` share
+    of every file), the held-out part thinned to about 4,096 moments."""
+
+    def __init__(self, paths: list[Path], holdout: float, need_answers: bool):
+        learn, held, learn_t, held_t = [], [], [], []
+        for p in paths:
+            obs, ans = moments(p)
+            if need_answers and ans is None:
+                raise SystemExit(f"{p}: no teacher's answers in the file and no --teacher")
+            keep = len(obs) - max(1, int(len(obs) * holdout))
+            learn.append(obs[:keep])
+            held.append(obs[keep:])
+            if ans is not None:
+                learn_t.append(ans[:keep])
+                held_t.append(ans[keep:])
+            print(f"{p.name}: {len(obs):,} moments, the last {len(obs) - keep:,} held out", flush=True)
+        stride = max(1, sum(len(h) for h in held) // 4096)
+        self.obs_dim = learn[0].shape[1]
+        self.learn = torch.from_numpy(np.concatenate(learn))
+        self.held = torch.from_numpy(np.concatenate(held)[::stride].copy())
+        self.learn_answers = self.held_answers = None
+        if need_answers:
+            self.learn_answers = torch.from_numpy(np.concatenate(learn_t))
+            self.held_answers = torch.from_numpy(np.concatenate(held_t)[::stride].copy())
+
+
+# ------------------------------------------------------------------------------------------------ teacher
+def _actor_weights(ck: dict) -> dict:
     return {k[len("actor."):]: v for k, v in ck["model"].items() if k.startswith("actor.")}
+
+
+class Teacher:
+    """The teacher's logits for a batch of moments: a fly actor's, or the answers stored with the moments."""
+
+    def __init__(self, data: Moments, checkpoint: Path | None, graph: str, fallback_graph: str, hops: int, device):
+        """graph: --teacher-graph (may be empty: then the checkpoint's own config.model.fly_graph, then
+        fallback_graph, the student's)."""
+        self.data, self.device = data, device
+        self.net = None
+        self.name = "the answers in the data"
+        if checkpoint is not None:
+            ck = torch.load(checkpoint, map_location="cpu", weights_only=True)
+            cfg = (ck.get("config") or {}).get("model", {})
+            net = FlyActor(graph or cfg.get("fly_graph") or fallback_graph, data.obs_dim, 90,
+                           hops=int(cfg.get("fly_hops", hops)))
+            net.load_state_dict(_actor_weights(ck), strict=False)
+            self.net = net.to(device).eval()
+            self.name = checkpoint.name
+
+    @property
+    def n_act(self) -> int:
+        return 90 if self.net is not None else self.data.learn_answers.shape[1]
+
+    def logits(self, x: torch.Tensor, rows, held: bool) -> torch.Tensor:
+        if self.net is not None:
+            return self.net(x).float()
+        stored = self.data.held_answers if held else self.data.learn_answers
+        return stored[rows].to(self.device).float()
+
+
+# ------------------------------------------------------------------------------------------------ student
+def kl_to(target: torch.Tensor, logits: torch.Tensor) -> torch.Tensor:
+    """Per moment: KL(target || softmax(logits)), target a probability vector (teach.py:139-141)."""
+    return (target * (torch.log(target.clamp_min(1e-12)) - torch.log_softmax(logits, -1))).sum(-1)
+
+
+class Student:
+    """The network being taught, its optimiser and learning-rate schedule, and the running average of its weights."""
+
+    NEURON_SHARE = 0.3                   # the gains' and thresholds' rate, as a share of --lr
+
+    def __init__(self, net: FlyActor, shown: FlyActor, lr: float, steps: int, average: float):
+        self.net, self.shown = net, shown
+        self.steps, self.average = steps, average
+        neuron = [net.gain, net.theta]
+        others = [p for name, p in net.named_parameters() if name not in ("w", "gain", "theta")]
+        self.opt = torch.optim.Adam([{"params": [net.w], "lr": lr},
+                                     {"params": neuron, "lr": self.NEURON_SHARE * lr},
+                                     {"params": others, "lr": lr}])
+        self.base = [g["lr"] for g in self.opt.param_groups]
+
+    def learn(self, step: int, x: torch.Tensor, target: torch.Tensor) -> float:
+        decay = 0.1 ** (step / self.steps)               # a tenth of the rate at the last step
+        for g, b in zip(self.opt.param_groups, self.base):
+            g["lr"] = b * decay
+        loss = kl_to(target, self.net(x).float()).mean()
+        self.opt.zero_grad(set_to_none=True)
+        loss.backward()
+        self.opt.step()
+        follow = 1.0 - min(self.average, step / (step + 9.0))
+        with torch.no_grad():
+            for a, b in zip(self.shown.parameters(), self.net.parameters()):
+                a.lerp_(b, follow)
+        return float(loss.detach())
+
+
+@torch.no_grad()
+def score(shown: FlyActor, teacher: Teacher, data: Moments, temp: float, device) -> tuple[float, float]:
+    """On the held-out moments: the share where the student's first choice is the teacher's, and the mean KL."""
+    agree = total = 0.0
+    for i in range(0, len(data.held), 512):
+        x = data.held[i:i + 512].to(device).float()
+        t = teacher.logits(x, slice(i, i + 512), held=True)
+        s = shown(x).float()
+        agree += float((t.argmax(-1) == s.argmax(-1)).sum())
+        total += float(kl_to(torch.softmax(t / temp, -1), s).sum())
+    return agree / len(data.held), total / len(data.held)
+
+
+def _make_student(args, obs_dim: int, n_act: int) -> tuple[FlyActor, int]:
+    if args.start == "fresh":
+        return FlyActor(args.graph, obs_dim, n_act, hops=args.hops, fan=args.fan), 0
+    ck = torch.load(args.start, map_location="cpu", weights_only=True)
+    cfg = (ck.get("config") or {}).get("model", {})
+    net = FlyActor(args.graph, obs_dim, n_act, hops=int(cfg.get("fly_hops", args.hops)), fan=args.fan)
+    net.load_state_dict(_actor_weights(ck), strict=False)
+    return net, int(ck.get("taught_steps", 0))
 
 
 def main(argv=None) -> int:
@@ -76,109 +197,45 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel", default="torch", choices=["torch", "hip", "cuda"])
     ap.add_argument("--seed", type=int, default=0)
     args = ap.parse_args(argv)
-    dev = torch.device(args.device)
+    device = torch.device(args.device)
     torch.manual_seed(args.seed)
-    rng = np.random.default_rng(args.seed)
+    draw = np.random.default_rng(args.seed)
 
-    # ---- the game moments (and the teacher's answers where the files hold them)
-    seen, unseen, seen_t, unseen_t = [], [], [], []
-    for p in args.data:
-        m, ans = moments(p)
-        if args.teacher is None and ans is None:
-            raise SystemExit(f"{p}: no teacher's answers in the file and no --teacher")
-        cut = len(m) - max(1, int(len(m) * args.holdout))
-        seen.append(m[:cut]); unseen.append(m[cut:])
-        if ans is not None:
-            seen_t.append(ans[:cut]); unseen_t.append(ans[cut:])
-        print(f"{p.name}: {len(m):,} moments, the last {len(m) - cut:,} held out", flush=True)
-    od = seen[0].shape[1]
-    every = max(1, sum(len(u) for u in unseen) // 4096)                    # (4,096 of them are enough)
-    seen = torch.from_numpy(np.concatenate(seen))
-    unseen = torch.from_numpy(np.concatenate(unseen)[::every].copy())
-    stored = args.teacher is None
-    if stored:
-        seen_t = torch.from_numpy(np.concatenate(seen_t))
-        unseen_t = torch.from_numpy(np.concatenate(unseen_t)[::every].copy())
+    data = Moments(args.data, args.holdout, need_answers=args.teacher is None)
+    teacher = Teacher(data, args.teacher, args.teacher_graph, args.graph, args.hops, device)
+    net, step0 = _make_student(args, data.obs_dim, teacher.n_act)
+    net.kernel = "torch" if args.kernel == "torch" else "hip"
+    net = net.to(device)
+    shown = FlyActor(args.graph, data.obs_dim, teacher.n_act, hops=net.hops, fan=args.fan).to(device).eval()
+    shown.load_state_dict(net.state_dict())
+    print(net.describe(), flush=True)
+    student = Student(net, shown, args.lr, args.steps, args.average)
+    saved_cfg = {"fly_graph": str(args.graph), "fly_hops": net.hops, "fly_kernel": "torch"}
 
-    # ---- the teacher, and the student
-    teacher = None
-    n_act = seen_t.shape[1] if stored else 90
-    if not stored:
-        tck = torch.load(args.teacher, map_location="cpu", weights_only=True)
-        tcfg = (tck.get("config") or {}).get("model", {})
-        teacher = FlyActor(args.teacher_graph or tcfg.get("fly_graph") or args.graph, od, 90,
-                           hops=int(tcfg.get("fly_hops", args.hops)))
-        teacher.load_state_dict(_actor_state(tck), strict=False)
-        teacher = teacher.to(dev).eval()
-    if args.start == "fresh":
-        student, step0 = FlyActor(args.graph, od, n_act, hops=args.hops, fan=args.fan), 0
-    else:
-        sck = torch.load(args.start, map_location="cpu", weights_only=True)
-        scfg = (sck.get("config") or {}).get("model", {})
-        student = FlyActor(args.graph, od, n_act, hops=int(scfg.get("fly_hops", args.hops)), fan=args.fan)
-        student.load_state_dict(_actor_state(sck), strict=False)
-        step0 = int(sck.get("taught_steps", 0))
-    student.kernel = "hip" if args.kernel in ("hip", "cuda") else "torch"
-    student = student.to(dev)
-    shown = FlyActor(args.graph, od, n_act, hops=student.hops, fan=args.fan).to(dev).eval()   # the running average
-    shown.load_state_dict(student.state_dict())
-    print(student.describe(), flush=True)
-    cfg = {"fly_graph": str(args.graph), "fly_hops": student.hops, "fly_kernel": "torch"}
-
-    def answers(x, idx, held):
-        if stored:
-            return (unseen_t if held else seen_t)[idx].to(dev).float()
-        return teacher(x).float()
-
-    @torch.no_grad()
-    def score() -> tuple[float, float]:
-        same = kl = 0.0
-        for i in range(0, len(unseen), 512):
-            x = unseen[i:i + 512].to(dev).float()
-            t = answers(x, slice(i, i + 512), True)
-            s = shown(x).float()
-            same += float((t.argmax(-1) == s.argmax(-1)).sum())
-            target = torch.softmax(t / args.temp, -1)
-            kl += float((target * (torch.log(target.clamp_min(1e-12)) - torch.log_softmax(s, -1))).sum())
-        return same / len(unseen), kl / len(unseen)
-
-    plugs = [p for k, p in student.named_parameters() if k not in ("w", "gain", "theta")]
-    opt = torch.optim.Adam([{"params": [student.w], "lr": args.lr},
-                            {"params": [student.gain, student.theta], "lr": 0.3 * args.lr},
-                            {"params": plugs, "lr": args.lr}])
-    base = [g["lr"] for g in opt.param_groups]
-    a0, k0 = score()
-    a = a0
-    print(f"start | unseen: same first choice {a0:.3f}, distance {k0:.3f} | {len(seen):,} moments to learn from, "
-          f"{args.steps * args.batch / len(seen):.1f} passes over them", flush=True)
-    t0, run = time.time(), 0.0
+    first, first_kl = score(shown, teacher, data, args.temp, device)
+    agree = first
+    print(f"start | unseen: same first choice {first:.3f}, distance {first_kl:.3f} | {len(data.learn):,} moments to "
+          f"learn from, {args.steps * args.batch / len(data.learn):.1f} passes over them", flush=True)
+    began, smooth = time.time(), 0.0
     for step in range(1, args.steps + 1):
-        for g, b in zip(opt.param_groups, base):                   # the rate falls to a tenth by the end
-            g["lr"] = b * 0.1 ** (step / args.steps)
-        idx = torch.as_tensor(np.sort(rng.integers(0, len(seen), args.batch)))
-        x = seen[idx].to(dev).float()
+        rows = torch.as_tensor(np.sort(draw.integers(0, len(data.learn), args.batch)))
+        x = data.learn[rows].to(device).float()
         with torch.no_grad():
-            target = torch.softmax(answers(x, idx, False) / args.temp, -1)
-        loss = (target * (torch.log(target.clamp_min(1e-12)) - torch.log_softmax(student(x).float(), -1))).sum(-1).mean()
-        opt.zero_grad(set_to_none=True)
-        loss.backward()
-        opt.step()
-        keep = min(args.average, step / (step + 9.0))               # (a young average follows closely)
-        with torch.no_grad():
-            for sa, sb in zip(shown.parameters(), student.parameters()):
-                sa.lerp_(sb, 1.0 - keep)
-        run = loss.item() if step == 1 else 0.98 * run + 0.02 * loss.item()
-        if step % args.eval_every == 0 or step == args.steps:
-            a, k = score()
-            print(f"step {step:,} | distance {run:.3f} | unseen: same first choice {a:.3f}, distance {k:.3f} | "
-                  f"{step * args.batch / (time.time() - t0):,.0f} moments a second", flush=True)
-            args.out.parent.mkdir(parents=True, exist_ok=True)
-            torch.save({"model": {"actor." + k_: v.detach().cpu() for k_, v in shown.state_dict().items()},
-                        "steps": step0 + step, "taught_steps": step0 + step, "config": {"model": cfg},
-                        "taught_by": args.teacher.name if args.teacher else "the answers in the data",
-                        "unseen_same_first_choice": a}, args.out)
-    print(f"saved {args.out} (the running average; the teacher's first choice on {a:.3f} of unseen moments, {a0:.3f} at "
-          f"the start)")
+            target = torch.softmax(teacher.logits(x, rows, held=False) / args.temp, -1)
+        loss = student.learn(step, x, target)
+        smooth = loss if step == 1 else 0.98 * smooth + 0.02 * loss
+        if step % args.eval_every and step != args.steps:
+            continue
+        agree, dist = score(shown, teacher, data, args.temp, device)
+        rate = step * args.batch / (time.time() - began)
+        print(f"step {step:,} | distance {smooth:.3f} | unseen: same first choice {agree:.3f}, distance {dist:.3f} | "
+              f"{rate:,.0f} moments a second", flush=True)
+        args.out.parent.mkdir(parents=True, exist_ok=True)
+        torch.save({"model": {"actor." + k: v.detach().cpu() for k, v in shown.state_dict().items()},
+                    "steps": step0 + step, "taught_steps": step0 + step, "config": {"model": saved_cfg},
+                    "taught_by": teacher.name, "unseen_same_first_choice": agree}, args.out)
+    print(f"saved {args.out} (the running average; the teacher's first choice on {agree:.3f} of unseen moments, "
+          f"{first:.3f} at the start)")
     return 0
 
 

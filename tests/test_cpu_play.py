@@ -49,11 +49,11 @@ def test_actor_cpu_play(monkeypatch, name, hops, fan):
     want = Oracle(net_bytes(s), params_from_torch(f, s), "f64").forward(obs)
     with torch.no_grad():
         got = f(torch.as_tensor(obs)).numpy()
-        assert f._nat["h"]                                      # the library played
+        assert f._decider[1] is not None                        # the library played
         monkeypatch.setenv("FLYGUY_NATIVE", "0")
         f.w.mul_(1.0)                                           # (a new weight version: set-up again, now without it)
         sparse = f(torch.as_tensor(obs)).numpy()
-        assert not f._nat["h"]
+        assert f._decider[1] is None
     scale = max(1.0, np.abs(want).max())
     assert np.abs(got - want).max() <= 1e-5 * scale
     assert np.abs(sparse - want).max() <= 1e-5 * scale
@@ -151,5 +151,5 @@ def test_actor_cpu_play_on_several_threads(monkeypatch):
         monkeypatch.setenv("FLYGUY_CPU_THREADS", "4")
         f.w.mul_(1.0)                                           # (a new weight version: set-up again, on 4 threads)
         four = f(obs).numpy()
-        assert f._nat["h"]
+        assert f._decider[1] is not None
     assert np.array_equal(four.view(np.uint32), one.view(np.uint32))
