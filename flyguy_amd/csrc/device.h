@@ -108,6 +108,14 @@ struct Slab {
     }
 };
 
+// Whether the 8-lane group's line of a state is zero on all of its samples (every lane of the wave must call this).  A
+// neuron's output is relu(...) >= 0, so a line of h with no sample > 0 is a neuron that fires on none of the tile's
+// samples: its gradient g = (h > 0 ? gh : 0) is zero there whatever gh is.
+__device__ __forceinline__ bool group_silent(const float4& h) {
+    const unsigned long long fires = __ballot(h.x > 0.f || h.y > 0.f || h.z > 0.f || h.w > 0.f);
+    return ((fires >> (threadIdx.x & 56)) & 0xFFull) == 0;
+}
+
 // Reduce-scatter over the 8 lanes of a group: lane s ends with the sum over the group's lanes of d[s].  Three
 // butterfly steps, each pairing lanes that hold the same set of slots and keeping the half named by a lane bit:
 // lanes i and 7-i (row_half_mirror) split the slots by bit 2, then i and i^2, then i and i^1 (quad perms).

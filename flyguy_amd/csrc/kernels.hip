@@ -301,12 +301,16 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
+    // The source row's own line (the per-edge gradient's operand) comes first, with the wave's first pairs: with a
+    // neuron backward (MODE 1, 2) a row that fires on none of the tile's samples has g = 0 there, so its gathers are
+    // skipped (NO_ROW reads zeros without touching memory); its sums and partials are zero either way.
     float4 hj = splat(0.f);
+    if (live) hj = MODE == 0 ? *at4(hs, lhs, tile, sg.x, sub) : *at4u(hs, lhs, tile, sg.x, sub);
+    const bool quiet = MODE != 0 && group_silent(hj);
     const Slab<TILED> slab(gz + (size_t)tile * lg.tile, lg.row, gz_rows, sub);
     // the partial of (position, tile) of this lane's slot: one contiguous 256-byte block per wave and step
     float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
     float4 acc = splat(0.f);
-    BwdIn in{};
     const bool whole = live && sg.y < 0;
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
@@ -314,13 +318,9 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
         stage8(slots[grp], sub, nxt, c, wt);
         float4 v[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(c[s], sub) : splat(0.f);
+        for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(quiet ? NO_ROW : c[s], sub) : splat(0.f);
         __builtin_amdgcn_sched_barrier(0);
         if (left > 8) nxt = q[64 * (j + 1)];
-        if (j == 0) {                           // the row's own inputs, after the first gathers (see k_fwd)
-            if (live) hj = MODE == 0 ? *at4(hs, lhs, tile, sg.x, sub) : *at4u(hs, lhs, tile, sg.x, sub);
-            if (whole) in = bwd_inputs<MODE>(epi, sg.x, sg.z, tile, sub);
-        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 8; ++s) fma4(wt[s], v[s], acc);
@@ -331,8 +331,11 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
             gwp[64 * j] = rs8(d, sub);
         }
     }
-    if (whole && !(wok && wv.y > 0)) in = bwd_inputs<MODE>(epi, sg.x, sg.z, tile, sub);
     if (!live) return;
+    // the row's other inputs of the neuron backward, after the loop: live across it they would cost registers, and
+    // with them waves per SIMD
+    BwdIn in{};
+    if (whole) in = bwd_inputs_h<MODE>(epi, sg.x, sg.z, tile, sub, hj);
     if (sg.y >= 0) {
         *at4w(part, lp, tile, sg.y, sub) = acc;
         return;
@@ -360,12 +363,17 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
     int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
+    // the source row's own lines first, and on a tile where the row fires on no sample its gathers are skipped (k_bwd)
     float4 hja = splat(0.f), hjb = splat(0.f);
+    if (live) {
+        hja = *at4u(hs, lhs, ta, sg.x, sub);
+        if (hasb) hjb = *at4u(hs, lhs, tb, sg.x, sub);
+    }
+    const bool quiet_a = group_silent(hja), quiet_b = group_silent(hjb);
     const Slab<true> sa(gz + (size_t)ta * lg.tile, lg.row, gz_rows, sub);
     const Slab<true> sb(gz + (size_t)(hasb ? tb : ta) * lg.tile, lg.row, gz_rows, sub);
     float* gwp = gwpart ? gwpart + (size_t)pr * gw_ld + wv.x + lane : nullptr;
     float4 acca = splat(0.f), accb = splat(0.f);
-    BwdIn ina{}, inb{};
     const bool whole = live && sg.y < 0;
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
@@ -373,21 +381,11 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
         stage8(slots[grp], sub, nxt, c, wt);
         float4 va[8], vb[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) va[s] = s < left ? sa.get(c[s], sub) : splat(0.f);
+        for (int s = 0; s < 8; ++s) va[s] = s < left ? sa.get(quiet_a ? NO_ROW : c[s], sub) : splat(0.f);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) vb[s] = (hasb && s < left) ? sb.get(c[s], sub) : splat(0.f);
+        for (int s = 0; s < 8; ++s) vb[s] = (hasb && s < left) ? sb.get(quiet_b ? NO_ROW : c[s], sub) : splat(0.f);
         __builtin_amdgcn_sched_barrier(0);
         if (left > 8) nxt = q[64 * (j + 1)];
-        if (j == 0) {
-            if (live) {
-                hja = *at4u(hs, lhs, ta, sg.x, sub);
-                if (hasb) hjb = *at4u(hs, lhs, tb, sg.x, sub);
-            }
-            if (whole) {                        // (hs is the layer's h: the core's launches hand over e.h)
-                ina = bwd_inputs_h<MODE>(epi, sg.x, sg.z, ta, sub, hja);
-                if (hasb) inb = bwd_inputs_h<MODE>(epi, sg.x, sg.z, tb, sub, hjb);
-            }
-        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -401,11 +399,12 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
             gwp[64 * j] = rs8(d, sub);
         }
     }
-    if (whole && !(wok && wv.y > 0)) {
-        ina = bwd_inputs<MODE>(epi, sg.x, sg.z, ta, sub);
-        if (hasb) inb = bwd_inputs<MODE>(epi, sg.x, sg.z, tb, sub);
-    }
     if (!live) return;
+    BwdIn ina{}, inb{};                         // the rows' other inputs, after the loop (k_bwd)
+    if (whole) {                                // (hs is the layer's h: the core's launches hand over e.h)
+        ina = bwd_inputs_h<MODE>(epi, sg.x, sg.z, ta, sub, hja);
+        if (hasb) inb = bwd_inputs_h<MODE>(epi, sg.x, sg.z, tb, sub, hjb);
+    }
     if (sg.y >= 0) {
         *at4w(part, lp, ta, sg.y, sub) = acca;
         if (hasb) *at4w(part, lp, tb, sg.y, sub) = accb;
