@@ -82,6 +82,14 @@ struct Core {
     double s_samples = 0;
     long long rows_total = 0;
     int prec = 0;                    // 0: float32 states [B/32][rows][32]; 1: bfloat16 states [B/64][rows][64]
+    // Whether rows fire, for layers 0 .. hops-1: per (tile, row) a byte written by the layer's forward
+    // (fire_bytes[layer], [Tm][fires_bytes_ld(rows)]) and the bitmaps packed from them (fire_bits[layer], [Tm][fires_ld(rows)]).
+    // The forward of hop k skips the gathers of layer k-1's rows that fire on no sample of a tile, and the backward
+    // those of rows whose own output is zero on the tile.  skip_silent false (FLYGUY_SKIP_SILENT=0): neither (the
+    // results are the same).
+    bool skip_silent = true;
+    std::vector<unsigned char*> fire_bytes;
+    std::vector<unsigned*> fire_bits;
     long long adam_t = 0;
     int B = 0;
     hipStream_t st = nullptr;

@@ -417,6 +417,12 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     }
     c->info0 = dalloc<float4>(*c, c->n_s);
     if (!c->info0) return nullptr;
+    if (const char* f = std::getenv("FLYGUY_SKIP_SILENT")) c->skip_silent = f[0] != '0';
+    for (int l = 0; l < K; ++l) {                   // (the top layer's would have no reader)
+        c->fire_bytes.push_back(dalloc<unsigned char>(*c, Tm * (size_t)fires_bytes_ld(c->sizes[l])));
+        c->fire_bits.push_back(dalloc<unsigned>(*c, Tm * (size_t)fires_ld(c->sizes[l])));
+        if (!c->fire_bytes.back() || !c->fire_bits.back()) return nullptr;
+    }
     c->lg = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->dl = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->part = dalloc<float>(*c, Tm * std::max<long long>(max_slot, 1) * S);
@@ -493,12 +499,20 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
         FG_CHECK(pack(c, set, false, false), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
+    // each layer below the top records which rows fire on each tile; its bitmaps are packed before the next hop
+    auto bytes = [&](int layer) { return c.skip_silent ? c.fire_bytes[(size_t)layer] : nullptr; };
+    auto bits = [&](int layer) { return c.skip_silent ? c.fire_bits[(size_t)layer] : nullptr; };
     FwdEpi e0;
     e0.bias = c.arr(set, 4);
     e0.info = c.info0;
     e0.z = c.drive; e0.lz = tiled(c.n_s);
     e0.h = c.h0; e0.lh = tiled(c.n_s);
-    { Timed t(c, ST_PLUG); FG_CHECK(launch_fwd(c.pp.view(), c.in_cw, c.x, tiled(c.obs_dim), c.obs_dim, e0, c.part, tiled(c.pp.nslot), T, st), false); }
+    e0.fires = bytes(0);
+    {
+        Timed t(c, ST_PLUG);
+        FG_CHECK(launch_fwd(c.pp.view(), c.in_cw, c.x, tiled(c.obs_dim), c.obs_dim, e0, c.part, tiled(c.pp.nslot), T, st), false);
+        if (c.skip_silent) FG_CHECK(launch_fires_pack(bytes(0), c.n_s, bits(0), T, st), false);
+    }
     const float* hp = c.h0;
     int hk = 0;
     for (auto& d : c.hop) {
@@ -507,7 +521,13 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
         if (d.has_drive) { e.drive = c.drive; e.ldrive = tiled(c.n_s); }
         e.h = d.h; e.lh = tiled(d.rows);
         if (c.keep_z) { e.z = d.zk; e.lz = tiled(d.rows); }
-        { Timed t(c, ST_HOP + std::min(hk, 7)); FG_CHECK(launch_fwd(d.fp.view(), d.cw, hp, tiled(d.src), d.src, e, c.part, tiled(d.fp.nslot), T, st), false); }
+        const bool record = hk + 1 < c.hops;
+        if (record) e.fires = bytes(hk + 1);
+        {
+            Timed t(c, ST_HOP + std::min(hk, 7));
+            FG_CHECK(launch_fwd(d.fp.view(), d.cw, hp, tiled(d.src), d.src, e, c.part, tiled(d.fp.nslot), T, st, bits(hk)), false);
+            if (record && c.skip_silent) FG_CHECK(launch_fires_pack(bytes(hk + 1), d.rows, bits(hk + 1), T, st), false);
+        }
         hp = d.h;
         ++hk;
     }
@@ -566,6 +586,7 @@ bool backward(Core& c, const float* dlogits, int B) {
         HopD& d = c.hop[k - 1];
         BwdEpi e;
         e.gdrive = c.gdrive; e.lgd = tiled(c.n_s);
+        e.skip_silent = c.skip_silent;
         const float* hbelow;
         int rows_below;
         float *ggp, *gsp;

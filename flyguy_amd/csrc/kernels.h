@@ -55,6 +55,9 @@ struct FwdEpi {
     Lay lz{};
     float* h = nullptr;
     Lay lh{};
+    // Per tile a byte per row: 1 when the row fires (h > 0) on some sample of the tile, else 0 ([T][fires_bytes_ld(rows)];
+    // every row of the tile is written).  launch_fires_pack turns them into the bitmap the next hop reads.  nullptr: off.
+    unsigned char* fires = nullptr;
 };
 
 // The backward through a layer of neurons (flyguy_train.cu:143-156 and, for the sensory layer, 174-179 and the
@@ -74,6 +77,7 @@ struct BwdEpi {
     float* gdrive = nullptr;      // the drive's gradient: a re-drive row d >= 0 adds into it; -(d + 3): writes it
     Lay lgd{};                    //   first (no load); a sensory row of re-drive field -2 reads 0 from it
     bool first = false;           // mode 1: every re-drive row of the rows writes first (the top layer)
+    bool skip_silent = true;      // modes 1, 2: skip the gathers of a source row whose output is zero on the tile
     float* ggain_part = nullptr;  // [T][gp_ld]: sum over the tile of g * z, in plan columns: a whole row at its
     float* gsum_part = nullptr;   //   segment, split row i at nseg + i (the read-out kernel: the row itself);
     long long gp_ld = 0;          //   [T][gp_ld]: sum over the tile of g
@@ -103,9 +107,19 @@ struct PackJob {
 };
 constexpr int PACK_JOBS = 4;
 hipError_t launch_pack_n(const PackJob* jobs, int n, hipStream_t st, bool bf16w = false);
-// src_rows / gz_rows: rows of the gathered state (a gather of a row outside it reads zeros)
+// src_rows / gz_rows: rows of the gathered state (a gather of a row outside it reads zeros).  src_fires: the source
+// layer's firing bitmaps (launch_fires_pack; fires_ld(src_rows) words per tile; tiled states only), or nullptr
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
-                      float* part, Lay lp, int T, hipStream_t st);
+                      float* part, Lay lp, int T, hipStream_t st, const unsigned* src_fires = nullptr);
+// A tile's firing bitmap: 4 header words (word 0: the number of rows that fire on no sample of the tile), then a
+// bit per row (row r: bit r % 32 of word 4 + r / 32), padded to whole 16-byte units.
+inline int fires_ld(int rows) { return 4 + ((rows + 31) / 32 + 3) / 4 * 4; }
+// the bytes of a tile, rows rounded up to whole 32-row words (the pack reads each word's bytes as two 16-byte loads)
+__host__ __device__ inline int fires_bytes_ld(int rows) { return (rows + 31) / 32 * 32; }
+// the largest bitmap (words per tile) a hop kernel stages in LDS; a larger source layer's bits are not used
+constexpr int FIRES_LDS_WORDS = 8192;
+// bytes [T][fires_bytes_ld(rows)] (FwdEpi::fires) -> bitmaps [T][fires_ld(rows)]
+hipError_t launch_fires_pack(const unsigned char* bytes, int rows, unsigned* bits, int T, hipStream_t st);
 // gwpart: the per-position weight-gradient partials, gw_ld apart, one row per tile; with pair (a tiled layer backward,
 // modes 1 and 2, whose hsrc must be epi.h: the layer's own output) one row per pair of tiles (tiles 2p and 2p + 1
 // summed), ceil(T / 2) rows, and so are the rows' gain and threshold partials (epi.ggain_part, epi.gsum_part)

@@ -87,6 +87,7 @@ __device__ __forceinline__ void st_stream(float4* p, const float4& v) {
     const f4v t = {v.x, v.y, v.z, v.w};
     __builtin_nontemporal_store(t, reinterpret_cast<f4v*>(p));
 }
+// (the lanes of whole 8-lane groups call this together)
 __device__ __forceinline__ void fwd_finish(const FwdEpi& e, int t, int tile, int sub, float4 acc, const FwdIn& in) {
     if (e.drive) add4(in.dv, acc);              // (zero when the row has no re-drive)
     if (e.z) st_stream(at4w(e.z, e.lz, tile, t, sub), acc);
@@ -95,15 +96,32 @@ __device__ __forceinline__ void fwd_finish(const FwdEpi& e, int t, int tile, int
         const float4 hv = make_float4(fmaxf(fmaf(g, acc.x, -sp), 0.f), fmaxf(fmaf(g, acc.y, -sp), 0.f),
                                       fmaxf(fmaf(g, acc.z, -sp), 0.f), fmaxf(fmaf(g, acc.w, -sp), 0.f));
         st_stream(at4uw(e.h, e.lh, tile, t, sub), hv);
+        if (e.fires) {                          // whether the row fires on some sample of the tile
+            const bool on = !group_silent(hv);
+            if (sub == 0) e.fires[(size_t)tile * fires_bytes_ld((int)(e.lh.tile / TW)) + t] = on ? 1 : 0;   // (tiled h)
+        }
     }
 }
 
 template <bool TILED>
 __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw, const float* __restrict__ src, Lay ls,
-                                            int src_rows, FwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB) {
+                                            int src_rows, FwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB,
+                                            const unsigned* __restrict__ src_fires, int fw_ld) {
     __shared__ __align__(16) int2 slots[WG / LPR][LPR];
+    extern __shared__ __align__(16) unsigned fires[];     // the source rows' firing bits of this tile
     int rb;
     const int tile = tile_of(blockIdx.x, RB, T, rb);
+    // The bitmap is staged only for a tile on which some source row is silent (its header says how many)
+    bool bits = false;
+    if (fw_ld > 0) {
+        const unsigned* b = src_fires + (size_t)tile * fw_ld;
+        if (__builtin_amdgcn_readfirstlane(b[0]) > 0) {   // (uniform: the whole workgroup reads the same word)
+            const uint4* b4 = reinterpret_cast<const uint4*>(b + 4);
+            for (int i = threadIdx.x; i < (fw_ld - 4) / 4; i += WG) reinterpret_cast<uint4*>(fires)[i] = b4[i];
+            __syncthreads();
+            bits = true;
+        }
+    }
     const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
@@ -121,6 +139,10 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     // complete in order, so requested earlier they would hold up the first gathers.  The bias still starts the sum
     // (flyguy_train.cu:75).
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
+        if (bits) {                             // a source row that fires on no sample of the tile adds zeros: skip its
+            const unsigned r = (unsigned)nxt.x; // gather (NO_ROW reads zeros without touching memory)
+            if (r >= (unsigned)src_rows || !((fires[r >> 5] >> (r & 31)) & 1u)) nxt.x = NO_ROW;
+        }
         int c[8];
         float wt[8];
         stage8(slots[grp], sub, nxt, c, wt);
@@ -177,6 +199,39 @@ __global__ __launch_bounds__(WG) void k_fwd_combine(Plan p, const float* __restr
     const FwdIn in = fwd_inputs(epi, s.x, s.w, tile, sub);
     add_parts(part, lp, tile, s.y, s.z, sub, acc);
     fwd_finish(epi, s.x, tile, sub, acc, in);
+}
+
+// One workgroup per tile: the tile's firing bytes -> its bitmap (bits, then the count of silent rows in the header)
+__global__ __launch_bounds__(WG) void k_fires_pack(const unsigned char* __restrict__ bytes, int rows,
+                                                   unsigned* __restrict__ bits, int ld) {
+    __shared__ unsigned silent[WG / 64];
+    const int tile = blockIdx.x;
+    const unsigned char* b = bytes + (size_t)tile * fires_bytes_ld(rows);
+    unsigned* out = bits + (size_t)tile * ld;
+    unsigned quiet = 0;
+    for (int w = threadIdx.x; w < ld - 4; w += WG) {
+        // the word's 32 bytes as two aligned 16-byte loads (rows of a tile are fires_bytes_ld(rows) bytes apart);
+        // each byte is 0 or 1, so bit 8 j of a 32-bit piece is row 4 i + j of the piece's 4 rows
+        unsigned m = 0;
+        if (32 * w < rows) {
+            const uint4 lo = reinterpret_cast<const uint4*>(b)[2 * w], hi = reinterpret_cast<const uint4*>(b)[2 * w + 1];
+            const unsigned v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const unsigned x = v[i] & 0x01010101u;
+                m |= ((x | (x >> 7) | (x >> 14) | (x >> 21)) & 0xFu) << (4 * i);
+            }
+            const int valid = min(32, rows - 32 * w);
+            if (valid < 32) m &= (1u << valid) - 1u;
+            quiet += (unsigned)(valid - __popc(m));
+        }
+        out[4 + w] = m;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) quiet += __shfl_xor(quiet, o, 64);
+    if ((threadIdx.x & 63) == 0) silent[threadIdx.x >> 6] = quiet;
+    __syncthreads();
+    if (threadIdx.x < 4) out[threadIdx.x] = threadIdx.x == 0 ? ((silent[0] + silent[1]) + silent[2]) + silent[3] : 0u;
 }
 
 // ------------------------------------------------------------------------------------------------ backward
@@ -306,7 +361,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     // skipped (NO_ROW reads zeros without touching memory); its sums and partials are zero either way.
     float4 hj = splat(0.f);
     if (live) hj = MODE == 0 ? *at4(hs, lhs, tile, sg.x, sub) : *at4u(hs, lhs, tile, sg.x, sub);
-    const bool quiet = MODE != 0 && group_silent(hj);
+    const bool quiet = MODE != 0 && epi.skip_silent && group_silent(hj);
     const Slab<TILED> slab(gz + (size_t)tile * lg.tile, lg.row, gz_rows, sub);
     // the partial of (position, tile) of this lane's slot: one contiguous 256-byte block per wave and step
     float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
@@ -369,7 +424,7 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
         hja = *at4u(hs, lhs, ta, sg.x, sub);
         if (hasb) hjb = *at4u(hs, lhs, tb, sg.x, sub);
     }
-    const bool quiet_a = group_silent(hja), quiet_b = group_silent(hjb);
+    const bool quiet_a = epi.skip_silent && group_silent(hja), quiet_b = epi.skip_silent && group_silent(hjb);
     const Slab<true> sa(gz + (size_t)ta * lg.tile, lg.row, gz_rows, sub);
     const Slab<true> sb(gz + (size_t)(hasb ? tb : ta) * lg.tile, lg.row, gz_rows, sub);
     float* gwp = gwpart ? gwpart + (size_t)pr * gw_ld + wv.x + lane : nullptr;
@@ -682,13 +737,16 @@ hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* c
 }
 
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
-                      float* part, Lay lp, int T, hipStream_t st) {
+                      float* part, Lay lp, int T, hipStream_t st, const unsigned* src_fires) {
     if (p.nwave > 0) {
         const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
+        const int fw = src_fires && ls.row == TW && fires_ld(src_rows) <= FIRES_LDS_WORDS ? fires_ld(src_rows) : 0;
         if (ls.row == TW)
-            k_fwd<true><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB);
+            k_fwd<true><<<(unsigned)((long long)T * RB), WG, (size_t)(fw > 0 ? fw - 4 : 0) * 4, st>>>(
+                p, cw, src, ls, src_rows, epi, part, lp, T, RB, src_fires, fw);
         else
-            k_fwd<false><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB);
+            k_fwd<false><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB,
+                                                                       nullptr, 0);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -752,6 +810,12 @@ hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, in
         default:
             return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_fires_pack(const unsigned char* bytes, int rows, unsigned* bits, int T, hipStream_t st) {
+    if (rows <= 0 || T <= 0) return hipSuccess;
+    k_fires_pack<<<(unsigned)T, WG, 0, st>>>(bytes, rows, bits, fires_ld(rows));
+    return hipGetLastError();
 }
 
 hipError_t launch_obs_in(const float* obs, float* x, int obs_dim, int B, hipStream_t st) {
