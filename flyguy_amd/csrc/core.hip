@@ -642,13 +642,20 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
         FG_CHECK(pack(c, set, false, true), false);
         FG_CHECK(rowinfo(c, gain, theta), false);
     }
+    auto bytes = [&](int layer) { return c.skip_silent ? c.fire_bytes[(size_t)layer] : nullptr; };   // (as forward)
+    auto bits = [&](int layer) { return c.skip_silent ? c.fire_bits[(size_t)layer] : nullptr; };
     FwdEpi16 e0;
     e0.bias = c.arr(set, 4);
     e0.info = c.info0;
     e0.z = s16(c.drive);
     e0.h = s16(c.h0);
     e0.rows = c.n_s;
-    { Timed t(c, ST_PLUG); FG_CHECK(launch_fwd16c(c.pp.view(), c.in_cw, s16(c.x), c.obs_dim, e0, c.part, T, st), false); }
+    e0.fires = bytes(0);
+    {
+        Timed t(c, ST_PLUG);
+        FG_CHECK(launch_fwd16c(c.pp.view(), c.in_cw, s16(c.x), c.obs_dim, e0, c.part, T, st), false);
+        if (c.skip_silent) FG_CHECK(launch_fires_pack(bytes(0), c.n_s, bits(0), T, st), false);
+    }
     const u16* hp = s16(c.h0);
     int hk = 0;
     for (auto& d : c.hop) {
@@ -658,7 +665,13 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
         e.h = s16(d.h);
         if (c.keep_z) e.z = s16(d.zk);
         e.rows = d.rows;
-        { Timed t(c, ST_HOP + std::min(hk, 7)); FG_CHECK(launch_fwd16c(d.fp.view(), d.cw, hp, d.src, e, c.part, T, st), false); }
+        const bool record = hk + 1 < c.hops;
+        if (record) e.fires = bytes(hk + 1);
+        {
+            Timed t(c, ST_HOP + std::min(hk, 7));
+            FG_CHECK(launch_fwd16c(d.fp.view(), d.cw, hp, d.src, e, c.part, T, st, bits(hk)), false);
+            if (record && c.skip_silent) FG_CHECK(launch_fires_pack(bytes(hk + 1), d.rows, bits(hk + 1), T, st), false);
+        }
         hp = s16(d.h);
         ++hk;
     }
@@ -718,6 +731,7 @@ static bool backward16(Core& c, const float* dlogits, int B) {
         BwdEpi16 e;
         e.gdrive = c.gdrive;
         e.n_s = c.n_s;
+        e.skip_silent = c.skip_silent;
         int rows_below;
         float *ggp, *gsp;
         const int* nid_below;

@@ -82,15 +82,26 @@ __device__ __forceinline__ void fwd_finish16(const FwdEpi16& e, int t, int tile,
 #pragma unroll
         for (int k = 0; k < 8; ++k) hv[k] = fmaxf(fmaf(in.g, acc[k], -in.sp), 0.f);
         st8(e.h, e.rows, tile, t, sub, hv);
+        if (e.fires) {                          // whether the row fires on some sample of the tile (a value > 0 that
+            bool any = false;                   // rounds to a bfloat16 zero counts as firing: that only skips less)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) any = any || hv[k] > 0.f;
+            const bool on = !group_silent(any);
+            if (sub == 0) e.fires[(size_t)tile * fires_bytes_ld(e.rows) + t] = on ? 1 : 0;
+        }
     }
 }
 
 // the plug or one hop over its row plan (as k_fwd); split rows leave float32 partials [T][nslot][64]
+// src_fires: the source layer's firing bitmaps (k_fires_pack, fw_ld words per tile; fw_ld 0: none)
 __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ cw, const bf16_t* __restrict__ src,
-                                               int src_rows, FwdEpi16 epi, float* __restrict__ part, int T, int RB) {
+                                               int src_rows, FwdEpi16 epi, float* __restrict__ part, int T, int RB,
+                                               const unsigned* __restrict__ src_fires, int fw_ld) {
     __shared__ __align__(16) int2 slots[WG / LPR][LPR];
+    extern __shared__ __align__(16) unsigned fires[];
     int rb;
     const int tile = tile_of(blockIdx.x, RB, T, rb);
+    const bool bits = stage_fires(src_fires, fw_ld, tile, fires);     // (only for a tile with silent source rows)
     const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
@@ -105,6 +116,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     FwdIn16 in{};
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
+        if (bits) drop_silent(nxt, fires, src_rows);   // a silent source row adds zeros: its gather reads NO_ROW
         int c[8];
         float wt[8];
         stage8(slots[grp], sub, nxt, c, wt);
@@ -203,8 +215,10 @@ __device__ __forceinline__ float dot8(const u32x4& a, const u32x4& b) {
     return d;
 }
 // MODE 1: a hop layer (d: the row's re-drive row); 2: the sensory layer
+// (hr: the row's h line, already loaded by the caller)
 template <int MODE>
-__device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, int tile, int sub, BwdIn16& in) {
+__device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, int tile, int sub, BwdIn16& in,
+                                             const u32x4* hr = nullptr) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) in.z[k] = in.gd[k] = 0.f;
     bool load;                               // (re-drive fields as in BwdEpi)
@@ -216,7 +230,7 @@ __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, in
         load = d >= 0 && !e.first;
     }
     if (load) ldf8(f8p(e.gdrive, e.n_s, tile, in.d, sub), in.gd);
-    in.hr = ldr8(e.h, e.rows, tile, j, sub);
+    in.hr = hr ? *hr : ldr8(e.h, e.rows, tile, j, sub);
     if constexpr (MODE == 2) ld8(e.z, e.rows, tile, j, sub, in.z);
     const float4 r = e.info[j];
     in.gn = r.x;
@@ -313,9 +327,12 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
         (void*)(gz + (size_t)tile * gz_rows * TW16), (short)0, gz_rows * 128, 0x00020000);
     float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
     const bool whole = live && sg.y < 0;
-    u32x4 hj = {0u, 0u, 0u, 0u};                // the row's h, as stored: the weight gradient's operand
+    // the row's h, as stored (the weight gradient's operand), first: where the row fires on no sample of the tile its
+    // g is zero, and its gathers are skipped (as in k_bwd)
+    u32x4 hj = {0u, 0u, 0u, 0u};
+    if (live) hj = ldr8(epi.h, epi.rows, tile, sg.x, sub);
+    const bool quiet = epi.skip_silent && group_silent(bf16_lane_fires(hj));
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    BwdIn16 in{};
     int j = 0, left = wok ? wv.y : 0;
     auto step = [&](auto full) {               // (as in k_cfwd16: full steps, then the wave's last)
         constexpr bool FULL = decltype(full)::value;
@@ -324,17 +341,10 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
         stage8(slots[grp], sub, nxt, c, wt);
         u32x4 raw[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) raw[s] = (FULL || s < left) ? gather16(rs, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
+        for (int s = 0; s < 8; ++s)
+            raw[s] = (FULL || s < left) ? gather16(rs, quiet ? NO_ROW : c[s], sub) : u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (FULL) nxt = q[64 * (j + 1)];
-        if (j == 0) {                           // the row's own inputs, after the first gathers
-            if (whole) {
-                bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in);
-                hj = in.hr;
-            } else if (live) {
-                hj = ldr8(epi.h, epi.rows, tile, sg.x, sub);
-            }
-        }
         __builtin_amdgcn_sched_barrier(0);
         float d[8];
 #pragma unroll
@@ -346,12 +356,13 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
     };
     for (; left > 8; ++j, left -= 8) step(Full<true>{});
     if (left > 0) step(Full<false>{});
-    if (whole && !(wok && wv.y > 0)) bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in);
     if (!live) return;
     if (sg.y >= 0) {
         store8(part + ((size_t)tile * p.nslot + sg.y) * TW16 + sub * 8, acc);
         return;
     }
+    BwdIn16 in{};                               // the row's other inputs, after the loop (k_bwd)
+    bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in, &hj);
     bwd_finish16<MODE>(epi, sg.x, tile, sub, acc, in, nullptr, w * 8 + (grp & 7));
 }
 
@@ -381,9 +392,15 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
         (void*)(gz + (size_t)(hasb ? tb : ta) * gz_rows * TW16), (short)0, hasb ? gz_rows * 128 : 0, 0x00020000);
     float* gwp = gwpart ? gwpart + (size_t)pr * gw_ld + wv.x + lane : nullptr;
     const bool whole = live && sg.y < 0;
+    // the row's h lines first, and on a tile where the row fires on no sample its gathers are skipped (k_cbwd16)
     u32x4 hja = {0u, 0u, 0u, 0u}, hjb = {0u, 0u, 0u, 0u};
+    if (live) {
+        hja = ldr8(epi.h, epi.rows, ta, sg.x, sub);
+        if (hasb) hjb = ldr8(epi.h, epi.rows, tb, sg.x, sub);
+    }
+    const bool quiet_a = epi.skip_silent && group_silent(bf16_lane_fires(hja));
+    const bool quiet_b = epi.skip_silent && group_silent(bf16_lane_fires(hjb));
     float acca[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, accb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    BwdIn16 ina{}, inb{};
     int j = 0, left = wok ? wv.y : 0;
     auto step = [&](auto full) {
         constexpr bool FULL = decltype(full)::value;
@@ -392,24 +409,13 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
         stage8(slots[grp], sub, nxt, c, wt);
         u32x4 va[8], vb[8];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) va[s] = (FULL || s < left) ? gather16(ra, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
+        for (int s = 0; s < 8; ++s)
+            va[s] = (FULL || s < left) ? gather16(ra, quiet_a ? NO_ROW : c[s], sub) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int s = 0; s < 8; ++s) vb[s] = (FULL || s < left) ? gather16(rbs, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
+        for (int s = 0; s < 8; ++s)
+            vb[s] = (FULL || s < left) ? gather16(rbs, quiet_b ? NO_ROW : c[s], sub) : u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (FULL) nxt = q[64 * (j + 1)];
-        if (j == 0) {
-            if (whole) {
-                bwd_inputs16<MODE>(epi, sg.x, sg.z, ta, sub, ina);
-                hja = ina.hr;
-                if (hasb) {
-                    bwd_inputs16<MODE>(epi, sg.x, sg.z, tb, sub, inb);
-                    hjb = inb.hr;
-                }
-            } else if (live) {
-                hja = ldr8(epi.h, epi.rows, ta, sg.x, sub);
-                if (hasb) hjb = ldr8(epi.h, epi.rows, tb, sg.x, sub);
-            }
-        }
         __builtin_amdgcn_sched_barrier(0);
         float d[8];
 #pragma unroll
@@ -424,16 +430,15 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
     };
     for (; left > 8; ++j, left -= 8) step(Full<true>{});
     if (left > 0) step(Full<false>{});
-    if (whole && !(wok && wv.y > 0)) {
-        bwd_inputs16<MODE>(epi, sg.x, sg.z, ta, sub, ina);
-        if (hasb) bwd_inputs16<MODE>(epi, sg.x, sg.z, tb, sub, inb);
-    }
     if (!live) return;
     if (sg.y >= 0) {
         store8(part + ((size_t)ta * p.nslot + sg.y) * TW16 + sub * 8, acca);
         if (hasb) store8(part + ((size_t)tb * p.nslot + sg.y) * TW16 + sub * 8, accb);
         return;
     }
+    BwdIn16 ina{}, inb{};                       // the rows' other inputs, after the loop (k_bwd)
+    bwd_inputs16<MODE>(epi, sg.x, sg.z, ta, sub, ina, &hja);
+    if (hasb) bwd_inputs16<MODE>(epi, sg.x, sg.z, tb, sub, inb, &hjb);
     float2 ka, kb = make_float2(0.f, 0.f);
     bwd_finish16<MODE>(epi, sg.x, ta, sub, acca, ina, &ka);
     if (hasb) bwd_finish16<MODE>(epi, sg.x, tb, sub, accb, inb, &kb);
@@ -523,10 +528,12 @@ hipError_t launch_obs_in16(const float* obs, unsigned short* x, int obs_dim, int
 }
 
 hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* src, int src_rows, const FwdEpi16& epi,
-                         float* part, int T, hipStream_t st) {
+                         float* part, int T, hipStream_t st, const unsigned* src_fires) {
     if (p.nwave > 0) {
         const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
-        k_cfwd16<<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, src_rows, epi, part, T, RB);
+        const int fw = src_fires && fires_ld(src_rows) <= FIRES_LDS_WORDS ? fires_ld(src_rows) : 0;
+        k_cfwd16<<<(unsigned)((long long)T * RB), WG, (size_t)(fw > 0 ? fw - 4 : 0) * 4, st>>>(
+            p, cw, src, src_rows, epi, part, T, RB, src_fires, fw);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

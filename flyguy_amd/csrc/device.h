@@ -5,6 +5,8 @@
 
 namespace fg {
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));     // 8 16-bit states of a lane
+
 __device__ __forceinline__ const float4* at4(const float* base, Lay L, int tile, int row, int sub) {
     return reinterpret_cast<const float4*>(base + (size_t)tile * L.tile + (size_t)row * L.row) + sub;
 }
@@ -111,9 +113,34 @@ struct Slab {
 // Whether the 8-lane group's line of a state is zero on all of its samples (every lane of the wave must call this).  A
 // neuron's output is relu(...) >= 0, so a line of h with no sample > 0 is a neuron that fires on none of the tile's
 // samples: its gradient g = (h > 0 ? gh : 0) is zero there whatever gh is.
-__device__ __forceinline__ bool group_silent(const float4& h) {
-    const unsigned long long fires = __ballot(h.x > 0.f || h.y > 0.f || h.z > 0.f || h.w > 0.f);
+// (lane_fires: whether the lane's own samples hold a value > 0)
+__device__ __forceinline__ bool group_silent(bool lane_fires) {
+    const unsigned long long fires = __ballot(lane_fires);
     return ((fires >> (threadIdx.x & 56)) & 0xFFull) == 0;
+}
+__device__ __forceinline__ bool group_silent(const float4& h) {
+    return group_silent(h.x > 0.f || h.y > 0.f || h.z > 0.f || h.w > 0.f);
+}
+// The 8 stored bfloat16 values of a lane: whether one may be > 0 (any with a nonzero magnitude; a negative value,
+// which a neuron's output never is, counts as firing too, which only turns a skip off)
+__device__ __forceinline__ bool bf16_lane_fires(const u32x4& h) {
+    return ((h[0] | h[1] | h[2] | h[3]) & 0x7FFF7FFFu) != 0u;
+}
+// Stage the firing bitmap of a tile (k_fires_pack) in LDS when the tile has silent rows; every thread of the
+// workgroup calls this.  Returns whether it did (then the hop skips the silent rows' gathers).
+__device__ __forceinline__ bool stage_fires(const unsigned* src_fires, int fw_ld, int tile, unsigned* lds) {
+    if (fw_ld <= 0) return false;
+    const unsigned* b = src_fires + (size_t)tile * fw_ld;
+    if (__builtin_amdgcn_readfirstlane(b[0]) == 0) return false;     // (uniform: one word for the whole workgroup)
+    const uint4* b4 = reinterpret_cast<const uint4*>(b + 4);
+    for (int i = threadIdx.x; i < (fw_ld - 4) / 4; i += WG) reinterpret_cast<uint4*>(lds)[i] = b4[i];
+    __syncthreads();
+    return true;
+}
+// A pair whose source row is silent on the tile (its bit clear, or outside the source layer) gathers NO_ROW instead
+__device__ __forceinline__ void drop_silent(int2& pair, const unsigned* lds, int src_rows) {
+    const unsigned r = (unsigned)pair.x;
+    if (r >= (unsigned)src_rows || !((lds[r >> 5] >> (r & 31)) & 1u)) pair.x = NO_ROW;
 }
 
 // Reduce-scatter over the 8 lanes of a group: lane s ends with the sum over the group's lanes of d[s].  Three

@@ -29,8 +29,6 @@ template <> struct Bits16<BF16> {
     }
 };
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
 // the 8 samples of (row, lane) of a 16-bit tile slab: a 16-byte buffer load, zeros past the slab
 __device__ __forceinline__ u32x4 gather16(__amdgpu_buffer_rsrc_t r, int row, int sub) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (unsigned)row * 128u + (unsigned)sub * 16u, 0, 0));

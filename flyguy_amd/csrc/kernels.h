@@ -170,6 +170,7 @@ struct FwdEpi16 {
     unsigned short* z = nullptr;             // the sensory layer's pre-activation (its drive)
     unsigned short* h = nullptr;
     int rows = 0;                            // rows of z and h
+    unsigned char* fires = nullptr;          // as FwdEpi::fires, per tile of 64 samples
 };
 struct BwdEpi16 {
     int mode = 1;                            // 1: a hop layer; 2: the sensory layer (+ plug)
@@ -181,6 +182,7 @@ struct BwdEpi16 {
     unsigned short* gz_out = nullptr;        // mode 1: the layer's gz, gathered by the next backward
     float* gdrive = nullptr;                 // float32 [T][n_s][64], re-drive fields as in BwdEpi
     bool first = false;                      // as in BwdEpi
+    bool skip_silent = true;                 // as in BwdEpi
     int n_s = 0;
     float *ggain_part = nullptr, *gsum_part = nullptr;
     long long gp_ld = 0;
@@ -194,7 +196,7 @@ struct BwdEpi16 {
 };
 hipError_t launch_obs_in16(const float* obs, unsigned short* x, int obs_dim, int B, hipStream_t st);
 hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* src, int src_rows, const FwdEpi16& epi,
-                         float* part, int T, hipStream_t st);
+                         float* part, int T, hipStream_t st, const unsigned* src_fires = nullptr);
 // gwpart: per-position weight-gradient partials, gw_ld apart, one row per tile; with pair (a hop layer, mode 1) one
 // row per pair of tiles, ceil(T / 2) rows (the sensory layer, mode 2, always takes one tile per workgroup)
 hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,

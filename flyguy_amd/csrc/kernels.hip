@@ -111,17 +111,7 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     extern __shared__ __align__(16) unsigned fires[];     // the source rows' firing bits of this tile
     int rb;
     const int tile = tile_of(blockIdx.x, RB, T, rb);
-    // The bitmap is staged only for a tile on which some source row is silent (its header says how many)
-    bool bits = false;
-    if (fw_ld > 0) {
-        const unsigned* b = src_fires + (size_t)tile * fw_ld;
-        if (__builtin_amdgcn_readfirstlane(b[0]) > 0) {   // (uniform: the whole workgroup reads the same word)
-            const uint4* b4 = reinterpret_cast<const uint4*>(b + 4);
-            for (int i = threadIdx.x; i < (fw_ld - 4) / 4; i += WG) reinterpret_cast<uint4*>(fires)[i] = b4[i];
-            __syncthreads();
-            bits = true;
-        }
-    }
+    const bool bits = stage_fires(src_fires, fw_ld, tile, fires);     // (only for a tile with silent source rows)
     const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
@@ -139,10 +129,7 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     // complete in order, so requested earlier they would hold up the first gathers.  The bias still starts the sum
     // (flyguy_train.cu:75).
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
-        if (bits) {                             // a source row that fires on no sample of the tile adds zeros: skip its
-            const unsigned r = (unsigned)nxt.x; // gather (NO_ROW reads zeros without touching memory)
-            if (r >= (unsigned)src_rows || !((fires[r >> 5] >> (r & 31)) & 1u)) nxt.x = NO_ROW;
-        }
+        if (bits) drop_silent(nxt, fires, src_rows);   // a silent source row adds zeros: its gather reads NO_ROW
         int c[8];
         float wt[8];
         stage8(slots[grp], sub, nxt, c, wt);

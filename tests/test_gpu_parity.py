@@ -165,12 +165,13 @@ def test_gradients_add_up_over_pieces(gpu_lib, full):
         assert rel(a, b) <= 1e-5, name
 
 
-@pytest.mark.parametrize("B", [96, 4096])
-def test_skipping_silent_rows_changes_nothing(gpu_lib, monkeypatch, full, B):
+@pytest.mark.parametrize("B,flags", [(96, 0), (4096, 0), (192, 1), (4096, 1)])
+def test_skipping_silent_rows_changes_nothing(gpu_lib, monkeypatch, full, B, flags):
     """The forward skips the gathers of source rows that fire on no sample of a tile, the backward those of rows whose
     own output is zero on it (FLYGUY_SKIP_SILENT=0 turns both off): logits, every layer's state and all seven
     gradients are bit-identical with and without, on the benchmark network with a third of its neurons silenced
-    (threshold raised) so that whole lines are zero, at B = 96 (a lone last tile of the two-tile backward) and 4096."""
+    (threshold raised) so that whole lines are zero; float32 states at B = 96 (a lone last tile of the two-tile
+    backward) and 4096, bfloat16 states (flags 1, tiles of 64 samples) at B = 192 and 4096."""
     s, params = full
     P = [p.copy() for p in params]
     rng = np.random.default_rng(31)
@@ -180,7 +181,7 @@ def test_skipping_silent_rows_changes_nothing(gpu_lib, monkeypatch, full, B):
     out = {}
     for mode in ("1", "0"):
         monkeypatch.setenv("FLYGUY_SKIP_SILENT", mode)
-        core = Core(s, P, max_batch=B)
+        core = Core(s, P, max_batch=B, flags=flags)
         lg = core.forward(obs)
         states = [core.state(layer, 0, s["sizes"][layer], B) for layer in range(s["hops"] + 1)]
         core.zero_grad()
@@ -188,8 +189,9 @@ def test_skipping_silent_rows_changes_nothing(gpu_lib, monkeypatch, full, B):
         out[mode] = (lg, states, core.get(4))
         del core
     (l1, s1, g1), (l0, s0, g0) = out["1"], out["0"]
-    silent = [float((~(st > 0).reshape(st.shape[0], -1, 32).any(2)).mean()) for st in s1[:-1]]
-    say(f"   B {B}: silent (row, tile) lines per layer {[round(v, 3) for v in silent]}")
+    tile = 64 if flags else 32
+    silent = [float((~(st > 0).reshape(st.shape[0], -1, tile).any(2)).mean()) for st in s1[:-1]]
+    say(f"   B {B} flags {flags}: silent (row, tile) lines per layer {[round(v, 3) for v in silent]}")
     assert max(silent) > 0.2
     assert np.array_equal(l1, l0)
     for a, b in zip(s1, s0):
