@@ -13,8 +13,11 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
   roofline: the dominant kernel's algorithmic bytes per launch / its mean duration (HIP events on the library's
            stream over the timed region), against 8 TB/s;
   cpu_baseline: the reference's own CPU forward (fly_infer.cpp, compiled into oracle/_ref) on a bounded sample of
-           the same network, one core (and, under "all_cores", one handle per thread on up to 16 host cores);
-           train: the oracle's float32 restatement on a small batch.
+           the same network, one core (and, under "all_cores", one handle per thread on up to 16 host cores), and
+           under "torch_cpu" the reference's PyTorch CPU path (FlyActor's sparse products) at batch 1 and 4096;
+           train: one teaching step of that PyTorch path on the CPU at B = 4096.
+  silent_floor (in each roofline): the dominant hop launch re-timed with its source layer silenced, so that every
+           gather is skipped: the kernel's floor without memory traffic, measured in the same run.
   config5: the bfloat16-state core at B = 16384 (forward and teaching step) on the same network and on its
            Erdos-Renyi control;
   trainer: samples / s of the teaching trainer's own loop (flyguy_amd/flyguy_train, run as a child process on
@@ -46,6 +49,8 @@ def algorithmic_bytes(s: dict, B: int, sz: int = 4) -> dict:
     hop_fwd = [N[k] * B * sz + D[k] * B * sz + N[k + 1] * B * sz + E[k] * 8 + (N[k + 1] + 1) * 4 for k in range(K)]
     infer = OD * B * 4 + 2 * N[0] * B * sz + s["fan"] * N[0] * 8 + N[0] * 4 + sum(hop_fwd) \
         + N[K] * B * sz + A * B * 4 + A * N[K] * 4
+    if s["n_w"] < sum(E):        # strengths shared by several hops (the whole connectome): (col, widx) per connection
+        infer += 4 * s["n_w"]    # (counted above as its 8 bytes) and each strength read once
     n_neurons_in_play = len(set(s["n0"].tolist()).union(*[set(h["nid"].tolist()) for h in s["hop"]]))
     n_params = s["n_w"] + 2 * n_neurons_in_play + s["n_s"] * s["fan"] + s["n_s"] + A * N[K] + A
     hop_bwd = []
@@ -58,19 +63,27 @@ def algorithmic_bytes(s: dict, B: int, sz: int = 4) -> dict:
     return {"hop_fwd": hop_fwd, "hop_bwd": hop_bwd, "infer": infer, "train": train, "n_params": n_params}
 
 
-# The vector-memory gather pipe of MI355X, measured (not a published figure): a wave-wide 16-byte-per-lane gather
-# takes about 19.5 CU-cycles per KB, i.e. 256 CUs x 2.4 GHz x 1024 / 19.5 bytes / s, whether the rows hit L2 or not.
-PEAK_GATHER = 256 * 2.4e9 * 1024 / 19.5
+def silent_floor(ms: float, floor_ms: float, E: int, B: int) -> dict:
+    """A hop launch against the same launch with every source row silent, measured in this run: each gather then reads
+    NO_ROW (zeros, no memory access), so that launch takes only the kernel's instruction issue and data return for
+    the same lines (one 128-byte line per connection and 32-sample tile)."""
+    lines = E * (B // 32)
+    return {"ms": round(floor_ms, 4), "frac": round(floor_ms / ms, 4), "lines_per_launch": lines,
+            "gathered_GB_per_s_at_floor": round(lines * 128 / (floor_ms * 1e-3) / 1e9, 1),
+            "note": "the same kernel with the source layer's gains set to 0 (every gather skipped); 1 - frac is the "
+                    "share of the launch spent waiting on the memory system"}
 
 
-def gather_pipe(E: int, B: int, ms: float) -> dict:
-    """The hop kernel against the gather pipe: one 128-byte line per connection and 32-sample tile."""
-    byts = E * (B // 32) * 128
-    ach = byts / (ms * 1e-3)
-    return {"bytes_per_launch": byts, "achieved": round(ach / 1e9, 1), "peak": round(PEAK_GATHER / 1e9, 1),
-            "unit": "GB/s", "frac": round(ach / PEAK_GATHER, 4),
-            "note": "gathered lines (connections x tiles x 128 B) against the measured line rate of the vector-memory "
-                    "pipe; the peak is a probe measurement, not a published figure"}
+def kernel_sources_sha() -> str:
+    """SHA-256 over the library's kernel sources: a counter run recorded for other sources is stale."""
+    import hashlib
+    h = hashlib.sha256()
+    d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "flyguy_amd", "csrc")
+    for n in sorted(os.listdir(d)):
+        if n.endswith((".hip", ".h")):
+            with open(os.path.join(d, n), "rb") as fh:
+                h.update(n.encode() + b"\0" + fh.read())
+    return h.hexdigest()
 
 
 def host_info() -> dict:
@@ -162,24 +175,60 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
         fwd["host"] = host_info()
     train = None
     if train_batch > 0:
-        from flyguy_amd.export import net_bytes
-        from oracle.oracle import Oracle
-        o = Oracle(net_bytes(s), params, "f32")
-        obs = rng.standard_normal((train_batch, s["obs_dim"])).astype(np.float32)
-        tl = (rng.standard_normal((train_batch, s["n_act"])) * 2).astype(np.float32)
-        t0 = time.perf_counter()
-        lg = o.forward(obs)
-        dl, _, _ = o.loss(lg, tl)
-        grads = o.backward(dl)
-        for p, g in zip(params, grads):
-            z = np.zeros_like(g)
-            pp, e = p.astype(np.float32).copy(), p.astype(np.float32).copy()
-            o.adam(pp, g, z, z.copy(), e, 1e-4, 1, 1.0, 0.999)
-        dt = time.perf_counter() - t0
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-        train = {"value": train_batch / dt, "unit": "samples/s", "cores": threads, "kind": "port",
-                 "sample": f"one teaching step (forward, KL, backward, Adam) on {train_batch} samples through the "
-                           f"oracle's float32 restatement, {dt:.1f} s"}
+        torch_fwd, train = torch_cpu_baselines(s, params, train_batch)
+        if fwd is not None:
+            fwd["torch_cpu"] = torch_fwd
+    return fwd, train
+
+
+def torch_cpu_baselines(s, params, batch: int) -> tuple[dict, dict]:
+    """The reference's PyTorch CPU path (fly.py:252-305, this package's FlyActor over the same network): batch-1
+    decisions (median of 30) and a batch forward through sparse CSR products of the current weights (the CPU
+    decision library switched off, as FLYGUY_NATIVE=0 does), and one teaching step (forward, KL, backward through
+    the sparse products' own backward, Adam over three rate groups) on `batch` samples, on torch's CPU threads."""
+    import numpy as np
+    import torch
+    from flyguy_amd.fly import FlyActor
+    rng = np.random.default_rng(2)
+    f = FlyActor.from_structure(s, params)
+    threads = torch.get_num_threads()
+    old = os.environ.get("FLYGUY_NATIVE")
+    os.environ["FLYGUY_NATIVE"] = "0"
+    try:
+        x = torch.as_tensor(rng.standard_normal((batch, s["obs_dim"])).astype(np.float32))
+        with torch.no_grad():
+            f(x[:1])
+            lat = []
+            for i in range(30):
+                t0 = time.perf_counter()
+                f(x[i:i + 1])
+                lat.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            f(x)
+            dt_f = time.perf_counter() - t0
+    finally:
+        if old is None:
+            os.environ.pop("FLYGUY_NATIVE")
+        else:
+            os.environ["FLYGUY_NATIVE"] = old
+    fwd = {"batch1_median_ms": round(1e3 * float(np.median(lat)), 3), "value": round(batch / dt_f, 1),
+           "unit": "decisions/s", "cores": threads, "kind": "port",
+           "sample": f"30 batch-1 decisions and one batch of {batch} through FlyActor's sparse CSR products "
+                     f"(fly.py:252-284), {dt_f:.1f} s for the batch"}
+    tl = torch.as_tensor((rng.standard_normal((batch, s["n_act"])) * 2).astype(np.float32))
+    others = [p for n, p in f.named_parameters() if n not in ("w", "gain", "theta")]
+    opt = torch.optim.Adam([{"params": [f.w], "lr": 1e-4}, {"params": [f.gain, f.theta], "lr": 3e-5},
+                            {"params": others, "lr": 1e-4}])
+    t0 = time.perf_counter()
+    lt = torch.log_softmax(tl, -1)
+    loss = (lt.exp() * (lt - torch.log_softmax(f(x), -1))).sum(-1).mean()
+    opt.zero_grad()
+    loss.backward()
+    opt.step()
+    dt = time.perf_counter() - t0
+    train = {"value": round(batch / dt, 1), "unit": "samples/s", "cores": threads, "kind": "port",
+             "sample": f"one teaching step (forward, KL, backward, Adam) on {batch} samples through FlyActor's "
+                       f"PyTorch path on the CPU (sparse products with their own backward, fly.py:51-72), {dt:.1f} s"}
     return fwd, train
 
 
@@ -310,6 +359,7 @@ def config4_leg(steps: int, warmup: int, B: int = 1024) -> dict:
     logits = torch.empty(B, s["n_act"], device=dev)
     stats = torch.zeros(2, device=dev)
     res = {"hop_connections": [len(h["col"]) for h in s["hop"]], "strengths": s["n_w"], "batch": B}
+    ab = algorithmic_bytes(s, B)                # (of the pruned hops the library runs: the masked-out work is not done)
     for what, fn in (("forward", lambda: call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)),
                      ("train", lambda: call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4,
                                             3e-5, 1e-4, 0.0, 0.999, stats.data_ptr()))):
@@ -321,8 +371,10 @@ def config4_leg(steps: int, warmup: int, B: int = 1024) -> dict:
             fn()
         torch.cuda.synchronize()
         t = (time.perf_counter() - t0) / steps
+        byts = ab["infer" if what == "forward" else "train"]
         res[what] = {"value": round(B / t, 1), "unit": "decisions/s" if what == "forward" else "samples/s",
-                     "ms_per_step": round(1e3 * t, 4)}
+                     "ms_per_step": round(1e3 * t, 4), "algorithmic_bytes": byts,
+                     "whole_batch_frac": round(byts / t / PEAK_HBM, 4)}
     print(f"# whole connectome B={B}: forward {res['forward']['ms_per_step']:.3f} ms, train "
           f"{res['train']['ms_per_step']:.3f} ms", file=sys.stderr, flush=True)
     lib().fc_free(core)
@@ -342,6 +394,9 @@ def main() -> int:
     ap.add_argument("--config5-steps", type=int, default=10, help="timed bfloat16 B=16384 batches and steps (0: skip)")
     ap.add_argument("--config4-steps", type=int, default=10,
                     help="timed whole-connectome B=1024 batches and steps (0: skip; its index build takes ~20 s)")
+    ap.add_argument("--no-floor", action="store_true",
+                    help="skip the silent-source re-timing of the dominant hops (a counter run then sees only the "
+                         "benchmark's own launches)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run 3 copies of 1 GiB (read 1 GiB, write 1 GiB each) so a counter run can scale "
                          "FETCH_SIZE / WRITE_SIZE by what they read for a copy of known size")
@@ -437,11 +492,42 @@ def main() -> int:
     dom_b = max(bwd_hops, key=bwd_hops.get)
     kb = int(dom_b[3]) - 1
     ach_b = ab["hop_bwd"][kb] / (bwd_hops[dom_b] * 1e-3)
-    traffic = None
+    traffic, traffic_note = None, "no counter run recorded"
     tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_synth3hop_b4096.json")
     if os.path.exists(tfile):
         with open(tfile) as fh:
-            traffic = json.load(fh).get("k_fwd " + dom_f)
+            tj = json.load(fh)
+        if tj.get("sources_sha256") == kernel_sources_sha():
+            traffic, traffic_note = tj.get("k_fwd " + dom_f), tj.get("command", "")
+        else:
+            traffic_note = "the counter run predates the current kernel sources (profiles/traffic_synth3hop_b4096.json)"
+
+    # the dominant hops' floors: the same launches with their source layer silenced (gains 0, so every gather is
+    # skipped), forward and teaching step (rate 0: the weights stay as they are), then the weights restored
+    def layer_neurons(layer):
+        return np.asarray(s["n0"] if layer == 0 else s["hop"][layer - 1]["nid"], np.int64)
+    floor_f = floor_b = None
+    if not args.no_floor:
+        quiet = params[1].copy()
+        for layer in {kf, kb}:
+            quiet[layer_neurons(layer)] = 0.0
+        gq = torch.as_tensor(quiet).to(dev)
+        call("fc_copy", core, 0, 1, (ctypes.c_void_p * 7)(None, gq.data_ptr(), None, None, None, None, None))
+        for _ in range(W):
+            fwd()
+        _, prof_qf = timed(fwd)
+
+        def teach_still():
+            call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 0.0, 0.0, 0.0, 0.0, 0.999,
+                 stats.data_ptr())
+        for _ in range(W):
+            teach_still()
+        _, prof_qt = timed(teach_still)
+        call("fc_copy", core, 0, 1, ptrs)
+        floor_f = silent_floor(fwd_hops[dom_f], stage_ms(prof_qf, dom_f), len(s["hop"][kf]["col"]), B)
+        floor_b = silent_floor(bwd_hops[dom_b], stage_ms(prof_qt, dom_b), len(s["hop"][kb]["col"]), B)
+        print(f"# floors: {dom_f} {floor_f['ms']:.3f} of {fwd_hops[dom_f]:.3f} ms, {dom_b} {floor_b['ms']:.3f} of "
+              f"{bwd_hops[dom_b]:.3f} ms", file=sys.stderr, flush=True)
 
     cpu_f = cpu_t = None
     if not args.no_cpu:
@@ -476,10 +562,11 @@ def main() -> int:
                    "redrive_rows": [int((h["drow"] >= 0).sum()) for h in s["hop"]]},
         "roofline": {"bound": "hbm", "kernel": "k_fwd " + dom_f, "achieved": round(ach_f / 1e9, 1), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(ach_f / PEAK_HBM, 4), "traffic": traffic,
+                     "traffic_source": traffic_note,
                      "algorithmic_bytes_per_launch": ab["hop_fwd"][kf], "mean_launch_ms": round(fwd_hops[dom_f], 4),
                      "whole_batch_frac": round(ab["infer"] / (t_fwd / K) / PEAK_HBM, 4),
                      "whole_batch_algorithmic_bytes": ab["infer"],
-                     "gather_pipe": gather_pipe(len(s["hop"][kf]["col"]), B, fwd_hops[dom_f])},
+                     "silent_floor": floor_f},
         "cpu_baseline": cpu_f,
         "train": {"value": round(sps, 1), "unit": "samples/s", "ms_per_step": round(ms_train, 4),
                   "workload": "fp32 teaching step: forward, KL(teacher||student) over 90 actions, fused backward, "
@@ -492,7 +579,7 @@ def main() -> int:
                                "mean_launch_ms": round(bwd_hops[dom_b], 4),
                                "whole_step_frac": round(ab["train"] / (t_train / K) / PEAK_HBM, 4),
                                "whole_step_algorithmic_bytes": ab["train"],
-                               "gather_pipe": gather_pipe(len(s["hop"][kb]["col"]), B, bwd_hops[dom_b])},
+                               "silent_floor": floor_b},
                   "cpu_baseline": cpu_t},
         "trainer": trainer,
         "config5": config5,

@@ -164,6 +164,66 @@ class FlyActor(nn.Module):
         nn.init.orthogonal_(self.out.weight, out_gain)
         nn.init.zeros_(self.out.bias)
 
+    @classmethod
+    def from_structure(cls, s: dict, params: list | None = None) -> "FlyActor":
+        """An actor over a network given as a library structure (flyguy_amd.export.structure / read_net: NET.bin's
+        arrays) instead of a graph file, with the seven weight arrays in the library's order (params, or zeros).
+        Its strengths are the network's strengths in play (w[i] is NET.bin's strength i, so e{k} = widx); buffers,
+        parameters and every forward path are FlyActor's."""
+        f = cls.__new__(cls)
+        nn.Module.__init__(f)
+        K = int(s["hops"])
+        f.n_neurons, f.n_conn, f.hops = int(s["n_neurons"]), int(s["n_w"]), K
+        f.obs_dim, f.fan = int(s["obs_dim"]), int(s["fan"])
+        f.whole_graph, f.gather_limit, f.kernel = True, 60_000_000, "torch"
+        f.sizes = [int(v) for v in s["sizes"]]
+
+        def keep(name, arr, dtype=np.int64):
+            f.register_buffer(name, torch.as_tensor(np.ascontiguousarray(arr, dtype=dtype)), persistent=False)
+
+        f.used = 0
+        for k in range(1, K + 1):
+            h = s["hop"][k - 1]
+            crow, col, widx = (np.asarray(h[x], np.int64) for x in ("crow", "col", "widx"))
+            tcrow, tcol, twidx = (np.asarray(h[x], np.int64) for x in ("tcrow", "tcol", "twidx"))
+            edge_of = np.full(f.n_conn, -1, np.int64)
+            edge_of[widx] = np.arange(len(widx))
+            drow = np.asarray(h["drow"], np.int64)
+            keep(f"e{k}", widx)
+            keep(f"r{k}", np.repeat(np.arange(len(crow) - 1), np.diff(crow)))
+            keep(f"c{k}", col)
+            keep(f"crow{k}", crow)
+            keep(f"tcrow{k}", tcrow)
+            keep(f"tcol{k}", tcol)
+            keep(f"tperm{k}", edge_of[twidx])
+            keep(f"ci{k}", col, np.int32)
+            keep(f"tci{k}", tcol, np.int32)
+            keep(f"n{k}", h["nid"])
+            keep(f"s{k}", np.flatnonzero(drow >= 0))
+            keep(f"d{k}", drow[drow >= 0])
+            f.used += len(col)
+        f.in_play = f.n_conn
+        keep("n0", s["n0"])
+        keep("dn_rows", s["dn_rows"])
+        in_crow, in_col = np.asarray(s["in_crow"], np.int64), np.asarray(s["in_col"], np.int64)
+        keep("in_r", np.repeat(np.arange(len(in_crow) - 1), np.diff(in_crow)))
+        keep("in_c", in_col)
+        keep("in_crow", in_crow)
+        keep("in_tcrow", s["in_tcrow"])
+        keep("in_tcol", s["in_tcol"])
+        keep("in_tperm", s["in_tperm"])
+        keep("in_ci", in_col, np.int32)
+        keep("in_tci", s["in_tcol"], np.int32)
+        P = params if params is not None else [np.zeros(n, np.float32) for n in (
+            f.n_conn, f.n_neurons, f.n_neurons, len(in_col), f.sizes[0], int(s["n_act"]) * int(s["n_dn"]), int(s["n_act"]))]
+        as_param = lambda a: nn.Parameter(torch.as_tensor(np.array(a, np.float32)))   # noqa: E731
+        f.w, f.gain, f.theta, f.in_w, f.in_b = (as_param(a) for a in P[:5])
+        f.out = nn.Linear(int(s["n_dn"]), int(s["n_act"]))
+        with torch.no_grad():
+            f.out.weight.copy_(torch.as_tensor(np.asarray(P[5], np.float32)).view(int(s["n_act"]), int(s["n_dn"])))
+            f.out.bias.copy_(torch.as_tensor(np.asarray(P[6], np.float32)))
+        return f
+
     def describe(self) -> str:
         plug = self.in_w.numel() + self.in_b.numel() + sum(p.numel() for p in self.out.parameters())
         return (f"fly actor: {self.n_neurons:,} neurons and {self.n_conn:,} connections in the graph; {self.hops} hops: "
