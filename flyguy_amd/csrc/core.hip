@@ -8,7 +8,7 @@
 //              current weights at each pass), and the row plans (forward: CSR rows; backward: CSC rows);
 //   states: x, drive, h0, gdrive, h_k per hop, two gz buffers, logits / dlogits (a hop layer's pre-activation z is
 //           not kept: the backward needs it only where h > 0, and there it is (h + softplus(theta)) / gain);
-//   partial sums: split rows, per-edge weight gradients [T][E_k], per-row gain / threshold gradients [T][rows],
+//   partial sums: split rows, per-edge weight gradients [T or T/2][E_k], per-row gain / threshold gradients [T][rows],
 //                 plug gradients [T][n_s] / [T][E_in], read-out gradients [chunks][n_act * n_dn].
 #include <algorithm>
 #include <cmath>
@@ -394,8 +394,15 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     c->pm = dalloc<float>(*c, (size_t)(5 * o));
     if (!c->pm) return nullptr;
 
-    // states (float32 or bfloat16, max_batch samples per row) and partial sums
-    const size_t Tm = c->Tm, S = TW;
+    // states (float32 or bfloat16, max_batch samples per row) and partial sums.  Per-tile partials take one row per
+    // tile of the handle's own width (32 samples, or 64 with bfloat16 states); the weight-gradient partials one row
+    // per tile, or per pair of tiles when every hop's backward takes two (the bfloat16 sensory layer takes one).
+    const size_t Tm = c->Tm, S = TW, Tp = (size_t)bm / tq;
+    size_t gw_rows = 0;
+    for (int k = 1; k <= K; ++k) {
+        const bool pair = c->hop[k - 1].pair_bwd && (prec == 0 || k >= 2);
+        gw_rows = std::max(gw_rows, pair ? (Tp + 1) / 2 : Tp);
+    }
     auto state = [&](long long rows) -> float* {
         return prec ? reinterpret_cast<float*>(dalloc<unsigned short>(*c, (size_t)bm * rows))
                     : dalloc<float>(*c, (size_t)bm * rows);
@@ -410,8 +417,8 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         d.h = state(d.rows);
         // (its partials' columns: the plan of the hop above, or the rows themselves for the top layer's read-out)
         const size_t gc = &d != &c->hop.back() ? (size_t)std::max(d.rows, (&d + 1)->gcols) : (size_t)d.rows;
-        d.ggp = dalloc<float>(*c, Tm * gc);
-        d.gsp = dalloc<float>(*c, Tm * gc);
+        d.ggp = dalloc<float>(*c, Tp * gc);
+        d.gsp = dalloc<float>(*c, Tp * gc);
         d.info = dalloc<float4>(*c, d.rows);
         if (!d.h || !d.ggp || !d.gsp || !d.info) return nullptr;
     }
@@ -419,18 +426,18 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     if (!c->info0) return nullptr;
     if (const char* f = std::getenv("FLYGUY_SKIP_SILENT")) c->skip_silent = f[0] != '0';
     for (int l = 0; l < K; ++l) {                   // (the top layer's would have no reader)
-        c->fire_bytes.push_back(dalloc<unsigned char>(*c, Tm * (size_t)fires_bytes_ld(c->sizes[l])));
-        c->fire_bits.push_back(dalloc<unsigned>(*c, Tm * (size_t)fires_ld(c->sizes[l])));
+        c->fire_bytes.push_back(dalloc<unsigned char>(*c, Tp * (size_t)fires_bytes_ld(c->sizes[l])));
+        c->fire_bits.push_back(dalloc<unsigned>(*c, Tp * (size_t)fires_ld(c->sizes[l])));
         if (!c->fire_bytes.back() || !c->fire_bits.back()) return nullptr;
     }
     c->lg = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->dl = dalloc<float>(*c, (size_t)bm * c->n_act);
     c->part = dalloc<float>(*c, Tm * std::max<long long>(max_slot, 1) * S);
-    c->gwpart = dalloc<float>(*c, Tm * max_pos);
-    c->ggp0 = dalloc<float>(*c, Tm * (size_t)std::max(c->n_s, c->hop[0].gcols));
-    c->gsp0 = dalloc<float>(*c, Tm * (size_t)std::max(c->n_s, c->hop[0].gcols));
-    c->ginb = dalloc<float>(*c, Tm * c->n_s);
-    c->ginw = dalloc<float>(*c, Tm * c->E_in);
+    c->gwpart = dalloc<float>(*c, gw_rows * max_pos);
+    c->ggp0 = dalloc<float>(*c, Tp * (size_t)std::max(c->n_s, c->hop[0].gcols));
+    c->gsp0 = dalloc<float>(*c, Tp * (size_t)std::max(c->n_s, c->hop[0].gcols));
+    c->ginb = dalloc<float>(*c, Tp * c->n_s);
+    c->ginw = dalloc<float>(*c, Tp * c->E_in);
     c->gow_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act * c->n_dn);
     c->gob_p = dalloc<float>(*c, (size_t)readout_chunks(bm) * c->n_act);
     c->stats_part = dalloc<float>(*c, (size_t)2 * ((bm + 31) / 32));     // one pair per 32 samples (k_loss)

@@ -96,16 +96,22 @@ def test_exact_forward_backward(gpu_lib, name, hops, fan):
 
 
 @pytest.mark.parametrize("tiles", ["1", "2"])
-def test_exact_one_and_two_tile_backward(gpu_lib, monkeypatch, tiles):
+@pytest.mark.parametrize("hops", [3, 4])
+def test_exact_one_and_two_tile_backward(gpu_lib, monkeypatch, tiles, hops):
     """Both hop backward kernels (one tile per workgroup, two: chosen per layer from how unevenly the gathered rows
-    are used, forced here), bit-exact at B = 192: three tiles, so the two-tile kernel also meets a lone last tile."""
+    are used, forced here), bit-exact at B = 192: three tiles, so the two-tile kernel also meets a lone last tile.
+    With 4 hops, a source row of hop 2 sends 18 connections, more than the backward plan's segment cap (16 for a
+    product this small): its row is split, so the split-row combine runs in its paired form on a hop layer."""
     monkeypatch.setenv("FLYGUY_BWD_TILES", tiles)
-    s, P, obs = _exact_case("b", 3, 8, 4)
+    s, P, obs = _exact_case("b", hops, 8, 4)
+    if hops == 4:
+        out = np.bincount(np.asarray(s["hop"][1]["col"]), minlength=s["sizes"][1])
+        assert out.max() > 16
     rng = np.random.default_rng(50)
     for i in (0, 3):                                            # denser strengths and plug weights: most gradients move
         P[i] = (rng.choice([-1.0, 1.0, 1.0], P[i].size) * (rng.random(P[i].size) < 0.5)).astype(np.float32)
     obs = np.concatenate([obs, -obs[::-1], np.roll(obs, 7, axis=1)])
-    say(f"bf16 exact b hops 3 fan 8, B 192, {tiles} tile(s) per backward workgroup")
+    say(f"bf16 exact b hops {hops} fan 8, B 192, {tiles} tile(s) per backward workgroup")
     o = Core16(s, P)
     want = o.forward(obs)
     for layer, (h, _) in enumerate(o.states):
