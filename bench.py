@@ -10,8 +10,9 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
   value  : decisions / s of the batched forward (fc_forward: plug, 3 hops, read-out), K timed batches;
   train  : samples / s of the full teaching step (fc_teach_step: forward, KL loss, backward, Adam + running
            average), K timed steps;
-  roofline: the dominant kernel's algorithmic bytes per launch / its mean duration (HIP events on the library's
-           stream over the timed region), against 8 TB/s;
+  roofline: the dominant kernel's algorithmic bytes per launch / its mean duration (HIP events around that kernel
+           alone, on the library's stream over the timed region), against 8 TB/s; the dominant kernel and the
+           per-stage times (stages_ms) come from a few calls profiled stage by stage before the timed region;
   cpu_baseline: the reference's own CPU forward (fly_infer.cpp, compiled into oracle/_ref) on a bounded sample of
            the same network, one core (and, under "all_cores", one handle per thread on up to 16 host cores), and
            under "torch_cpu" the reference's PyTorch CPU path (FlyActor's sparse products) at batch 1 and 4096;
@@ -306,16 +307,18 @@ def config5_leg(steps: int, warmup: int, B: int = 16384) -> dict:
                                                 3e-5, 1e-4, 0.0, 0.999, stats.data_ptr()))):
             for _ in range(warmup):
                 fn()
-            torch.cuda.synchronize()
-            call("fc_profile", core, 1)
+            call("fc_profile", core, 1)             # per-stage times from a few calls outside the timed region
             profile_read(core, reset=True)
+            for _ in range(min(steps, 3)):
+                fn()
+            torch.cuda.synchronize()
+            prof = profile_read(core, reset=True)
+            call("fc_profile", core, 0)
             t0 = time.perf_counter()
             for _ in range(steps):
                 fn()
             torch.cuda.synchronize()
             t = (time.perf_counter() - t0) / steps
-            prof = profile_read(core, reset=True)
-            call("fc_profile", core, 0)
             byts = ab["infer" if what == "forward" else "train"]
             res[what] = {"value": round(B / t, 1), "unit": "decisions/s" if what == "forward" else "samples/s",
                          "ms_per_step": round(1e3 * t, 4), "whole_batch_frac": round(byts / t / PEAK_HBM, 4),
@@ -410,7 +413,7 @@ def main() -> int:
 
     import numpy as np
     import torch
-    from flyguy_amd._lib import bwd_pairs, call, lib, profile_read
+    from flyguy_amd._lib import STAGES, bwd_pairs, call, lib, profile_read
     from flyguy_amd.export import net_bytes
     from flyguy_amd.synth import synth_3hop
 
@@ -439,9 +442,28 @@ def main() -> int:
     print(f"# set-up {time.perf_counter() - t_setup:.1f} s", file=sys.stderr, flush=True)
     ab = algorithmic_bytes(s, B)
 
-    def timed(fn):
-        """K calls bracketed by synchronisations, with per-stage HIP events on the library's stream (fc_profile)"""
+    stage_of = {name: i for i, name in STAGES.items()}
+
+    def stage_ms(prof, name):
+        tot, n = prof.get(name, (0.0, 0))
+        return tot / n if n else float("nan")
+
+    def profiled(fn, n=5):
+        """n calls with every stage bracketed by HIP events (fc_profile 1): the per-stage times, which pick the
+        dominant kernel; outside the timed region, since ~30 events per call lengthen it by about 3%"""
         call("fc_profile", core, 1)
+        profile_read(core, reset=True)
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        prof = profile_read(core, reset=True)
+        call("fc_profile", core, 0)
+        return prof
+
+    def timed(fn, stage):
+        """K calls bracketed by synchronisations; only `stage` is bracketed by HIP events on the library's stream
+        (fc_profile 2 + stage), so its mean launch duration comes from the timed region itself"""
+        call("fc_profile", core, 2 + stage_of[stage])
         profile_read(core, reset=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -451,7 +473,11 @@ def main() -> int:
         t = time.perf_counter() - t0
         prof = profile_read(core, reset=True)
         call("fc_profile", core, 0)
-        return t, prof
+        return t, stage_ms(prof, stage)
+
+    def dominant(prof, kind):
+        hops = {f"hop{k + 1} {kind}": stage_ms(prof, f"hop{k + 1} {kind}") for k in range(s["hops"])}
+        return max(hops, key=hops.get)
 
     # ---- batched forward
     def fwd():
@@ -459,7 +485,9 @@ def main() -> int:
     for _ in range(W):
         fwd()
     torch.cuda.synchronize()
-    t_fwd, prof_fwd = timed(fwd)
+    prof_fwd = profiled(fwd)
+    dom_f = dominant(prof_fwd, "fwd")
+    t_fwd, dom_f_ms = timed(fwd, dom_f)
     assert torch.isfinite(logits).all()
     ms_fwd = 1e3 * t_fwd / K
     dps = B * K / t_fwd
@@ -471,7 +499,9 @@ def main() -> int:
     for _ in range(W):
         teach()
     torch.cuda.synchronize()
-    t_train, prof_train = timed(teach)
+    prof_train = profiled(teach)
+    dom_b = dominant(prof_train, "bwd")
+    t_train, dom_b_ms = timed(teach, dom_b)
     assert np.isfinite(float(stats[0]))
     kl = float(stats[0]) / B
     ms_train = 1e3 * t_train / K
@@ -479,19 +509,11 @@ def main() -> int:
     print(f"# train: {ms_train:.3f} ms / step of {B}, {sps:,.0f} samples/s, kl {kl:.4f}",
           file=sys.stderr, flush=True)
 
-    def stage_ms(prof, name):
-        tot, n = prof.get(name, (0.0, 0))
-        return tot / n if n else float("nan")
-
-    # dominant kernels: the largest hop of the forward, the largest hop backward of the step
-    fwd_hops = {f"hop{k + 1} fwd": stage_ms(prof_fwd, f"hop{k + 1} fwd") for k in range(s["hops"])}
-    dom_f = max(fwd_hops, key=fwd_hops.get)
+    # dominant kernels: the largest hop of the forward, the largest hop backward of the step, timed in the timed region
     kf = int(dom_f[3]) - 1
-    ach_f = ab["hop_fwd"][kf] / (fwd_hops[dom_f] * 1e-3)
-    bwd_hops = {f"hop{k + 1} bwd": stage_ms(prof_train, f"hop{k + 1} bwd") for k in range(s["hops"])}
-    dom_b = max(bwd_hops, key=bwd_hops.get)
+    ach_f = ab["hop_fwd"][kf] / (dom_f_ms * 1e-3)
     kb = int(dom_b[3]) - 1
-    ach_b = ab["hop_bwd"][kb] / (bwd_hops[dom_b] * 1e-3)
+    ach_b = ab["hop_bwd"][kb] / (dom_b_ms * 1e-3)
     traffic, traffic_note = None, "no counter run recorded"
     tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_synth3hop_b4096.json")
     if os.path.exists(tfile):
@@ -515,19 +537,19 @@ def main() -> int:
         call("fc_copy", core, 0, 1, (ctypes.c_void_p * 7)(None, gq.data_ptr(), None, None, None, None, None))
         for _ in range(W):
             fwd()
-        _, prof_qf = timed(fwd)
+        _, quiet_f_ms = timed(fwd, dom_f)
 
         def teach_still():
             call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 0.0, 0.0, 0.0, 0.0, 0.999,
                  stats.data_ptr())
         for _ in range(W):
             teach_still()
-        _, prof_qt = timed(teach_still)
+        _, quiet_b_ms = timed(teach_still, dom_b)
         call("fc_copy", core, 0, 1, ptrs)
-        floor_f = silent_floor(fwd_hops[dom_f], stage_ms(prof_qf, dom_f), len(s["hop"][kf]["col"]), B)
-        floor_b = silent_floor(bwd_hops[dom_b], stage_ms(prof_qt, dom_b), len(s["hop"][kb]["col"]), B)
-        print(f"# floors: {dom_f} {floor_f['ms']:.3f} of {fwd_hops[dom_f]:.3f} ms, {dom_b} {floor_b['ms']:.3f} of "
-              f"{bwd_hops[dom_b]:.3f} ms", file=sys.stderr, flush=True)
+        floor_f = silent_floor(dom_f_ms, quiet_f_ms, len(s["hop"][kf]["col"]), B)
+        floor_b = silent_floor(dom_b_ms, quiet_b_ms, len(s["hop"][kb]["col"]), B)
+        print(f"# floors: {dom_f} {floor_f['ms']:.3f} of {dom_f_ms:.3f} ms, {dom_b} {floor_b['ms']:.3f} of "
+              f"{dom_b_ms:.3f} ms", file=sys.stderr, flush=True)
 
     cpu_f = cpu_t = None
     if not args.no_cpu:
@@ -563,7 +585,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "k_fwd " + dom_f, "achieved": round(ach_f / 1e9, 1), "peak": 8000.0,
                      "unit": "GB/s", "frac": round(ach_f / PEAK_HBM, 4), "traffic": traffic,
                      "traffic_source": traffic_note,
-                     "algorithmic_bytes_per_launch": ab["hop_fwd"][kf], "mean_launch_ms": round(fwd_hops[dom_f], 4),
+                     "algorithmic_bytes_per_launch": ab["hop_fwd"][kf], "mean_launch_ms": round(dom_f_ms, 4),
                      "whole_batch_frac": round(ab["infer"] / (t_fwd / K) / PEAK_HBM, 4),
                      "whole_batch_algorithmic_bytes": ab["infer"],
                      "silent_floor": floor_f},
@@ -576,7 +598,7 @@ def main() -> int:
                                                          + dom_b, "achieved": round(ach_b / 1e9, 1),
                                "peak": 8000.0, "unit": "GB/s", "frac": round(ach_b / PEAK_HBM, 4),
                                "algorithmic_bytes_per_launch": ab["hop_bwd"][kb],
-                               "mean_launch_ms": round(bwd_hops[dom_b], 4),
+                               "mean_launch_ms": round(dom_b_ms, 4),
                                "whole_step_frac": round(ab["train"] / (t_train / K) / PEAK_HBM, 4),
                                "whole_step_algorithmic_bytes": ab["train"],
                                "silent_floor": floor_b},

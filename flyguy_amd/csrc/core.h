@@ -45,6 +45,7 @@ enum Stage {
 
 struct Prof {
     bool on = false;
+    int only = -1;                                   // >= 0: only this stage is timed
     std::vector<std::pair<hipEvent_t, int>> rec;   // (event, stage*2 + 0 start / 1 end) in recording order
     std::vector<hipEvent_t> pool;
     double ms[ST_COUNT] = {0};
@@ -105,7 +106,7 @@ struct Timed {
     Timed(Core& c_, int s) : c(c_), stage(s) { mark(0); }
     ~Timed() { mark(1); }
     void mark(int end) {
-        if (!c.prof.on) return;
+        if (!c.prof.on || (c.prof.only >= 0 && c.prof.only != stage)) return;
         hipEvent_t e = c.prof.get();
         if (e && hipEventRecord(e, c.st) == hipSuccess) c.prof.rec.push_back({e, stage * 2 + end});
     }

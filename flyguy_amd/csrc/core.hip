@@ -961,8 +961,10 @@ void fc_export_state(void* h, int layer, int what, float* dst, int B) {
 void fc_profile(void* h, int on) {
     Core* c = (Core*)h;
     if (!c) { set_error("null handle"); return; }
-    if (!on && c->prof.on) prof_collect(*c);
+    if (on < 0 || on >= 2 + ST_COUNT) { set_error("fc_profile: on must be 0, 1 or 2 + a stage"); return; }
+    if (c->prof.on) prof_collect(*c);            // (events recorded so far count under the old setting)
     c->prof.on = on != 0;
+    c->prof.only = on >= 2 ? on - 2 : -1;
 }
 
 int fc_profile_read(void* h, double* ms, long long* counts, int n, int reset) {

@@ -102,7 +102,8 @@ float fc_teach_step(void* core, const float* obs, const float* teacher, int B, f
  * 2: the observation batch x [obs_dim][B] (layer ignored).  For tests and diagnostics. */
 void fc_export_state(void* core, int layer, int what, float* dst, int B);
 
-/* Profiling: with on = 1 every stage of the library's work is bracketed by HIP events on its stream.
+/* Profiling: with on = 1 every stage of the library's work is bracketed by HIP events on its stream; with
+ * on = 2 + s only stage s is (two events per run of it, so timing the whole call is not disturbed); 0 stops.
  * fc_profile_read waits for the recorded events and writes, per stage, the summed milliseconds and the number of
  * timed runs (reset != 0 clears the totals); returns the number of stages (25) or -1.  Stages: 0 observation
  * transpose, 1 (index, weight) packing, 2 plug + sensory layer, 3+k forward of hop k+1, 11 read-out, 12 loss,
