@@ -493,6 +493,20 @@ def main() -> int:
     dps = B * K / t_fwd
     print(f"# forward: {ms_fwd:.3f} ms / batch of {B}, {dps:,.0f} decisions/s", file=sys.stderr, flush=True)
 
+    # ---- one decision on the GPU: batch 1 padded to one 32-sample tile (NativeFlyActor's rule), each call
+    # synchronised, as a bot deciding one car at a time would run it
+    lat = []
+    for _ in range(200):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        call("fc_forward", core, obs.data_ptr(), 32, logits.data_ptr(), 0)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t0)
+    lat_b32 = {"median_ms": round(1e3 * float(np.median(lat[20:])), 4),
+               "p90_ms": round(1e3 * float(np.percentile(lat[20:], 90)), 4), "calls": len(lat) - 20,
+               "workload": "fc_forward of one 32-sample tile (a batch-1 decision padded), synchronised per call"}
+    print(f"# one decision (B=32 tile) on the GPU: {lat_b32['median_ms']:.3f} ms median", file=sys.stderr, flush=True)
+
     # ---- teaching step
     def teach():
         call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4, 3e-5, 1e-4, 0.0, 0.999, stats.data_ptr())
@@ -589,6 +603,7 @@ def main() -> int:
                      "whole_batch_frac": round(ab["infer"] / (t_fwd / K) / PEAK_HBM, 4),
                      "whole_batch_algorithmic_bytes": ab["infer"],
                      "silent_floor": floor_f},
+        "decision_latency_gpu": lat_b32,
         "cpu_baseline": cpu_f,
         "train": {"value": round(sps, 1), "unit": "samples/s", "ms_per_step": round(ms_train, 4),
                   "workload": "fp32 teaching step: forward, KL(teacher||student) over 90 actions, fused backward, "
