@@ -89,6 +89,18 @@ struct Core {
     // those of rows whose own output is zero on the tile.  skip_silent false (FLYGUY_SKIP_SILENT=0): neither (the
     // results are the same).
     bool skip_silent = true;
+    // What the derived tables were made from.  wver[set] counts the writes to the weights (set 0) and to the running
+    // average (set 1): fc_copy into the handle, an Adam step, the trainer's host-side edits.  A table made from a
+    // set at its current version is not made again: the forward's packed pairs and per-row records (from one set),
+    // the transposed read-out weights (from one set) and the backward's packed pairs (from the weights).
+    struct Stamp {
+        int set = -1;
+        unsigned long long ver = 0;
+        bool same(int s, unsigned long long v) const { return set == s && ver == v; }
+    };
+    unsigned long long wver[2] = {1, 1};
+    Stamp made_fpairs, made_info, made_owT, made_tpairs;
+    void weights_written(int set) { if (set == 0 || set == 1) ++wver[set]; }
     std::vector<unsigned char*> fire_bytes;
     std::vector<unsigned*> fire_bits;
     long long adam_t = 0;

@@ -492,6 +492,35 @@ static hipError_t pack(Core& c, int set, bool transposed, bool bf16w) {
     return e;
 }
 
+// The forward's packed pairs and per-row records from `set`, unless they were made from its current version
+static hipError_t derive_forward(Core& c, int set, bool bf16w, const float* gain, const float* theta) {
+    if (!c.made_fpairs.same(set, c.wver[set])) {
+        const hipError_t e = pack(c, set, false, bf16w);
+        if (e != hipSuccess) return e;
+        c.made_fpairs = {set, c.wver[set]};
+    }
+    if (!c.made_info.same(set, c.wver[set])) {
+        const hipError_t e = rowinfo(c, gain, theta);
+        if (e != hipSuccess) return e;
+        c.made_info = {set, c.wver[set]};
+    }
+    return hipSuccess;
+}
+// The backward's transposed pairs and per-row records from the weights (SET_P), unless current
+static hipError_t derive_backward(Core& c, bool bf16w, const float* gain, const float* theta) {
+    if (!c.made_tpairs.same(SET_P, c.wver[SET_P])) {
+        const hipError_t e = pack(c, SET_P, true, bf16w);
+        if (e != hipSuccess) return e;
+        c.made_tpairs = {SET_P, c.wver[SET_P]};
+    }
+    if (!c.made_info.same(SET_P, c.wver[SET_P])) {
+        const hipError_t e = rowinfo(c, gain, theta);
+        if (e != hipSuccess) return e;
+        c.made_info = {SET_P, c.wver[SET_P]};
+    }
+    return hipSuccess;
+}
+
 static bool forward16(Core& c, const float* obs, int B, float* logits, int set);
 static bool backward16(Core& c, const float* dlogits, int B);
 
@@ -503,8 +532,7 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
     {
         Timed t(c, ST_PACK);
-        FG_CHECK(pack(c, set, false, false), false);
-        FG_CHECK(rowinfo(c, gain, theta), false);
+        FG_CHECK(derive_forward(c, set, false, gain, theta), false);
     }
     // each layer below the top records which rows fire on each tile; its bitmaps are packed before the next hop
     auto bytes = [&](int layer) { return c.skip_silent ? c.fire_bytes[(size_t)layer] : nullptr; };
@@ -541,7 +569,8 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     {
         Timed t(c, ST_LOGITS);
         FG_CHECK(launch_logits_mfma(hp, false, c.sizes[c.hops], c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, c.owT,
-                                    c.lpart, logits, B, st), false);
+                                    c.lpart, logits, B, st, c.made_owT.same(set, c.wver[set])), false);
+        c.made_owT = {set, c.wver[set]};
     }
     c.B = B;
     return true;
@@ -556,8 +585,7 @@ bool backward(Core& c, const float* dlogits, int B) {
     for (int i = 0; i < 7; ++i) G[i] = c.arr(SET_G, i);
     {
         Timed t(c, ST_PACK);
-        FG_CHECK(pack(c, SET_P, true, false), false);
-        FG_CHECK(rowinfo(c, gain, theta), false);
+        FG_CHECK(derive_backward(c, false, gain, theta), false);
     }
 
     HopD& top = c.hop[K - 1];
@@ -572,7 +600,10 @@ bool backward(Core& c, const float* dlogits, int B) {
     et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
     {
         Timed t(c, ST_RBWD);
-        FG_CHECK(launch_owT(c.arr(SET_P, 5), c.n_act, c.n_dn, c.owT, st), false);
+        if (!c.made_owT.same(SET_P, c.wver[SET_P])) {
+            FG_CHECK(launch_owT(c.arr(SET_P, 5), c.n_act, c.n_dn, c.owT, st), false);
+            c.made_owT = {SET_P, c.wver[SET_P]};
+        }
         FG_CHECK(launch_readout_bwd_h_mfma(dlogits, c.owT, c.dn_inv, c.n_act, top.rows, et, B, st), false);
         FG_CHECK(launch_readout_bwd_w_mfma(dlogits, top.h, false, top.rows, c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st),
                  false);
@@ -646,8 +677,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
     {
         Timed t(c, ST_PACK);
-        FG_CHECK(pack(c, set, false, true), false);
-        FG_CHECK(rowinfo(c, gain, theta), false);
+        FG_CHECK(derive_forward(c, set, true, gain, theta), false);
     }
     auto bytes = [&](int layer) { return c.skip_silent ? c.fire_bytes[(size_t)layer] : nullptr; };   // (as forward)
     auto bits = [&](int layer) { return c.skip_silent ? c.fire_bits[(size_t)layer] : nullptr; };
@@ -685,7 +715,8 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     {
         Timed t(c, ST_LOGITS);
         FG_CHECK(launch_logits_mfma(hp, true, c.sizes[c.hops], c.dn, c.n_dn, c.arr(set, 5), c.arr(set, 6), c.n_act, c.owT,
-                                    c.lpart, logits, B, st), false);
+                                    c.lpart, logits, B, st, c.made_owT.same(set, c.wver[set])), false);
+        c.made_owT = {set, c.wver[set]};
     }
     c.B = B;
     return true;
@@ -699,8 +730,7 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     for (int i = 0; i < 7; ++i) G[i] = c.arr(SET_G, i);
     {
         Timed t(c, ST_PACK);
-        FG_CHECK(pack(c, SET_P, true, true), false);
-        FG_CHECK(rowinfo(c, gain, theta), false);
+        FG_CHECK(derive_backward(c, true, gain, theta), false);
     }
     HopD& top = c.hop[K - 1];
     BwdEpi16 et;
@@ -716,7 +746,10 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     et.ggain_part = top.ggp; et.gsum_part = top.gsp; et.gp_ld = top.rows;
     {
         Timed t(c, ST_RBWD);
-        FG_CHECK(launch_owT(c.arr(SET_P, 5), c.n_act, c.n_dn, c.owT, st), false);
+        if (!c.made_owT.same(SET_P, c.wver[SET_P])) {
+            FG_CHECK(launch_owT(c.arr(SET_P, 5), c.n_act, c.n_dn, c.owT, st), false);
+            c.made_owT = {SET_P, c.wver[SET_P]};
+        }
         FG_CHECK(launch_readout_bwd_h16_mfma(dlogits, c.owT, c.dn_inv, c.n_act, top.rows, et, B, st), false);
         FG_CHECK(launch_readout_bwd_w_mfma(dlogits, top.h, true, top.rows, c.dn, c.n_dn, c.n_act, c.gow_p, c.gob_p, B, st),
                  false);
@@ -805,6 +838,8 @@ float step(Core& c, float lr, float lr_neuron, float lr_plug, float max_norm, fl
     Timed tm(c, ST_ADAM);
     hipError_t e = launch_adam(c.arr(SET_P, 0), c.arr(SET_G, 0), c.arr(SET_M, 0), c.arr(SET_V, 0), c.arr(SET_EMA, 0), s,
                                c1, c2, nullptr, gs, ema, c.st);
+    c.weights_written(SET_P);
+    c.weights_written(SET_EMA);
     if (e != hipSuccess) { set_error(std::string("adam: ") + hipGetErrorString(e)); return -1.f; }
     return g;
 }
@@ -846,7 +881,11 @@ void* fc_create(const char* net_path, int max_batch) {
 void fc_free(void* h) { release((Core*)h); }
 
 void fc_set_stream(void* h, void* stream) {
-    if (h) ((Core*)h)->st = (hipStream_t)stream;
+    Core* c = (Core*)h;
+    if (!c) return;
+    if (c->st != (hipStream_t)stream)           // (tables made on another stream are made again on this one)
+        c->made_fpairs = c->made_info = c->made_owT = c->made_tpairs = Core::Stamp{};
+    c->st = (hipStream_t)stream;
 }
 
 void fc_sizes(void* h, long long* out) {
@@ -864,6 +903,7 @@ void fc_copy(void* h, int which, int to_core, float** ptrs) {
         float* lib = c->arr(which, i);
         FG_CHECK(hipMemcpyAsync(to_core ? lib : ptrs[i], to_core ? ptrs[i] : lib, c->psize[i] * 4, hipMemcpyDeviceToDevice,
                                 c->st), );
+        if (to_core) c->weights_written(which);
     }
     FG_CHECK(hipStreamSynchronize(c->st), );
 }

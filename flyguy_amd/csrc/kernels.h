@@ -137,9 +137,10 @@ hipError_t launch_readout_bwd_h_mfma(const float* dl, const float* owT, const in
                                      const BwdEpi& epi, int B, hipStream_t st);
 // lpart: RO_SPLIT x B x n_act floats of scratch (the sums over each split of the read-out rows)
 constexpr int RO_SPLIT = 8;
+// (owT_current: owT already holds ow transposed, so the transpose is not launched again)
 hipError_t launch_logits_mfma(const void* hK, bool bf16_states, int rows, const int* dn, int n_dn, const float* ow,
                               const float* ob, int n_act, float* owT, float* lpart, float* logits, int B,
-                              hipStream_t st);
+                              hipStream_t st, bool owT_current = false);
 // the read-out weights' gradient partials come per chunk of RO_CHUNK_S samples: readout_chunks(B) of them
 constexpr int RO_CHUNK_S = 128;
 int readout_chunks(int B);

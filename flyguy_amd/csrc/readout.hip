@@ -186,13 +186,13 @@ hipError_t launch_readout_bwd_w_mfma(const float* dl, const void* hK, bool bf16_
 
 hipError_t launch_logits_mfma(const void* hK, bool bf16_states, int rows, const int* dn, int n_dn, const float* ow,
                               const float* ob, int n_act, float* owT, float* lpart, float* logits, int B,
-                              hipStream_t st) {
+                              hipStream_t st, bool owT_current) {
     const int ma = readout_pad(n_act);
     if (ma > 32 * RO_MAXB || B % 32 != 0) return hipErrorInvalidValue;
     const size_t sm = (size_t)((n_dn + 3) & ~3) * sizeof(int) + (size_t)RO_WAVES * 32 * 33 * sizeof(float);
     if (sm > 64 * 1024) return hipErrorInvalidValue;
     const long long n = (long long)n_dn * ma;
-    k_owT<<<(unsigned)((n + WG - 1) / WG), WG, 0, st>>>(ow, n_act, n_dn, ma, owT);
+    if (!owT_current) k_owT<<<(unsigned)((n + WG - 1) / WG), WG, 0, st>>>(ow, n_act, n_dn, ma, owT);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || B == 0) return e;
     const dim3 grid((unsigned)(B / 32), RO_SPLIT);

@@ -156,6 +156,8 @@ static bool get_dev(Core& c, const float* d, std::vector<float>& v, size_t n) {
     return hipStreamSynchronize(c.st) == hipSuccess;
 }
 static bool put_dev(Core& c, float* d, const std::vector<float>& v) {
+    c.weights_written(SET_P);                  // (it may write the weights or the running average)
+    c.weights_written(SET_EMA);
     if (!v.empty() && hipMemcpyAsync(d, v.data(), v.size() * 4, hipMemcpyHostToDevice, c.st) != hipSuccess) return false;
     return hipStreamSynchronize(c.st) == hipSuccess;
 }

@@ -36,7 +36,11 @@ void fc_sizes(void* core, long long* out);
 void fc_copy(void* core, int which, int to_core, float** ptrs);
 
 /* obs [B][obs_dim] -> logits [B][n_act] with the weights (ema 0) or their running average (ema 1); the states
- * stay in the library for fc_backward.  Replaces fc_forward, flyguy_train.cu:592-598. */
+ * stay in the library for fc_backward.  Replaces fc_forward, flyguy_train.cu:592-598.
+ * The tables a pass derives from a set (packed (source, weight) pairs, per-row records, the transposed read-out
+ * weights) are made again only after that set was written (fc_copy into it, an Adam step, the trainer's edits) or
+ * the stream changed; so repeated forwards with the same weights skip that work.  A forward captured in a HIP graph
+ * replays the tables it made (or found) at capture: capture again after writing the weights. */
 void fc_forward(void* core, const float* obs, int B, float* logits, int ema);
 
 /* Sets the gradient of all seven arrays to zero.  Replaces fc_zero_grad, flyguy_train.cu:599-602. */
@@ -82,7 +86,8 @@ void* fc_create_ex(const void* net_bytes, long long len, int max_batch, int flag
 /* Frees every buffer of the handle (the reference's handles live until the process ends). */
 void fc_free(void* core);
 
-/* Runs the library's work on this HIP stream (hipStream_t; NULL = the null stream) from now on. */
+/* Runs the library's work on this HIP stream (hipStream_t; NULL = the null stream) from now on.  A new stream
+ * makes the next passes derive their tables again, on that stream. */
 void fc_set_stream(void* core, void* stream);
 
 /* KL(teacher || student) over n_act actions for a batch: logits and teacher [B][n_act] device arrays,
