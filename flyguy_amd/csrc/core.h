@@ -27,6 +27,11 @@ struct HopD {
     bool pair_bwd = false;           // the layer's backward takes two tiles per workgroup (pair_tiles in core.hip)
     int gcols = 0;                   // the backward's gain / threshold partials of the layer below: plan columns
     int* gidx = nullptr;             //   (segments, then split rows) and each column's neuron (-1: none)
+    // The reductions' indices, with the first writer of each gradient entry in a backward marked: -1 nothing,
+    // -(i + 2) entry i written here first, i >= 0 entry i written before (by a hop above, or the top layer).
+    // ridx: per backward plan position, the strength; gridx: per plan column, the neuron (gidx's marking).
+    int* ridx = nullptr;
+    int* gridx = nullptr;
     int2 *cw = nullptr, *tcw = nullptr;
     DevPlan fp, bp;
     float *h = nullptr, *ggp = nullptr, *gsp = nullptr;
@@ -65,6 +70,7 @@ struct Core {
     int *in_crow = nullptr, *in_col = nullptr, *n0 = nullptr, *dn = nullptr, *dn_inv = nullptr;
     int2* in_cw = nullptr;
     float4* info0 = nullptr;
+    int* top_ridx = nullptr;         // the top layer's neurons for its gain / threshold sums, marked as HopD::ridx
     DevPlan pp;
     std::vector<HopD> hop;
     float* pm = nullptr;
@@ -151,7 +157,9 @@ bool prof_collect(Core& c);
 // logits [B][n_act]
 bool forward(Core& c, const float* obs, int B, float* logits, int set);
 // backward of the last forward (through SET_P) from dlogits [B][n_act]: gradients ADDED to the SET_G arrays
-bool backward(Core& c, const float* dlogits, int B);
+// fresh: the gradient arrays are zero and this backward is the only one adding to them (a teaching step), so the
+// first sum into each entry is stored instead of added (no read of the entry)
+bool backward(Core& c, const float* dlogits, int B, bool fresh = false);
 float grad_norm(Core& c);
 // Adam + running average over all seven arrays; lr for W, lr_neuron for gain / theta, lr_plug for the rest
 float step(Core& c, float lr, float lr_neuron, float lr_plug, float max_norm, float ema);

@@ -334,6 +334,7 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     std::vector<int> sensory_drow(c->n_s);
     for (int j = 0; j < c->n_s; ++j) sensory_drow[j] = touched[j] ? -1 : -2;
     c->hop.resize(K);
+    std::vector<std::vector<int>> bwd_w(K), bwd_n(K);   // per hop: strength per backward position, neuron per column
     for (int k = 0; k < K; ++k) {
         HopD& d = c->hop[k];
         HH& h = hh[k];
@@ -358,6 +359,9 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
             for (size_t i = 0; i < b.split.size(); ++i) gidx[b.seg.size() + i] = nid_below[(size_t)b.split[i].x];
             d.gidx = upload(*c, gidx);
             if (!d.gidx) return nullptr;
+            bwd_n[k] = std::move(gidx);
+            bwd_w[k].resize(b.pos.size());
+            for (size_t i = 0; i < b.pos.size(); ++i) bwd_w[k][i] = b.pos[i] >= 0 ? h.twidx[(size_t)b.pos[i]] : -1;
         }
         d.has_drive = std::any_of(h.drow.begin(), h.drow.end(), [](int v) { return v >= 0; });
         d.pair_bwd = pair_tiles(h.crow, d.rows);
@@ -370,6 +374,27 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         max_slot = std::max<long long>({max_slot, d.fp.nslot, d.bp.nslot});
         max_pos = std::max<long long>(max_pos, d.bp.npos);
         max_rows = std::max<long long>(max_rows, d.rows);
+    }
+    {   // the first sum into each gradient entry in a backward's order of reductions: the top layer's neurons, then
+        // hop K's strengths and the layer below's neurons, ..., hop 1's (a teaching step stores those sums)
+        auto mark = [](const std::vector<int>& idx, std::vector<unsigned char>& seen) {
+            std::vector<int> m(idx.size());
+            for (size_t i = 0; i < idx.size(); ++i) {
+                const int v = idx[i];
+                m[i] = v < 0 ? -1 : (seen[(size_t)v] ? v : -(v + 2));
+                if (v >= 0) seen[(size_t)v] = 1;
+            }
+            return m;
+        };
+        std::vector<unsigned char> wseen((size_t)std::max<long long>(c->n_w, 1), 0),
+            nseen((size_t)std::max(c->n_neurons, 1), 0);
+        c->top_ridx = upload(*c, mark(c->hop[K - 1].h_nid, nseen));
+        if (!c->top_ridx) return nullptr;
+        for (int k = K - 1; k >= 0; --k) {
+            c->hop[k].ridx = upload(*c, mark(bwd_w[k], wseen));
+            c->hop[k].gridx = upload(*c, mark(bwd_n[k], nseen));
+            if (!c->hop[k].ridx || !c->hop[k].gridx) return nullptr;
+        }
     }
     std::vector<int> dn_inv(c->sizes[K], -1);
     for (int j = 0; j < c->n_dn; ++j) dn_inv[dn[j]] = j;
@@ -522,7 +547,7 @@ static hipError_t derive_backward(Core& c, bool bf16w, const float* gain, const 
 }
 
 static bool forward16(Core& c, const float* obs, int B, float* logits, int set);
-static bool backward16(Core& c, const float* dlogits, int B);
+static bool backward16(Core& c, const float* dlogits, int B, bool fresh);
 
 bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     if (c.prec) return forward16(c, obs, B, logits, set);
@@ -576,8 +601,8 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     return true;
 }
 
-bool backward(Core& c, const float* dlogits, int B) {
-    if (c.prec) return backward16(c, dlogits, B);
+bool backward(Core& c, const float* dlogits, int B, bool fresh) {
+    if (c.prec) return backward16(c, dlogits, B, fresh);
     const int T = B / TW, K = c.hops;
     hipStream_t st = c.st;
     const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
@@ -612,10 +637,10 @@ bool backward(Core& c, const float* dlogits, int B) {
     {
         Timed t(c, ST_REDUCE);
         const long long now = (long long)c.n_act * c.n_dn;
-        const RedJob jobs[4] = {{c.gow_p, now, now, nch, nullptr, nullptr, G[5]},
-                                {c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6]},
-                                {top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1]},
-                                {top.gsp, top.rows, top.rows, T, top.nid, theta, G[2]}};
+        const RedJob jobs[4] = {{c.gow_p, now, now, nch, nullptr, nullptr, G[5], fresh},
+                                {c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], fresh},
+                                {top.ggp, top.rows, top.rows, T, c.top_ridx, nullptr, G[1], fresh},
+                                {top.gsp, top.rows, top.rows, T, c.top_ridx, theta, G[2], fresh}};
         FG_CHECK(launch_reduce_n(jobs, 4, st), false);
     }
 
@@ -655,11 +680,11 @@ bool backward(Core& c, const float* dlogits, int B) {
         Timed t(c, ST_REDUCE);
         // the layer's sums in one launch: each writes its own gradient array
         const int np = d.pair_bwd ? (T + 1) / 2 : T;   // (a two-tile backward stores its partials per pair of tiles)
-        const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, np, d.bp.pidx, nullptr, G[0]},
-                                {ggp, d.gcols, d.gcols, np, d.gidx, nullptr, G[1]},
-                                {gsp, d.gcols, d.gcols, np, d.gidx, theta, G[2]},
-                                {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4]},
-                                {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3]}};
+        const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, np, d.ridx, nullptr, G[0], fresh},
+                                {ggp, d.gcols, d.gcols, np, d.gridx, nullptr, G[1], fresh},
+                                {gsp, d.gcols, d.gcols, np, d.gridx, theta, G[2], fresh},
+                                {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], fresh},
+                                {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], fresh}};
         FG_CHECK(launch_reduce_n(jobs, k == 1 ? 5 : 3, st), false);
         cur ^= 1;
     }
@@ -722,7 +747,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     return true;
 }
 
-static bool backward16(Core& c, const float* dlogits, int B) {
+static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
     const int T = B / TW16, K = c.hops;
     hipStream_t st = c.st;
     const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
@@ -758,10 +783,10 @@ static bool backward16(Core& c, const float* dlogits, int B) {
     {
         Timed t(c, ST_REDUCE);
         const long long now = (long long)c.n_act * c.n_dn;
-        const RedJob jobs[4] = {{c.gow_p, now, now, nch, nullptr, nullptr, G[5]},
-                                {c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6]},
-                                {top.ggp, top.rows, top.rows, T, top.nid, nullptr, G[1]},
-                                {top.gsp, top.rows, top.rows, T, top.nid, theta, G[2]}};
+        const RedJob jobs[4] = {{c.gow_p, now, now, nch, nullptr, nullptr, G[5], fresh},
+                                {c.gob_p, c.n_act, c.n_act, nch, nullptr, nullptr, G[6], fresh},
+                                {top.ggp, top.rows, top.rows, T, c.top_ridx, nullptr, G[1], fresh},
+                                {top.gsp, top.rows, top.rows, T, c.top_ridx, theta, G[2], fresh}};
         FG_CHECK(launch_reduce_n(jobs, 4, st), false);
     }
     int cur = 0;
@@ -803,11 +828,11 @@ static bool backward16(Core& c, const float* dlogits, int B) {
         Timed t(c, ST_REDUCE);
         // the layer's sums in one launch: each writes its own gradient array
         const int np = pair ? (T + 1) / 2 : T;        // (a two-tile backward stores its partials per pair of tiles)
-        const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, np, d.bp.pidx, nullptr, G[0]},
-                                {ggp, d.gcols, d.gcols, np, d.gidx, nullptr, G[1]},
-                                {gsp, d.gcols, d.gcols, np, d.gidx, theta, G[2]},
-                                {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4]},
-                                {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3]}};
+        const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, np, d.ridx, nullptr, G[0], fresh},
+                                {ggp, d.gcols, d.gcols, np, d.gridx, nullptr, G[1], fresh},
+                                {gsp, d.gcols, d.gcols, np, d.gridx, theta, G[2], fresh},
+                                {c.ginb, c.n_s, c.n_s, T, nullptr, nullptr, G[4], fresh},
+                                {c.ginw, c.E_in, c.E_in, T, nullptr, nullptr, G[3], fresh}};
         FG_CHECK(launch_reduce_n(jobs, k == 1 ? 5 : 3, st), false);
         cur ^= 1;
     }
@@ -967,7 +992,7 @@ float fc_teach_step(void* h, const float* obs, const float* teacher, int B, floa
         Timed t(*c, ST_LOSS);
         FG_CHECK(launch_loss(c->lg, teacher, c->dl, c->stats_part, stats ? stats : c->stats, c->n_act, B, it, c->st), -1.f);
     }
-    if (!backward(*c, c->dl, B)) return -1.f;
+    if (!backward(*c, c->dl, B, true)) return -1.f;          // (the gradient was cleared above)
     return step(*c, lr, lr_neuron, lr_plug, max_norm, ema);
 }
 

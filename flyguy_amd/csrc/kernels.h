@@ -144,8 +144,10 @@ hipError_t launch_logits_mfma(const void* hK, bool bf16_states, int rows, const 
 // the read-out weights' gradient partials come per chunk of RO_CHUNK_S samples: readout_chunks(B) of them
 constexpr int RO_CHUNK_S = 128;
 int readout_chunks(int B);
-// G[idx[i]] += sum over nt tiles of part[t * ld + i] (times -sigmoid(theta[idx[i]]) if theta); idx[i] < 0: skipped,
-// idx == nullptr: i itself.  The indices a launch names are distinct, so no two threads add to one entry.
+// G[idx[i]] += sum over nt tiles of part[t * ld + i] (times -sigmoid(theta[idx[i]]) if theta); idx[i] = -1: skipped,
+// idx[i] = -(j + 2): entry j, the first sum into it in this backward; idx == nullptr: i itself (always the first).
+// fresh (the gradient was cleared and only this backward adds to it): a first sum is stored, not added.  The indices
+// a launch names are distinct, so no two threads write one entry.
 hipError_t launch_reduce(const float* part, long long ld, long long n, int nt, const int* idx, const float* theta,
                          float* G, hipStream_t st);
 // The same for up to RED_JOBS sums in one launch (a layer's weight, gain and threshold gradients, say).  The jobs of
@@ -158,6 +160,7 @@ struct RedJob {
     const int* idx = nullptr;
     const float* theta = nullptr;
     float* G = nullptr;
+    int fresh = 0;
 };
 constexpr int RED_JOBS = 5;
 hipError_t launch_reduce_n(const RedJob* jobs, int n, hipStream_t st);

@@ -533,14 +533,17 @@ int readout_chunks(int B) { return (B + RO_CHUNK_S - 1) / RO_CHUNK_S; }
 
 // ------------------------------------------------------------------------------------------------ reductions
 // G[idx[i]] += sum_t part[t * ld + i]  (times -sigmoid(theta[idx[i]]) when theta is given: the threshold's gradient);
-// idx[i] < 0 (a plan position no edge uses) adds nothing
+// idx[i] = -1 (a plan position no edge uses) adds nothing; idx[i] <= -2 marks entry -idx[i] - 2's first sum, which a
+// fresh job stores (kernels.h, RedJob)
 __global__ __launch_bounds__(WG) void k_reduce(JobTable<RedJob, RED_JOBS> jt) {
     long long b0;
     const RedJob r = job_of(jt, blockIdx.x, b0);
     const long long i = ((long long)blockIdx.x - b0) * WG + threadIdx.x;
     if (i >= r.n) return;
-    const long long o = r.idx ? r.idx[i] : i;
-    if (o < 0) return;
+    const int v = r.idx ? r.idx[i] : -1;
+    if (r.idx && v == -1) return;
+    const bool first = !r.idx || v < -1;
+    const long long o = !r.idx ? i : (v < -1 ? -(long long)v - 2 : (long long)v);
     const float* __restrict__ part = r.part;
     float s = 0.f;
     int t = 0;
@@ -553,7 +556,10 @@ __global__ __launch_bounds__(WG) void k_reduce(JobTable<RedJob, RED_JOBS> jt) {
     }
     for (; t < r.nt; ++t) s += part[(size_t)t * r.ld + i];
     if (r.theta) s *= -sigmoid_f(r.theta[o]);
-    r.G[o] += s;
+    if (r.fresh && first)
+        r.G[o] = s + 0.f;                       // (= 0 + s, -0 included, without reading the entry)
+    else
+        r.G[o] += s;
 }
 
 // KL(teacher || student) per sample, dl = d(mean loss)/d logits (flyguy_train.cu:104-123).  Eight lanes per sample,

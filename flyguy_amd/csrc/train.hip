@@ -765,7 +765,7 @@ static bool fwd_bwd(Core& c, const float* obs, const float* tl, int B, float it,
     FG_CHECK(launch_fill(c.arr(SET_G, 0), 0.f, c.PT, c.st), false);
     if (!forward(c, obs, B, c.lg, SET_P)) return false;
     FG_CHECK(launch_loss(c.lg, tl, c.dl, c.stats_part, stats, c.n_act, B, it, c.st, true), false);
-    return backward(c, c.dl, B);
+    return backward(c, c.dl, B, true);                      // (the gradient was cleared above)
 }
 
 typedef std::unique_ptr<Core, void (*)(Core*)> CoreP;

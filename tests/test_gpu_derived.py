@@ -81,3 +81,38 @@ def test_passes_follow_every_weight_write(gpu_lib, flags):
     side.synchronize()
     call("fc_set_stream", core.h, None)
     assert np.array_equal(_bits(got), _bits(fresh(core.get(0))))
+
+
+@pytest.mark.parametrize("flags", [0, 1])
+@pytest.mark.parametrize("name,hops,fan", [("b", 4, 8), ("a", 4, 5)])
+def test_teach_step_stores_first_sums_as_its_parts_add_them(gpu_lib, flags, name, hops, fan):
+    """A teaching step stores the first sum into each gradient entry instead of adding it to the cleared entry.  On
+    networks whose hops share strengths and neurons (an entry summed by several reductions), two steps leave the
+    weights, running average and Adam moments bit-identical to zero_grad + backward (which adds) + step."""
+    torch.manual_seed(5)
+    f = lively(FlyActor(toy(name), 517, 90, hops=hops, fan=fan), 5)
+    s = structure(f)
+    used = np.concatenate([np.asarray(h["widx"]) for h in s["hop"]])
+    assert len(np.unique(used)) < len(used)                    # some strengths are summed in several hops
+    params = params_from_torch(f, s)
+    B = 128
+    rng = np.random.default_rng(11)
+    obs = rng.standard_normal((B, 517)).astype(np.float32)
+    x = torch.as_tensor(obs).cuda()
+    t = torch.as_tensor((2 * rng.standard_normal((B, 90))).astype(np.float32)).cuda()
+    say(f"teach step vs its parts, {name} hops {hops} fan {fan}, flags {flags}")
+    a = Core(s, params, max_batch=B, flags=flags)
+    b = Core(s, params, max_batch=B, flags=flags)
+    for _ in range(2):
+        call("fc_teach_step", a.h, x.data_ptr(), t.data_ptr(), B, 1.0, 1e-2, 3e-3, 1e-2, 0.0, 0.9, None)
+        lg = torch.as_tensor(b.forward(obs)).cuda()
+        dl = torch.empty(B, 90, device="cuda")
+        st = torch.zeros(2, device="cuda")
+        call("fc_kl_loss", b.h, lg.data_ptr(), t.data_ptr(), B, 1.0, dl.data_ptr(), st.data_ptr())
+        b.zero_grad()
+        b.backward(dl.cpu().numpy())
+        call("fc_step", b.h, 1e-2, 3e-3, 1e-2, 0.0, 0.9)
+    torch.cuda.synchronize()
+    for which in (0, 1, 2, 3):
+        for pa, pb in zip(a.get(which), b.get(which)):
+            assert np.array_equal(_bits(pa), _bits(pb)), which
