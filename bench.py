@@ -2,7 +2,8 @@
 """Benchmark of the fly actor's batched inference and teaching step on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096]
-                    [--no-cpu] [--trainer-steps 60] [--config5-steps 10] [--config4-steps 10]
+                    [--no-cpu] [--no-floor] [--latency-calls 200] [--trainer-steps 60] [--config5-steps 10]
+                    [--config4-steps 10]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -395,6 +396,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--trainer-steps", type=int, default=60, help="teaching-trainer loop steps at B=4096 (0: skip)")
     ap.add_argument("--config5-steps", type=int, default=10, help="timed bfloat16 B=16384 batches and steps (0: skip)")
+    ap.add_argument("--latency-calls", type=int, default=200,
+                    help="synchronised one-tile forwards timed for a single decision's latency (the first 20 untimed; 0: skip)")
     ap.add_argument("--config4-steps", type=int, default=10,
                     help="timed whole-connectome B=1024 batches and steps (0: skip; its index build takes ~20 s)")
     ap.add_argument("--no-floor", action="store_true",
@@ -496,16 +499,18 @@ def main() -> int:
     # ---- one decision on the GPU: batch 1 padded to one 32-sample tile (NativeFlyActor's rule), each call
     # synchronised, as a bot deciding one car at a time would run it
     lat = []
-    for _ in range(200):
+    for _ in range(args.latency_calls):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         call("fc_forward", core, obs.data_ptr(), 32, logits.data_ptr(), 0)
         torch.cuda.synchronize()
         lat.append(time.perf_counter() - t0)
-    lat_b32 = {"median_ms": round(1e3 * float(np.median(lat[20:])), 4),
-               "p90_ms": round(1e3 * float(np.percentile(lat[20:], 90)), 4), "calls": len(lat) - 20,
-               "workload": "fc_forward of one 32-sample tile (a batch-1 decision padded), synchronised per call"}
-    print(f"# one decision (B=32 tile) on the GPU: {lat_b32['median_ms']:.3f} ms median", file=sys.stderr, flush=True)
+    lat_b32 = None
+    if len(lat) > 20:
+        lat_b32 = {"median_ms": round(1e3 * float(np.median(lat[20:])), 4),
+                   "p90_ms": round(1e3 * float(np.percentile(lat[20:], 90)), 4), "calls": len(lat) - 20,
+                   "workload": "fc_forward of one 32-sample tile (a batch-1 decision padded), synchronised per call"}
+        print(f"# one decision (B=32 tile) on the GPU: {lat_b32['median_ms']:.3f} ms median", file=sys.stderr, flush=True)
 
     # ---- teaching step
     def teach():
