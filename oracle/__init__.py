@@ -1,7 +1,7 @@
 """ORACLE - test infrastructure only.
 
-CPU restatements of the reference's fly-actor path, used as the checker of the MI355X library by tests/,
-__graft_entry__.smoke() and bench.py's CPU baseline, never by the product:
+CPU restatements of the reference's fly-actor path, against which tests/, __graft_entry__.smoke() and bench.py's
+CPU baseline hold the MI355X library; never used by the product:
   fly_oracle.c / oracle.py   forward, KL loss, backward, Adam (flyguy/native/flyguy_train.cu:51-203), float and
                              double builds, reading NET.bin with its own parser;
   index.py                   the graph indexing of FlyActor.__init__ (flyguy/fly.py:35-154) and

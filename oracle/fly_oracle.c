@@ -1,6 +1,6 @@
 /* ORACLE - test infrastructure only.  A CPU restatement of the reference's arithmetic for the fly actor's
- * forward, KL loss, backward and Adam, used by tests/, __graft_entry__.smoke() and bench.py's CPU baseline
- * as the checker of the MI355X library.  It is never part of the product path.
+ * forward, KL loss, backward and Adam, against which tests/, __graft_entry__.smoke() and bench.py's CPU baseline
+ * hold the MI355X library.  It is never part of the product path.
  *
  * Compiled twice (oracle/Makefile): REAL=float follows the reference kernels' per-element arithmetic and
  * summation order (flyguy/native/flyguy_train.cu, fused multiply-adds as nvcc contracts them); REAL=double
