@@ -2,8 +2,8 @@
 """Benchmark of the fly actor's batched inference and teaching step on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096]
-                    [--no-cpu] [--no-floor] [--latency-calls 200] [--trainer-steps 60] [--config5-steps 10]
-                    [--config4-steps 10]
+                    [--no-cpu] [--no-floor] [--latency-calls 200] [--trainer-steps 60] [--bf16-steps 10]
+                    [--connectome-steps 10]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -20,8 +20,11 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
            train: one teaching step of that PyTorch path on the CPU at B = 4096.
   silent_floor (in each roofline): the dominant hop launch re-timed with its source layer silenced, so that every
            gather is skipped: the kernel's floor without memory traffic, measured in the same run.
-  config5: the bfloat16-state core at B = 16384 (forward and teaching step) on the same network and on its
+  decision_latency_gpu: one fc_forward of a 32-sample tile (a batch-1 decision padded), synchronised per call;
+  bf16_b16384: the bfloat16-state core at B = 16384 (forward and teaching step) on the same network and on its
            Erdos-Renyi control;
+  whole_connectome_b1024: forward and teaching step at B = 1024 on a graph of the whole connectome's size (166,700
+           neurons, 15.3M connections) indexed by FlyActor, with roofline fractions on the pruned hops' bytes;
   trainer: samples / s of the teaching trainer's own loop (flyguy_amd/flyguy_train, run as a child process on
            synthetic binary16 FLYD chunks of the same network: draw, gather, step, as its log reports them) at
            B = 4096, at the reference trainer's default B = 512, and with --bf16 1 at B = 16384.
@@ -116,7 +119,7 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
         fwd = {"value": sample / dt, "unit": "decisions/s", "cores": 1, "kind": "reference",
                "sample": f"{sample} batch-1 decisions of the same network through fly_infer.cpp (compiled from the "
                          f"reference), {dt:.1f} s"}
-        # configuration 1: batch-1 decisions one call at a time, median latency over 300 (as the bot times them), of
+        # batch-1 decisions one call at a time, median latency over 300 (as the bot times them), of
         # the reference's compiled CPU forward and of this package's CPU decision library (include/fly_infer.h),
         # alternating decision by decision so that both meet the same clock and cache conditions
         from flyguy_amd.cpu_decisions import CpuDecisions
@@ -152,7 +155,7 @@ def cpu_baselines(s, params, sample: int, train_batch: int) -> tuple[dict | None
             c1["ours_threads"][str(n_thr)] = {"median_ms": round(1e3 * float(np.median(lat)), 4),
                                               "p90_ms": round(1e3 * float(np.percentile(lat, 90)), 4)}
             del f
-        fwd["config1"] = c1
+        fwd["batch1"] = c1
         del ours
         # the same on every host core this process may use (at most 16, a GPU's share of the host): one handle per
         # thread (a handle is not thread-safe; ctypes releases the GIL during the call), sample / 4 decisions each
@@ -275,7 +278,7 @@ def trainer_leg(s, params, batches, steps: int) -> dict:
     return out
 
 
-def config5_leg(steps: int, warmup: int, B: int = 16384) -> dict:
+def bf16_leg(steps: int, warmup: int, B: int = 16384) -> dict:
     """The bfloat16-state core (fc_create_ex, FC_STATES_BF16) at B = 16384 on the synthetic network and on its
     Erdos-Renyi control (uniform in-degrees, same counts): forward decisions/s and teaching-step samples/s."""
     import numpy as np
@@ -335,7 +338,7 @@ def config5_leg(steps: int, warmup: int, B: int = 16384) -> dict:
     return out
 
 
-def config4_leg(steps: int, warmup: int, B: int = 1024) -> dict:
+def connectome_leg(steps: int, warmup: int, B: int = 1024) -> dict:
     """The whole-connectome case (synthetic graph of 166,700 neurons and 15,283,167 connections, indexed by FlyActor)
     at B = 1024, float32: forward decisions/s and teaching-step samples/s."""
     import torch
@@ -395,10 +398,10 @@ def main() -> int:
     ap.add_argument("--cpu-train-batch", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--trainer-steps", type=int, default=60, help="teaching-trainer loop steps at B=4096 (0: skip)")
-    ap.add_argument("--config5-steps", type=int, default=10, help="timed bfloat16 B=16384 batches and steps (0: skip)")
+    ap.add_argument("--bf16-steps", type=int, default=10, help="timed bfloat16 B=16384 batches and steps (0: skip)")
     ap.add_argument("--latency-calls", type=int, default=200,
                     help="synchronised one-tile forwards timed for a single decision's latency (the first 20 untimed; 0: skip)")
-    ap.add_argument("--config4-steps", type=int, default=10,
+    ap.add_argument("--connectome-steps", type=int, default=10,
                     help="timed whole-connectome B=1024 batches and steps (0: skip; its index build takes ~20 s)")
     ap.add_argument("--no-floor", action="store_true",
                     help="skip the silent-source re-timing of the dominant hops (a counter run then sees only the "
@@ -575,12 +578,12 @@ def main() -> int:
         cpu_f, cpu_t = cpu_baselines(s, params, args.cpu_sample, args.cpu_train_batch)
     L.fc_free(core)
     core = None
-    config5 = None
-    if args.config5_steps > 0:
-        config5 = config5_leg(args.config5_steps, W)
-        config5["workload"] = ("bfloat16 states (x, drive, every layer's h, gathered gz), float32 sums, gradients and "
+    bf16 = None
+    if args.bf16_steps > 0:
+        bf16 = bf16_leg(args.bf16_steps, W)
+        bf16["workload"] = ("bfloat16 states (x, drive, every layer's h, gathered gz), float32 sums, gradients and "
                                "Adam; B=16384; the synthetic network (lognormal in-degree) and its Erdos-Renyi control")
-    config4 = config4_leg(args.config4_steps, W) if args.config4_steps > 0 else None
+    connectome = connectome_leg(args.connectome_steps, W) if args.connectome_steps > 0 else None
     trainer = None
     if args.trainer_steps > 0:
         trainer = trainer_leg(s, params, ((4096, False), (512, False), (16384, True)), args.trainer_steps)
@@ -624,8 +627,8 @@ def main() -> int:
                                "silent_floor": floor_b},
                   "cpu_baseline": cpu_t},
         "trainer": trainer,
-        "config5": config5,
-        "config4": config4,
+        "bf16_b16384": bf16,
+        "whole_connectome_b1024": connectome,
         "stages_ms": {"forward": {k: round(v[0] / v[1], 4) for k, v in prof_fwd.items()},
                       "train": {k: round(v[0] / v[1], 4) for k, v in prof_train.items()}},
     }
