@@ -35,7 +35,7 @@ struct HopD {
     int2 *cw = nullptr, *tcw = nullptr;
     DevPlan fp, bp;
     float *h = nullptr, *ggp = nullptr, *gsp = nullptr;
-    float4* info = nullptr;          // per row {gain, softplus(theta), re-drive row}, refreshed at every pass
+    float4* info = nullptr;          // per row {gain, softplus(theta), re-drive row}, from the current weights
     float* zk = nullptr;             // the pre-activation, kept only by survey passes (allocated on first use)
     std::vector<int> h_nid, h_crow, h_col, h_widx;   // host copies of the index arrays (the revive surgery)
 };

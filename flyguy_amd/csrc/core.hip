@@ -4,8 +4,8 @@
 // Device memory of a handle (max_batch = Bm, Tm = Bm / 32 tiles, states tiled [T][rows][32] fp32):
 //   parameters: one block of 5 sets x PT floats (sets in fc_copy order: weights, running average, m, v,
 //               gradient), each set holding the seven arrays at 64-float aligned offsets, so Adam is one launch;
-//   structure: NET.bin's index arrays, the packed (index, weight) pairs of every product (refreshed from the
-//              current weights at each pass), and the row plans (forward: CSR rows; backward: CSC rows);
+//   structure: NET.bin's index arrays, the packed (index, weight) pairs of every product (made again from the
+//              weights after every write to them), and the row plans (forward: CSR rows; backward: CSC rows);
 //   states: x, drive, h0, gdrive, h_k per hop, two gz buffers, logits / dlogits (a hop layer's pre-activation z is
 //           not kept: the backward needs it only where h > 0, and there it is (h + softplus(theta)) / gain);
 //   partial sums: split rows, per-edge weight gradients [T or T/2][E_k], per-row gain / threshold gradients [T][rows],

@@ -42,7 +42,7 @@ struct Plan {
 // of it returns zeros without touching memory; a masked global load of it is skipped.
 constexpr int NO_ROW = 0x01FFFFFF;
 
-// Per row of a layer, refreshed from the weights at every pass (k_rowinfo): {gain[nid], softplus(theta[nid]),
+// Per row of a layer, made from the weights after every write to them (k_rowinfo): {gain[nid], softplus(theta[nid]),
 // re-drive row in the sensory layer as int bits (-1: none), 0}.  One 16-byte load gives a row's whole neuron.
 // What follows the sum over a row's edges in the forward pass (flyguy_train.cu:84-94):
 // acc (+ bias) (+ drive[drow]) -> z; h = relu(gain * z - softplus(theta)).  info == nullptr: z only (raw product).
