@@ -80,14 +80,17 @@ def silent_floor(ms: float, floor_ms: float, E: int, B: int) -> dict:
 
 
 def kernel_sources_sha() -> str:
-    """SHA-256 over the library's kernel sources: a counter run recorded for other sources is stale."""
+    """SHA-256 over the library's kernel sources without their comments and with runs of white space made one
+    space: a counter run recorded for other code is stale, one recorded before a change of comments only is not."""
     import hashlib
+    import re
     h = hashlib.sha256()
     d = os.path.join(os.path.dirname(os.path.abspath(__file__)), "flyguy_amd", "csrc")
     for n in sorted(os.listdir(d)):
         if n.endswith((".hip", ".h")):
-            with open(os.path.join(d, n), "rb") as fh:
-                h.update(n.encode() + b"\0" + fh.read())
+            with open(os.path.join(d, n), encoding="utf-8") as fh:
+                code = re.sub(r"/\*.*?\*/|//[^\n]*", " ", fh.read(), flags=re.S)
+            h.update(n.encode() + b"\0" + " ".join(code.split()).encode())
     return h.hexdigest()
 
 
