@@ -43,7 +43,10 @@ struct HostPlan {
 // Cut rows into segments of at most seg_max edges (a longer row gets ceil(d / seg_max) segments of nearly equal
 // length), order all segments longest first (equal lengths keep (row, segment) order), deal them 8 to a wave and lay
 // the edges out in plan order: edge k of the segment of group g of wave w at position woff[w] + 64 (k / 8) + 8 g +
-// k % 8, each wave taking 64 positions per step of its longest segment.  drow (nullable): every row's re-drive row.
+// k % 8, each wave taking 64 positions per step of its longest segment.  drow (nullable): every row's re-drive field.
+// Among segments of equal length, whole rows with a re-drive line to load (drow >= 0) come first: that line comes
+// from HBM, and a wave waits for it once whether one or all eight of its rows load one, so they are gathered into as
+// few waves as the lengths allow (hop 1 forward 1.167 -> 1.116 ms at B=4096 on the synthetic 3-hop network).
 static bool make_plan(const int* rowptr, int rows, int seg_max, const int* drow, HostPlan& p) {
     p = HostPlan{};
     if (rows < 0 || seg_max <= 0 || (rows > 0 && rowptr[0] != 0)) return false;
@@ -65,7 +68,11 @@ static bool make_plan(const int* rowptr, int rows, int seg_max, const int* drow,
         }
         p.nslot += ns;
     }
-    std::stable_sort(segs.begin(), segs.end(), [](const S& a, const S& b) { return a.e - a.b > b.e - b.b; });
+    auto loads_drive = [&](const S& s) { return drow && s.slot < 0 && drow[s.row] >= 0; };
+    std::stable_sort(segs.begin(), segs.end(), [&](const S& a, const S& b) {
+        const int la = a.e - a.b, lb = b.e - b.b;
+        return la != lb ? la > lb : loads_drive(a) > loads_drive(b);
+    });
     const size_t n = segs.size(), nw = (n + 7) / 8;
     long long npos = 0;
     p.wave.resize(nw);
