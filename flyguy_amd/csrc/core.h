@@ -36,6 +36,7 @@ struct HopD {
     DevPlan fp, bp;
     float *h = nullptr, *ggp = nullptr, *gsp = nullptr;
     float4* info = nullptr;          // per row {gain, softplus(theta), re-drive row}, from the current weights
+    float4* sinfo = nullptr;         // the same per segment of the forward plan fp (a wave's 8 in one line)
     float* zk = nullptr;             // the pre-activation, kept only by survey passes (allocated on first use)
     std::vector<int> h_nid, h_crow, h_col, h_widx;   // host copies of the index arrays (the revive surgery)
 };
@@ -70,6 +71,7 @@ struct Core {
     int *in_crow = nullptr, *in_col = nullptr, *n0 = nullptr, *dn = nullptr, *dn_inv = nullptr;
     int2* in_cw = nullptr;
     float4* info0 = nullptr;
+    float4* sinfo0 = nullptr;        // the sensory rows' records per segment of the plug's plan
     int* top_ridx = nullptr;         // the top layer's neurons for its gain / threshold sums, marked as HopD::ridx
     DevPlan pp;
     std::vector<HopD> hop;

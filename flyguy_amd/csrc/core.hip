@@ -452,10 +452,12 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         d.ggp = dalloc<float>(*c, Tp * gc);
         d.gsp = dalloc<float>(*c, Tp * gc);
         d.info = dalloc<float4>(*c, d.rows);
-        if (!d.h || !d.ggp || !d.gsp || !d.info) return nullptr;
+        d.sinfo = dalloc<float4>(*c, d.fp.nseg);
+        if (!d.h || !d.ggp || !d.gsp || !d.info || !d.sinfo) return nullptr;
     }
     c->info0 = dalloc<float4>(*c, c->n_s);
-    if (!c->info0) return nullptr;
+    c->sinfo0 = dalloc<float4>(*c, c->pp.nseg);
+    if (!c->info0 || !c->sinfo0) return nullptr;
     if (const char* f = std::getenv("FLYGUY_SKIP_SILENT")) c->skip_silent = f[0] != '0';
     for (int l = 0; l < K; ++l) {                   // (the top layer's would have no reader)
         c->fire_bytes.push_back(dalloc<unsigned char>(*c, Tp * (size_t)fires_bytes_ld(c->sizes[l])));
@@ -502,7 +504,11 @@ bool check_batch(const Core* c, int B) {
 static hipError_t rowinfo(Core& c, const float* gain, const float* theta) {
     std::vector<RowJob> j;
     j.push_back({c.n0, nullptr, c.info0, c.n_s});
-    for (auto& d : c.hop) j.push_back({d.nid, d.has_drive ? d.drow : nullptr, d.info, d.rows});
+    j.push_back({c.n0, nullptr, c.sinfo0, c.pp.nseg, c.pp.seg});
+    for (auto& d : c.hop) {
+        j.push_back({d.nid, d.has_drive ? d.drow : nullptr, d.info, d.rows});
+        j.push_back({d.nid, d.has_drive ? d.drow : nullptr, d.sinfo, d.fp.nseg, d.fp.seg});
+    }
     hipError_t e = hipSuccess;
     for (size_t k = 0; k < j.size() && e == hipSuccess; k += ROW_JOBS)
         e = launch_rowinfo_n(j.data() + k, (int)std::min<size_t>(ROW_JOBS, j.size() - k), gain, theta, c.st);
@@ -572,6 +578,7 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     FwdEpi e0;
     e0.bias = c.arr(set, 4);
     e0.info = c.info0;
+    e0.sinfo = c.sinfo0;
     e0.z = c.drive; e0.lz = tiled(c.n_s);
     e0.h = c.h0; e0.lh = tiled(c.n_s);
     e0.fires = bytes(0);
@@ -585,6 +592,7 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     for (auto& d : c.hop) {
         FwdEpi e;
         e.info = d.info;
+        e.sinfo = d.sinfo;
         if (d.has_drive) { e.drive = c.drive; e.ldrive = tiled(c.n_s); }
         e.h = d.h; e.lh = tiled(d.rows);
         if (c.keep_z) { e.z = d.zk; e.lz = tiled(d.rows); }
@@ -716,6 +724,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     FwdEpi16 e0;
     e0.bias = c.arr(set, 4);
     e0.info = c.info0;
+    e0.sinfo = c.sinfo0;
     e0.z = s16(c.drive);
     e0.h = s16(c.h0);
     e0.rows = c.n_s;
@@ -730,6 +739,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     for (auto& d : c.hop) {
         FwdEpi16 e;
         e.info = d.info;
+        e.sinfo = d.sinfo;
         if (d.has_drive) { e.drive = s16(c.drive); e.n_s = c.n_s; }
         e.h = s16(d.h);
         if (c.keep_z) e.z = s16(d.zk);

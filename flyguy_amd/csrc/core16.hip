@@ -61,13 +61,15 @@ struct FwdIn16 {
     float dv[8];
     float g, sp;
 };
-__device__ __forceinline__ void fwd_inputs16(const FwdEpi16& e, int t, int d, int tile, int sub, FwdIn16& in) {
+// recs[i]: the row's record (as fwd_inputs)
+__device__ __forceinline__ void fwd_inputs16(const FwdEpi16& e, const float4* recs, int i, int d, int tile, int sub,
+                                             FwdIn16& in) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) in.dv[k] = 0.f;
     in.g = in.sp = 0.f;
     if (e.drive && d >= 0) ld8(e.drive, e.n_s, tile, d, sub, in.dv);
-    if (e.info) {
-        const float4 r = e.info[t];
+    if (recs) {
+        const float4 r = recs[i];
         in.g = r.x;
         in.sp = r.y;
     }
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
         __builtin_amdgcn_sched_barrier(0);
         if (left > 8) nxt = q[64 * (j + 1)];
         if (j == 0 && whole) {                 // the row's own inputs after the first gathers; the bias starts the sum
-            fwd_inputs16(epi, sg.x, sg.z, tile, sub, in);
+            fwd_inputs16(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub, in);
             if (epi.bias) {
                 const float b = epi.bias[sg.x];
 #pragma unroll
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
         for (int s = 0; s < 8; s += 2) fma_pair(wt[s], wt[s + 1], raw[s], raw[s + 1], acc);
     }
     if (whole && !(wok && wv.y > 0)) {          // a wave without edges
-        fwd_inputs16(epi, sg.x, sg.z, tile, sub, in);
+        fwd_inputs16(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub, in);
         if (epi.bias) {
             const float b = epi.bias[sg.x];
 #pragma unroll
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16_combine(Plan p, const float* __re
     const float b = epi.bias ? epi.bias[s.x] : 0.f;
     float acc[8] = {b, b, b, b, b, b, b, b};
     FwdIn16 in{};
-    fwd_inputs16(epi, s.x, s.w, tile, sub, in);
+    fwd_inputs16(epi, epi.info, s.x, s.w, tile, sub, in);
     add_parts16(part + (size_t)tile * p.nslot * TW16 + sub * 8, s.y, s.z, acc);
     fwd_finish16(epi, s.x, tile, sub, acc, in);
 }

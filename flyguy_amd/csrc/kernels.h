@@ -49,6 +49,8 @@ constexpr int NO_ROW = 0x01FFFFFF;
 struct FwdEpi {
     const float* bias = nullptr;
     const float4* info = nullptr;
+    const float4* sinfo = nullptr;    // the same records per segment of the product's plan: whole rows read these
+                                      // (k_fwd), split rows info (k_fwd_combine); both or neither are given
     const float* drive = nullptr;     // the sensory layer's drive, for re-drive rows (nullptr: none in this layer)
     Lay ldrive{};
     float* z = nullptr;               // the pre-activation: stored for the sensory layer (the drive) and raw products
@@ -169,6 +171,7 @@ hipError_t launch_reduce_n(const RedJob* jobs, int n, hipStream_t st);
 struct FwdEpi16 {
     const float* bias = nullptr;
     const float4* info = nullptr;
+    const float4* sinfo = nullptr;           // per segment of the plan, as FwdEpi::sinfo
     const unsigned short* drive = nullptr;   // re-drive source: the sensory layer's drive (nullptr: none here)
     int n_s = 0;                             // rows of drive
     unsigned short* z = nullptr;             // the sensory layer's pre-activation (its drive)
@@ -229,6 +232,9 @@ struct RowJob {
     const int *nid = nullptr, *drow = nullptr;
     float4* info = nullptr;
     int rows = 0;
+    // non-null: the records in the order of a row plan's segments instead (rows = the plan's segments, row = seg.x),
+    // so that a wave's 8 rows read one 128-byte line (FwdEpi::sinfo)
+    const int4* seg = nullptr;
 };
 constexpr int ROW_JOBS = 8;
 hipError_t launch_rowinfo_n(const RowJob* jobs, int n, const float* gain, const float* theta, hipStream_t st);

@@ -70,11 +70,13 @@ struct FwdIn {
     float4 dv;
     float g, sp;
 };
-__device__ __forceinline__ FwdIn fwd_inputs(const FwdEpi& e, int t, int d, int tile, int sub) {
+// recs[i]: the row's record (FwdEpi::sinfo from the wave's first segment and i its group for a whole row, info and
+// the row for a split one; nullptr: none)
+__device__ __forceinline__ FwdIn fwd_inputs(const FwdEpi& e, const float4* recs, int i, int d, int tile, int sub) {
     FwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f};
     if (e.drive && d >= 0) in.dv = *at4u(e.drive, e.ldrive, tile, d, sub);
-    if (e.info) {
-        const float4 r = e.info[t];
+    if (recs) {
+        const float4 r = recs[i];
         in.g = r.x;
         in.sp = r.y;
     }
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
         __builtin_amdgcn_sched_barrier(0);
         if (left > 8) nxt = q[64 * (j + 1)];
         if (j == 0 && whole) {
-            in = fwd_inputs(epi, sg.x, sg.z, tile, sub);
+            in = fwd_inputs(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub);
             if (epi.bias) acc = splat(epi.bias[sg.x]);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
         for (int s = 0; s < 8; ++s) fma4(wt[s], v[s], acc);
     }
     if (whole && !(wok && wv.y > 0)) {          // a wave without edges
-        in = fwd_inputs(epi, sg.x, sg.z, tile, sub);
+        in = fwd_inputs(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub);
         if (epi.bias) acc = splat(epi.bias[sg.x]);
     }
     if (!live) return;
@@ -184,7 +186,7 @@ __global__ __launch_bounds__(WG) void k_fwd_combine(Plan p, const float* __restr
     int4 s;
     if (!load_split(p, i, s)) return;     // whole 8-lane groups leave together
     float4 acc = epi.bias ? splat(epi.bias[s.x]) : splat(0.f);
-    const FwdIn in = fwd_inputs(epi, s.x, s.w, tile, sub);
+    const FwdIn in = fwd_inputs(epi, epi.info, s.x, s.w, tile, sub);
     add_parts(part, lp, tile, s.y, s.z, sub, acc);
     fwd_finish(epi, s.x, tile, sub, acc, in);
 }
@@ -695,8 +697,9 @@ __global__ __launch_bounds__(WG) void k_rowinfo(JobTable<RowJob, ROW_JOBS> t, co
     const RowJob J = job_of(t, blockIdx.x, b0);
     const long long r = ((long long)blockIdx.x - b0) * WG + threadIdx.x;
     if (r >= J.rows) return;
-    const int n = J.nid[r];
-    J.info[r] = make_float4(gain[n], softplus_f(theta[n]), __int_as_float(J.drow ? J.drow[r] : -1), 0.f);
+    const int row = J.seg ? J.seg[r].x : (int)r;
+    const int n = J.nid[row];
+    J.info[r] = make_float4(gain[n], softplus_f(theta[n]), __int_as_float(J.drow ? J.drow[row] : -1), 0.f);
 }
 
 // a state tensor (tiled) -> [rows][B] (tests and diagnostics)
