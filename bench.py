@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096]
                     [--no-cpu] [--no-floor] [--latency-calls 200] [--trainer-steps 60] [--bf16-steps 10]
-                    [--connectome-steps 10]
+                    [--connectome-steps 10] [--hophip-steps 5]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -25,6 +25,8 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
            Erdos-Renyi control;
   whole_connectome_b1024: forward and teaching step at B = 1024 on a graph of the whole connectome's size (166,700
            neurons, 15.3M connections) indexed by FlyActor, with roofline fractions on the pruned hops' bytes;
+  hophip_b4096: the HopCuda-style path at B = 4096: FlyActor's forward and a teaching step through PyTorch autograd
+           and torch.optim.Adam, its hop products on the fh_* kernels (float32 and binary16 states);
   trainer: samples / s of the teaching trainer's own loop (flyguy_amd/flyguy_train, run as a child process on
            synthetic binary16 FLYD chunks of the same network: draw, gather, step, as its log reports them) at
            B = 4096, at the reference trainer's default B = 512, and with --bf16 1 at B = 16384.
@@ -391,6 +393,55 @@ def connectome_leg(steps: int, warmup: int, B: int = 1024) -> dict:
     return res
 
 
+def hophip_leg(s, params, steps: int, warmup: int, B: int = 4096) -> dict:
+    """The HopCuda-style path (fly_cuda.py's, fly.py:170-185): FlyActor's own forward with its hop products on the
+    fh_* kernels (HopHip, states [rows][B], PyTorch autograd between the hops), KL against teacher logits, backward
+    and PyTorch's Adam, on the benchmark network at B = 4096; binary16 states too (kernel "cuda16")."""
+    import torch
+    from flyguy_amd.fly import FlyActor
+
+    dev = torch.device("cuda:0")
+    f = FlyActor.from_structure(s, params).to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    obs = torch.randn(B, s["obs_dim"], device=dev, generator=g)
+    teacher = torch.randn(B, s["n_act"], device=dev, generator=g) * 2.0
+    pt = torch.softmax(teacher, 1)
+    opt = torch.optim.Adam(f.parameters(), lr=1e-4)
+
+    def teach():
+        lp = torch.log_softmax(f(obs), 1)
+        loss = (pt * (torch.log(pt) - lp)).sum(1).mean()
+        opt.zero_grad(set_to_none=False)
+        loss.backward()
+        opt.step()
+
+    def decide():
+        with torch.no_grad():
+            f(obs)
+
+    res = {"batch": B, "workload": "FlyActor forward / teaching step (KL, autograd backward, torch.optim.Adam) with "
+                                   "its hop products on HopHip (float32: fh_to_tiled copies into fh_spmm_tiled / fh_spmm_bwd_tiled; "
+                                   "binary16 states: fh_spmm_h / fh_spmm_bwd_h), states [rows][B]"}
+    for kernel in ("hip", "cuda16"):
+        f.kernel = kernel
+        out = {}
+        for what, fn in (("forward", decide), ("train", teach)):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                fn()
+            torch.cuda.synchronize()
+            t = (time.perf_counter() - t0) / steps
+            out[what] = {"value": round(B / t, 1), "unit": "decisions/s" if what == "forward" else "samples/s",
+                         "ms_per_step": round(1e3 * t, 4)}
+        res["fp32" if kernel == "hip" else "binary16_states"] = out
+        print(f"# HopHip path B={B} kernel {kernel}: forward {out['forward']['ms_per_step']:.3f} ms, train "
+              f"{out['train']['ms_per_step']:.3f} ms", file=sys.stderr, flush=True)
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -404,6 +455,8 @@ def main() -> int:
     ap.add_argument("--bf16-steps", type=int, default=10, help="timed bfloat16 B=16384 batches and steps (0: skip)")
     ap.add_argument("--latency-calls", type=int, default=200,
                     help="synchronised one-tile forwards timed for a single decision's latency (the first 20 untimed; 0: skip)")
+    ap.add_argument("--hophip-steps", type=int, default=5,
+                    help="timed steps of the HopCuda-style path (FlyActor over HopHip) at B=4096 (0: skip)")
     ap.add_argument("--connectome-steps", type=int, default=10,
                     help="timed whole-connectome B=1024 batches and steps (0: skip; its index build takes ~20 s)")
     ap.add_argument("--no-floor", action="store_true",
@@ -587,6 +640,7 @@ def main() -> int:
         bf16["workload"] = ("bfloat16 states (x, drive, every layer's h, gathered gz), float32 sums, gradients and "
                                "Adam; B=16384; the synthetic network (lognormal in-degree) and its Erdos-Renyi control")
     connectome = connectome_leg(args.connectome_steps, W) if args.connectome_steps > 0 else None
+    hophip = hophip_leg(s, params, args.hophip_steps, W) if args.hophip_steps > 0 else None
     trainer = None
     if args.trainer_steps > 0:
         trainer = trainer_leg(s, params, ((4096, False), (512, False), (16384, True)), args.trainer_steps)
@@ -632,6 +686,7 @@ def main() -> int:
         "trainer": trainer,
         "bf16_b16384": bf16,
         "whole_connectome_b1024": connectome,
+        "hophip_b4096": hophip,
         "stages_ms": {"forward": {k: round(v[0] / v[1], 4) for k, v in prof_fwd.items()},
                       "train": {k: round(v[0] / v[1], 4) for k, v in prof_train.items()}},
     }

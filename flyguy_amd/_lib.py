@@ -39,6 +39,10 @@ _SIGS = {
     "fh_spmm_static": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp]),
     "fh_spmm_bwd": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp, vp]),
     "fh_to_half": (None, [vp, ci, ci, vp, vp, vp]),
+    "fh_to_tiled": (None, [vp, ci, ci, vp, vp]),
+    "fh_spmm_tiled": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp, vp, vp]),
+    "fh_spmm_bwd_tiled": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp,
+                                 vp]),
     "fh_absmax": (None, [vp, cll, vp, vp]),
     "fh_spmm_h": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp, vp, vp]),
     "fh_spmm_bwd_h": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp,

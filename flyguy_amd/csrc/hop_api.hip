@@ -51,16 +51,56 @@ bool spmm_args_ok(const int* wave, int nwave, const int* seg, int nseg, const in
              (nsplit > 0 && !split));
 }
 
-// pack the pairs into cw, then the product through the plan (split rows' partial sums in `partials`)
+// pack the pairs into cw, then the product through the plan (split rows' partial sums in `partials`); h row-major
+// [n_src][B], or tiled [B/32][n_src][32] (h_tiled)
 void spmm_run(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
               const int* pcol, const int* pidx, long long npos, const float* w, const float* h, float* out, int n_rows,
-              int n_src, int B, int2* cw, float* partials, hipStream_t st) {
+              int n_src, int B, int2* cw, float* partials, hipStream_t st, bool h_tiled = false) {
     FG_CHECK(launch_pack(pcol, pidx, w, cw, npos, st), );
     FwdEpi e;
     e.z = out;
     e.lz = plain(B);
     Plan p{(const int2*)wave, nwave, (const int4*)seg, nseg, (const int4*)split, nsplit, n_rows, nslot, npos};
-    FG_CHECK(launch_fwd(p, cw, h, plain(B), n_src, e, partials, tiled(nslot), B / TW, st), );
+    FG_CHECK(launch_fwd(p, cw, h, h_tiled ? tiled(n_src) : plain(B), n_src, e, partials, tiled(nslot), B / TW, st), );
+}
+
+bool spmm_bwd_args_ok(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                      const int* pcol, const int* pidx, long long npos, const float* w, const float* gz, const float* h,
+                      const float* gh, const float* gw, int n_rows, int n_src, int B, const void* cw,
+                      const float* gwpart, const float* scratch) {
+    return !(B <= 0 || B % TW || n_rows <= 0 || n_src <= 0 || nwave < 0 || nseg < 0 || nseg > 8LL * nwave ||
+             npos < 0 || nslot < 0 || !w || !gz || !h || !gh ||
+             (nwave > 0 && (!wave || !seg || !pcol || !pidx || !cw)) || (gw && !gwpart) ||
+             (nsplit > 0 && (!split || !scratch)));
+}
+
+// the backward through the transposed plan: gz row-major [n_rows][B] or tiled (gz_tiled); h and gh row-major
+void spmm_bwd_run(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                  const int* pcol, const int* pidx, long long npos, const float* w, const float* gz, const float* h,
+                  float* gh, float* gw, int n_rows, int n_src, int B, int2* cw, float* gwpart, float* scratch,
+                  hipStream_t st, bool gz_tiled) {
+    const int T = B / TW;
+    FG_CHECK(launch_pack(pcol, pidx, w, cw, npos, st), );
+    BwdEpi e;
+    e.mode = 0;
+    e.gh_out = gh;
+    e.lgh = plain(B);
+    Plan p{(const int2*)wave, nwave, (const int4*)seg, nseg, (const int4*)split, nsplit, n_src, nslot, npos};
+    FG_CHECK(launch_bwd(p, cw, gz, gz_tiled ? tiled(n_rows) : plain(B), n_rows, h, plain(B), gw ? gwpart : nullptr,
+                        npos, e, scratch, tiled(nslot), T, st), );
+    if (gw) FG_CHECK(launch_reduce(gwpart, npos, npos, T, pidx, nullptr, gw, st), );
+}
+
+// one 8-lane group per (tile, row): a row's 128-byte line of the tile, row-major -> tiled
+__global__ __launch_bounds__(WG) void k_to_tiled(const float* __restrict__ x, int rows, int B, float* __restrict__ out,
+                                                 long long n) {
+    const long long i = (long long)blockIdx.x * WG + threadIdx.x;
+    if (i >= n) return;
+    const int sub = (int)(i & 7);
+    const long long rt = i >> 3;                    // tile * rows + row: the tiled layout's line, written in order
+    const int row = (int)(rt % rows), tile = (int)(rt / rows);
+    const float4 v = reinterpret_cast<const float4*>(x + (size_t)row * B + (size_t)tile * TW)[sub];
+    reinterpret_cast<float4*>(out + (size_t)rt * TW)[sub] = v;
 }
 
 }  // namespace
@@ -108,23 +148,53 @@ void fh_spmm_bwd(const int* wave, int nwave, const int* seg, int nseg, const int
                  float* gh, float* gw, int n_rows, int n_src, int B, void* cw, float* gwpart, float* scratch,
                  void* stream) {
     clear_error();
-    if (B <= 0 || B % TW || n_rows <= 0 || n_src <= 0 || nwave < 0 || nseg < 0 || nseg > 8LL * nwave || npos < 0 ||
-        nslot < 0 || !w || !gz || !h || !gh || (nwave > 0 && (!wave || !seg || !pcol || !pidx || !cw)) ||
-        (gw && !gwpart) || (nsplit > 0 && (!split || !scratch))) {
+    if (!spmm_bwd_args_ok(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, gz, h, gh, gw, n_rows,
+                          n_src, B, cw, gwpart, scratch)) {
         set_error("fh_spmm_bwd: bad argument");
         return;
     }
-    hipStream_t st = (hipStream_t)stream;
-    const int T = B / TW;
-    FG_CHECK(launch_pack(pcol, pidx, w, (int2*)cw, npos, st), );
-    BwdEpi e;
-    e.mode = 0;
-    e.gh_out = gh;
-    e.lgh = plain(B);
-    Plan p{(const int2*)wave, nwave, (const int4*)seg, nseg, (const int4*)split, nsplit, n_src, nslot, npos};
-    FG_CHECK(launch_bwd(p, (const int2*)cw, gz, plain(B), n_rows, h, plain(B), gw ? gwpart : nullptr, npos, e, scratch,
-                        tiled(nslot), T, st), );
-    if (gw) FG_CHECK(launch_reduce(gwpart, npos, npos, T, pidx, nullptr, gw, st), );
+    spmm_bwd_run(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, gz, h, gh, gw, n_rows, n_src, B,
+                 (int2*)cw, gwpart, scratch, (hipStream_t)stream, false);
+}
+
+void fh_to_tiled(const float* x, int rows, int B, float* out, void* stream) {
+    clear_error();
+    if (!x || !out || rows < 0 || B <= 0 || B % TW) {
+        set_error("fh_to_tiled: bad argument");
+        return;
+    }
+    const long long n = (long long)rows * B / 4;    // 8 lanes per 32-sample line
+    if (n == 0) return;
+    k_to_tiled<<<(unsigned)((n + WG - 1) / WG), WG, 0, (hipStream_t)stream>>>(x, rows, B, out, n);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) set_error(std::string("fh_to_tiled: ") + hipGetErrorString(e));
+}
+
+void fh_spmm_tiled(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                   const int* pcol, const int* pidx, long long npos, const float* w, const float* ht, float* out,
+                   int n_rows, int n_src, int B, void* cw, float* scratch, void* stream) {
+    clear_error();
+    if (!spmm_args_ok(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, ht, out, n_rows, n_src, B) ||
+        (nwave > 0 && !cw) || (nsplit > 0 && !scratch)) {
+        set_error("fh_spmm_tiled: bad argument");
+        return;
+    }
+    spmm_run(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, ht, out, n_rows, n_src, B, (int2*)cw,
+             scratch, (hipStream_t)stream, true);
+}
+
+void fh_spmm_bwd_tiled(const int* wave, int nwave, const int* seg, int nseg, const int* split, int nsplit, int nslot,
+                       const int* pcol, const int* pidx, long long npos, const float* w, const float* gzt, const float* h,
+                       float* gh, float* gw, int n_rows, int n_src, int B, void* cw, float* gwpart, float* scratch,
+                       void* stream) {
+    clear_error();
+    if (!spmm_bwd_args_ok(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, gzt, h, gh, gw, n_rows,
+                          n_src, B, cw, gwpart, scratch)) {
+        set_error("fh_spmm_bwd_tiled: bad argument");
+        return;
+    }
+    spmm_bwd_run(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, gzt, h, gh, gw, n_rows, n_src, B,
+                 (int2*)cw, gwpart, scratch, (hipStream_t)stream, true);
 }
 
 }  // extern "C"

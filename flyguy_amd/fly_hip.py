@@ -3,7 +3,8 @@
 z[target, b] = sum over connections (source -> target) of w * h[source, b]; states are [neurons, batch] with the
 batch contiguous and a multiple of 32.  crow / col: the connections by target (CSR, int64 / int32); tcrow / tcol /
 tperm: the same by source.  The backward is one pass over the transposed form that gives both the state gradient
-and the per-connection gradient (fh_spmm_bwd).
+and the per-connection gradient (fh_spmm_bwd).  In float32 the products gather from copies of h (forward) and of the
+output gradient (backward) in the tiled layout [B/32][rows][32] (fh_to_tiled, fh_spmm_tiled, fh_spmm_bwd_tiled).
 
 half=True reads the states as IEEE binary16 (rounded to nearest even) and the backward reads the output gradient as
 binary16 after dividing it by its largest magnitude (fly_cuda.py:93, 100-114); all sums stay float32.  The
@@ -119,9 +120,12 @@ class HopHip(torch.autograd.Function):
                  scratch.data_ptr(), _stream(h))
             ctx.hs = hs
         else:
+            # the product gathers from a tiled copy of h: half the time of gathers from the row-major h
+            ht = torch.empty(max(n_src * B, 1), device=h.device)
+            call("fh_to_tiled", h.data_ptr(), n_src, B, ht.data_ptr(), _stream(h))
             scratch = torch.empty(max(d["nslot"] * B, 1), device=h.device)
-            call("fh_spmm", *_args(d), w.data_ptr(), h.data_ptr(), out.data_ptr(), n_rows, n_src, B, cw.data_ptr(),
-                 scratch.data_ptr(), _stream(h))
+            call("fh_spmm_tiled", *_args(d), w.data_ptr(), ht.data_ptr(), out.data_ptr(), n_rows, n_src, B,
+                 cw.data_ptr(), scratch.data_ptr(), _stream(h))
             ctx.hs = None
         ctx.save_for_backward(w, h, tcrow, tcol, tperm)
         ctx.n_rows, ctx.half = n_rows, half
@@ -154,9 +158,11 @@ class HopHip(torch.autograd.Function):
                  gh.data_ptr(), gw.data_ptr() if gw is not None else None, ctx.n_rows, n_src, B, cw.data_ptr(),
                  gwpart.data_ptr() if gwpart is not None else None, scratch.data_ptr(), _stream(gz))
         else:
+            gzt = torch.empty(max(ctx.n_rows * B, 1), device=h.device)       # gathered tiled, as in the forward
+            call("fh_to_tiled", gz.data_ptr(), ctx.n_rows, B, gzt.data_ptr(), _stream(gz))
             gwpart = torch.empty(max(d["npos"] * (B // 32), 1), device=h.device) if gw is not None else None
             scratch = torch.empty(max(d["nslot"] * B, 1), device=h.device)
-            call("fh_spmm_bwd", *_args(d), w.data_ptr(), gz.data_ptr(), h.data_ptr(), gh.data_ptr(),
+            call("fh_spmm_bwd_tiled", *_args(d), w.data_ptr(), gzt.data_ptr(), h.data_ptr(), gh.data_ptr(),
                  gw.data_ptr() if gw is not None else None, ctx.n_rows, n_src, B, cw.data_ptr(),
                  gwpart.data_ptr() if gwpart is not None else None, scratch.data_ptr(), _stream(gz))
         return gw, (gh if ctx.needs_input_grad[1] else None), None, None, None, None, None, None

@@ -74,3 +74,54 @@ def test_random_product_half(gpu_lib, seed):
     _half_case(a, torch.as_tensor(r), torch.as_tensor(col.astype(np.int64)), w32, n_src, n_rows, B,
                torch.as_tensor(crow), torch.as_tensor(col), torch.as_tensor(tcrow), torch.as_tensor(tcol),
                torch.as_tensor(tperm), seed)
+
+
+@pytest.mark.parametrize("seed", range(18, 24))
+def test_row_major_and_tiled_entry_points_agree(gpu_lib, seed):
+    """fh_spmm / fh_spmm_bwd on row-major states and fh_spmm_tiled / fh_spmm_bwd_tiled on fh_to_tiled copies sum the
+    same terms in the same order: identical outputs and gradients.  fh_to_tiled against torch's own reshape."""
+    from flyguy_amd._lib import call
+    from flyguy_amd.fly_hip import _args, _plan
+    n_rows, n_src, B, crow, col, r, tcrow, tcol, tperm, w, rng = random_product(seed)
+    say(f"row-major vs tiled {seed}: {n_rows} rows x {n_src} sources, {len(col)} connections, B {B}")
+    dev, st = "cuda", torch.cuda.current_stream().cuda_stream
+    E, T = len(col), B // 32
+    wd = torch.zeros(max(E, 1), device=dev)                     # a real address also without connections
+    wd[:E] = torch.as_tensor(w.astype(np.float32)).to(dev)
+    h = torch.as_tensor(rng.random((n_src, B), np.float32)).to(dev)
+    gz = torch.as_tensor(rng.standard_normal((n_rows, B), np.float32)).to(dev)
+
+    def tiled(x):
+        out = torch.full((x.shape[0] * B,), float("nan"), device=dev)
+        call("fh_to_tiled", x.data_ptr(), x.shape[0], B, out.data_ptr(), st)
+        return out
+
+    ht, gzt = tiled(h), tiled(gz)
+    assert torch.equal(ht.view(T, n_src, 32), h.view(n_src, T, 32).transpose(0, 1))
+    assert torch.equal(gzt.view(T, n_rows, 32), gz.view(n_rows, T, 32).transpose(0, 1))
+
+    d = _plan(torch.as_tensor(crow).to(dev), torch.as_tensor(col).to(dev), None, E)
+    cw = torch.empty(max(d["npos"], 1), 2, dtype=torch.int32, device=dev)
+    part = torch.empty(max(d["nslot"] * B, 1), device=dev)
+    outs = []
+    for name, src in (("fh_spmm", h), ("fh_spmm_tiled", ht)):
+        out = torch.full((n_rows, B), float("nan"), device=dev)
+        call(name, *_args(d), wd.data_ptr(), src.data_ptr(), out.data_ptr(), n_rows, n_src, B, cw.data_ptr(),
+             part.data_ptr(), st)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+
+    d = _plan(torch.as_tensor(tcrow).to(dev), torch.as_tensor(tcol).to(dev), torch.as_tensor(tperm).to(dev), E)
+    cw = torch.empty(max(d["npos"], 1), 2, dtype=torch.int32, device=dev)
+    part = torch.empty(max(d["nslot"] * B, 1), device=dev)
+    gwpart = torch.empty(max(d["npos"] * T, 1), device=dev)
+    grads = []
+    for name, g in (("fh_spmm_bwd", gz), ("fh_spmm_bwd_tiled", gzt)):
+        gh = torch.full((n_src, B), float("nan"), device=dev)
+        gw = torch.zeros(max(E, 1), device=dev)
+        call(name, *_args(d), wd.data_ptr(), g.data_ptr(), h.data_ptr(), gh.data_ptr(), gw.data_ptr(), n_rows, n_src,
+             B, cw.data_ptr(), gwpart.data_ptr(), part.data_ptr(), st)
+        grads.append((gh, gw))
+    torch.cuda.synchronize()
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    assert not torch.isnan(outs[0]).any() and not torch.isnan(grads[0][0]).any()
