@@ -37,6 +37,7 @@ struct HopD {
     float *h = nullptr, *ggp = nullptr, *gsp = nullptr;
     float4* info = nullptr;          // per row {gain, softplus(theta), re-drive row}, from the current weights
     float4* sinfo = nullptr;         // the same per segment of the forward plan fp (a wave's 8 in one line)
+    float4* bsinfo = nullptr;        // the layer below's records per segment of the transposed plan bp
     float* zk = nullptr;             // the pre-activation, kept only by survey passes (allocated on first use)
     std::vector<int> h_nid, h_crow, h_col, h_widx;   // host copies of the index arrays (the revive surgery)
 };

@@ -453,7 +453,8 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         d.gsp = dalloc<float>(*c, Tp * gc);
         d.info = dalloc<float4>(*c, d.rows);
         d.sinfo = dalloc<float4>(*c, d.fp.nseg);
-        if (!d.h || !d.ggp || !d.gsp || !d.info || !d.sinfo) return nullptr;
+        d.bsinfo = dalloc<float4>(*c, d.bp.nseg);
+        if (!d.h || !d.ggp || !d.gsp || !d.info || !d.sinfo || !d.bsinfo) return nullptr;
     }
     c->info0 = dalloc<float4>(*c, c->n_s);
     c->sinfo0 = dalloc<float4>(*c, c->pp.nseg);
@@ -505,9 +506,12 @@ static hipError_t rowinfo(Core& c, const float* gain, const float* theta) {
     std::vector<RowJob> j;
     j.push_back({c.n0, nullptr, c.info0, c.n_s});
     j.push_back({c.n0, nullptr, c.sinfo0, c.pp.nseg, c.pp.seg});
-    for (auto& d : c.hop) {
+    for (size_t k = 0; k < c.hop.size(); ++k) {
+        HopD& d = c.hop[k];
         j.push_back({d.nid, d.has_drive ? d.drow : nullptr, d.info, d.rows});
         j.push_back({d.nid, d.has_drive ? d.drow : nullptr, d.sinfo, d.fp.nseg, d.fp.seg});
+        // the backward of hop k + 1 finishes the rows of the layer below (its transposed plan's rows)
+        j.push_back({k ? c.hop[k - 1].nid : c.n0, nullptr, d.bsinfo, d.bp.nseg, d.bp.seg});
     }
     hipError_t e = hipSuccess;
     for (size_t k = 0; k < j.size() && e == hipSuccess; k += ROW_JOBS)
@@ -687,6 +691,7 @@ bool backward(Core& c, const float* dlogits, int B, bool fresh) {
             hbelow = c.h0; rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
         }
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = d.gcols;
+        e.sinfo = d.bsinfo;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
             FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart,
@@ -837,6 +842,7 @@ static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
             rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
         }
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = d.gcols;
+        e.sinfo = d.bsinfo;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
             FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, c.gwpart, d.bp.npos, e, c.part, T, st,

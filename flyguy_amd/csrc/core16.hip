@@ -219,8 +219,9 @@ __device__ __forceinline__ float dot8(const u32x4& a, const u32x4& b) {
 // MODE 1: a hop layer (d: the row's re-drive row); 2: the sensory layer
 // (hr: the row's h line, already loaded by the caller)
 template <int MODE>
+// recs: the wave's 8 records in plan order (sinfo + 8 w; the row's is recs[i]), or null: the row's from info
 __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, int tile, int sub, BwdIn16& in,
-                                             const u32x4* hr = nullptr) {
+                                             const u32x4* hr = nullptr, const float4* recs = nullptr, int i = 0) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) in.z[k] = in.gd[k] = 0.f;
     bool load;                               // (re-drive fields as in BwdEpi)
@@ -234,7 +235,7 @@ __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, in
     if (load) ldf8(f8p(e.gdrive, e.n_s, tile, in.d, sub), in.gd);
     in.hr = hr ? *hr : ldr8(e.h, e.rows, tile, j, sub);
     if constexpr (MODE == 2) ld8(e.z, e.rows, tile, j, sub, in.z);
-    const float4 r = e.info[j];
+    const float2 r = *reinterpret_cast<const float2*>(recs ? recs + i : e.info + j);
     in.gn = r.x;
     in.sp = r.y;
 }
@@ -364,7 +365,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
         return;
     }
     BwdIn16 in{};                               // the row's other inputs, after the loop (k_bwd)
-    bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in, &hj);
+    bwd_inputs16<MODE>(epi, sg.x, sg.z, tile, sub, in, &hj, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7);
     bwd_finish16<MODE>(epi, sg.x, tile, sub, acc, in, nullptr, w * 8 + (grp & 7));
 }
 
@@ -439,8 +440,9 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
         return;
     }
     BwdIn16 ina{}, inb{};                       // the rows' other inputs, after the loop (k_bwd)
-    bwd_inputs16<MODE>(epi, sg.x, sg.z, ta, sub, ina, &hja);
-    if (hasb) bwd_inputs16<MODE>(epi, sg.x, sg.z, tb, sub, inb, &hjb);
+    const float4* recs = epi.sinfo ? epi.sinfo + 8 * w : nullptr;
+    bwd_inputs16<MODE>(epi, sg.x, sg.z, ta, sub, ina, &hja, recs, grp & 7);
+    if (hasb) bwd_inputs16<MODE>(epi, sg.x, sg.z, tb, sub, inb, &hjb, recs, grp & 7);
     float2 ka, kb = make_float2(0.f, 0.f);
     bwd_finish16<MODE>(epi, sg.x, ta, sub, acca, ina, &ka);
     if (hasb) bwd_finish16<MODE>(epi, sg.x, tb, sub, accb, inb, &kb);

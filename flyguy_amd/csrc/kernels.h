@@ -73,6 +73,8 @@ struct BwdEpi {
     const float* z = nullptr;     // the sensory layer's pre-activation (the drive); hop layers do not keep theirs:
     Lay lz{};                     //   where h > 0 it is (h + softplus(theta)) / gain, and elsewhere it is not needed
     const float4* info = nullptr; // per row {gain, softplus(theta), re-drive row}
+    const float4* sinfo = nullptr;// the same per segment of the plan (a wave's 8 in one line): whole rows read these,
+                                  //   split rows read info (k_bwd_combine); null: info throughout
     const int* drow = nullptr;    // per row: the re-drive row (-1: none), for kernels that do not follow a row plan
     float* gz_out = nullptr;      // mode 1
     Lay lgz{};
@@ -185,6 +187,7 @@ struct BwdEpi16 {
     const unsigned short* z = nullptr;       // the sensory layer's drive
     int rows = 0;
     const float4* info = nullptr;
+    const float4* sinfo = nullptr;           // as in BwdEpi
     const int* drow = nullptr;               // per row: re-drive row (read-out kernel only)
     unsigned short* gz_out = nullptr;        // mode 1: the layer's gz, gathered by the next backward
     float* gdrive = nullptr;                 // float32 [T][n_s][64], re-drive fields as in BwdEpi

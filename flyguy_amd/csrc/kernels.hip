@@ -235,8 +235,10 @@ struct BwdIn {
 // MODE (the epilogue's kind, a compile-time constant so that each kernel is straight-line code for its own case):
 // 0 the raw product, 1 a hop layer (d: the row's re-drive row), 2 the sensory layer
 // (the row's h given: a kernel that has loaded it already, from the same layer, hands it over)
+// recs: the wave's 8 records in plan order (sinfo + 8 w; the row's is recs[i]), or null: the row's from info
 template <int MODE>
-__device__ __forceinline__ BwdIn bwd_inputs_h(const BwdEpi& e, int j, int d, int tile, int sub, float4 h) {
+__device__ __forceinline__ BwdIn bwd_inputs_h(const BwdEpi& e, int j, int d, int tile, int sub, float4 h,
+                                              const float4* recs = nullptr, int i = 0) {
     BwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f, -1};
     if constexpr (MODE == 0) return in;
     // the row's drive gradient so far (see BwdEpi): a first write starts from zero; the sensory layer's own is
@@ -252,7 +254,7 @@ __device__ __forceinline__ BwdIn bwd_inputs_h(const BwdEpi& e, int j, int d, int
     if (load) in.gd = *at4u(e.gdrive, e.lgd, tile, in.d, sub);
     in.h = h;
     if constexpr (MODE == 2) in.z = *at4u(e.z, e.lz, tile, j, sub);
-    const float4 r = e.info[j];
+    const float2 r = *reinterpret_cast<const float2*>(recs ? recs + i : e.info + j);
     in.gn = r.x;
     in.sp = r.y;
     return in;
@@ -380,7 +382,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     // the row's other inputs of the neuron backward, after the loop: live across it they would cost registers, and
     // with them waves per SIMD
     BwdIn in{};
-    if (whole) in = bwd_inputs_h<MODE>(epi, sg.x, sg.z, tile, sub, hj);
+    if (whole) in = bwd_inputs_h<MODE>(epi, sg.x, sg.z, tile, sub, hj, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7);
     if (sg.y >= 0) {
         st_stream(at4w(part, lp, tile, sg.y, sub), acc);
         return;
@@ -447,8 +449,9 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
     if (!live) return;
     BwdIn ina{}, inb{};                         // the rows' other inputs, after the loop (k_bwd)
     if (whole) {                                // (hs is the layer's h: the core's launches hand over e.h)
-        ina = bwd_inputs_h<MODE>(epi, sg.x, sg.z, ta, sub, hja);
-        if (hasb) inb = bwd_inputs_h<MODE>(epi, sg.x, sg.z, tb, sub, hjb);
+        const float4* recs = epi.sinfo ? epi.sinfo + 8 * w : nullptr;
+        ina = bwd_inputs_h<MODE>(epi, sg.x, sg.z, ta, sub, hja, recs, grp & 7);
+        if (hasb) inb = bwd_inputs_h<MODE>(epi, sg.x, sg.z, tb, sub, hjb, recs, grp & 7);
     }
     if (sg.y >= 0) {
         st_stream(at4w(part, lp, ta, sg.y, sub), acca);
