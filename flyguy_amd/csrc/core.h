@@ -98,6 +98,7 @@ struct Core {
     // those of rows whose own output is zero on the tile.  skip_silent false (FLYGUY_SKIP_SILENT=0): neither (the
     // results are the same).
     bool skip_silent = true;
+    int plug_lds = -1;               // the plug staged in LDS: -1 by batch size, 0 never, S > 0 with S workgroups per tile
     // What the derived tables were made from.  wver[set] counts the writes to the weights (set 0) and to the running
     // average (set 1): fc_copy into the handle, an Adam step, the trainer's host-side edits.  A table made from a
     // set at its current version is not made again: the forward's packed pairs and per-row records (from one set),

@@ -460,6 +460,7 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     c->sinfo0 = dalloc<float4>(*c, c->pp.nseg);
     if (!c->info0 || !c->sinfo0) return nullptr;
     if (const char* f = std::getenv("FLYGUY_SKIP_SILENT")) c->skip_silent = f[0] != '0';
+    if (const char* f = std::getenv("FLYGUY_PLUG_LDS")) c->plug_lds = std::min(std::max(std::atoi(f), 0), 64);
     for (int l = 0; l < K; ++l) {                   // (the top layer's would have no reader)
         c->fire_bytes.push_back(dalloc<unsigned char>(*c, Tp * (size_t)fires_bytes_ld(c->sizes[l])));
         c->fire_bits.push_back(dalloc<unsigned>(*c, Tp * (size_t)fires_ld(c->sizes[l])));
@@ -502,10 +503,10 @@ bool check_batch(const Core* c, int B) {
 
 // ------------------------------------------------------------------------------------------------ passes
 // the per-row neuron records of every layer from this set's gain and theta
-static hipError_t rowinfo(Core& c, const float* gain, const float* theta) {
+static hipError_t rowinfo(Core& c, const float* gain, const float* theta, const float* bias) {
     std::vector<RowJob> j;
-    j.push_back({c.n0, nullptr, c.info0, c.n_s});
-    j.push_back({c.n0, nullptr, c.sinfo0, c.pp.nseg, c.pp.seg});
+    j.push_back({c.n0, nullptr, c.info0, c.n_s, nullptr, bias});          // (the plug's rows carry their bias)
+    j.push_back({c.n0, nullptr, c.sinfo0, c.pp.nseg, c.pp.seg, bias});
     for (size_t k = 0; k < c.hop.size(); ++k) {
         HopD& d = c.hop[k];
         j.push_back({d.nid, d.has_drive ? d.drow : nullptr, d.info, d.rows});
@@ -542,7 +543,7 @@ static hipError_t derive_forward(Core& c, int set, bool bf16w, const float* gain
         c.made_fpairs = {set, c.wver[set]};
     }
     if (!c.made_info.same(set, c.wver[set])) {
-        const hipError_t e = rowinfo(c, gain, theta);
+        const hipError_t e = rowinfo(c, gain, theta, c.arr(set, 4));
         if (e != hipSuccess) return e;
         c.made_info = {set, c.wver[set]};
     }
@@ -556,7 +557,7 @@ static hipError_t derive_backward(Core& c, bool bf16w, const float* gain, const 
         c.made_tpairs = {SET_P, c.wver[SET_P]};
     }
     if (!c.made_info.same(SET_P, c.wver[SET_P])) {
-        const hipError_t e = rowinfo(c, gain, theta);
+        const hipError_t e = rowinfo(c, gain, theta, c.arr(SET_P, 4));
         if (e != hipSuccess) return e;
         c.made_info = {SET_P, c.wver[SET_P]};
     }
@@ -565,6 +566,17 @@ static hipError_t derive_backward(Core& c, bool bf16w, const float* gain, const 
 
 static bool forward16(Core& c, const float* obs, int B, float* logits, int set);
 static bool backward16(Core& c, const float* dlogits, int B, bool fresh);
+
+// Workgroups per tile of the plug staged in LDS (launch_fwd_lds), or 0 for launch_fwd.  The staging pays when the
+// workgroups have plan waves enough to walk after copying the slab: at 64 tiles or more (B >= 2048), about 2048
+// workgroups in all (measured at B=4096 on the benchmark network, plug 0.191 ms through launch_fwd: 4 / 8 / 12 /
+// 16 / 32 / 64 workgroups per tile 0.202 / 0.153 / 0.153 / 0.154 / 0.164 / 0.179 ms).  FLYGUY_PLUG_LDS=0 turns it
+// off, =S forces S workgroups per tile.
+static int plug_split(const Core& c, int T) {
+    if ((size_t)c.obs_dim * TW * 4 > FWD_LDS_BYTES || c.plug_lds == 0) return 0;
+    if (c.plug_lds > 0) return c.plug_lds;
+    return T >= 64 ? std::max(1, 2048 / T) : 0;
+}
 
 bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     if (c.prec) return forward16(c, obs, B, logits, set);
@@ -588,7 +600,11 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     e0.fires = bytes(0);
     {
         Timed t(c, ST_PLUG);
-        FG_CHECK(launch_fwd(c.pp.view(), c.in_cw, c.x, tiled(c.obs_dim), c.obs_dim, e0, c.part, tiled(c.pp.nslot), T, st), false);
+        if (const int S = plug_split(c, T))
+            FG_CHECK(launch_fwd_lds(c.pp.view(), c.in_cw, c.x, c.obs_dim, e0, c.part, tiled(c.pp.nslot), T, S, st), false);
+        else
+            FG_CHECK(launch_fwd(c.pp.view(), c.in_cw, c.x, tiled(c.obs_dim), c.obs_dim, e0, c.part, tiled(c.pp.nslot), T, st),
+                     false);
         if (c.skip_silent) FG_CHECK(launch_fires_pack(bytes(0), c.n_s, bits(0), T, st), false);
     }
     const float* hp = c.h0;
@@ -736,7 +752,10 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     e0.fires = bytes(0);
     {
         Timed t(c, ST_PLUG);
-        FG_CHECK(launch_fwd16c(c.pp.view(), c.in_cw, s16(c.x), c.obs_dim, e0, c.part, T, st), false);
+        if (const int S = plug_split(c, T))
+            FG_CHECK(launch_fwd16c_lds(c.pp.view(), c.in_cw, s16(c.x), c.obs_dim, e0, c.part, T, S, st), false);
+        else
+            FG_CHECK(launch_fwd16c(c.pp.view(), c.in_cw, s16(c.x), c.obs_dim, e0, c.part, T, st), false);
         if (c.skip_silent) FG_CHECK(launch_fires_pack(bytes(0), c.n_s, bits(0), T, st), false);
     }
     const u16* hp = s16(c.h0);

@@ -59,19 +59,20 @@ __device__ __forceinline__ void fma_pair(float wa, float wb, const u32x4& ga, co
 // ------------------------------------------------------------------------------------------------ forward
 struct FwdIn16 {
     float dv[8];
-    float g, sp;
+    float g, sp, b;                             // b: the row's bias (the plug's records carry it)
 };
 // recs[i]: the row's record (as fwd_inputs)
 __device__ __forceinline__ void fwd_inputs16(const FwdEpi16& e, const float4* recs, int i, int d, int tile, int sub,
                                              FwdIn16& in) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) in.dv[k] = 0.f;
-    in.g = in.sp = 0.f;
+    in.g = in.sp = in.b = 0.f;
     if (e.drive && d >= 0) ld8(e.drive, e.n_s, tile, d, sub, in.dv);
     if (recs) {
         const float4 r = recs[i];
         in.g = r.x;
         in.sp = r.y;
+        in.b = r.w;
     }
 }
 __device__ __forceinline__ void fwd_finish16(const FwdEpi16& e, int t, int tile, int sub, float (&acc)[8], const FwdIn16& in) {
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
         if (j == 0 && whole) {                 // the row's own inputs after the first gathers; the bias starts the sum
             fwd_inputs16(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub, in);
             if (epi.bias) {
-                const float b = epi.bias[sg.x];
+                const float b = epi.sinfo ? in.b : epi.bias[sg.x];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) acc[k] = b;
             }
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
     if (whole && !(wok && wv.y > 0)) {          // a wave without edges
         fwd_inputs16(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub, in);
         if (epi.bias) {
-            const float b = epi.bias[sg.x];
+            const float b = epi.sinfo ? in.b : epi.bias[sg.x];
 #pragma unroll
             for (int k = 0; k < 8; ++k) acc[k] = b;
         }
@@ -155,6 +156,79 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
     fwd_finish16(epi, sg.x, tile, sub, acc, in);
 }
 
+
+// The plug with the tile's observation slab (src_rows lines of 64 bfloat16 samples) staged in LDS, as k_fwd_lds:
+// the same sums as k_cfwd16, plan waves walked by each wave with the next one's loads requested before the
+// previous one's stores.  No re-drive rows.
+__global__ __launch_bounds__(FWD_LDS_NW * 64) void k_cfwd16_lds(Plan p, const int2* __restrict__ cw,
+                                                               const bf16_t* __restrict__ src, int src_rows,
+                                                               FwdEpi16 epi, float* __restrict__ part, int T, int S) {
+    __shared__ __align__(16) int2 slots[FWD_LDS_NW * 64 / LPR][LPR];
+    extern __shared__ __align__(16) u32x4 xs16[];         // the tile's slab, src_rows x 8 (16 bytes each)
+    int s;
+    const int tile = tile_of(blockIdx.x, S, T, s);
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63, gi = grp & 7;
+    const int w0 = __builtin_amdgcn_readfirstlane(s * FWD_LDS_NW + (int)(threadIdx.x >> 6)), dw = S * FWD_LDS_NW;
+    const int n = w0 < p.nwave ? (p.nwave - 1 - w0) / dw + 1 : 0;
+    const int2 wrec = lane < n ? p.wave[w0 + lane * dw] : make_int2(0, 0);
+    const u32x4* g = reinterpret_cast<const u32x4*>(src + (size_t)tile * src_rows * TW16);
+    for (int i = threadIdx.x; i < src_rows * 8; i += FWD_LDS_NW * 64) xs16[i] = g[i];
+    __syncthreads();
+    struct It {
+        int w;
+        int2 wv, pr;
+        int4 sg;
+        float4 rec;
+        bool wok, live;
+    };
+    auto plan_of = [&](int k, It& it) {         // (k_fwd_lds)
+        it.w = w0 + k * dw;
+        const int2 v = make_int2(__builtin_amdgcn_readlane(wrec.x, k), __builtin_amdgcn_readlane(wrec.y, k));
+        it.wok = v.x >= 0 && v.y >= 0 && (long long)v.x + 64 * (((long long)v.y + 7) / 8) <= p.npos;
+        it.wv = it.wok ? v : make_int2(0, 0);
+        it.pr = (it.wok && it.wv.y > 0) ? cw[it.wv.x + lane] : make_int2(NO_ROW, 0);
+        it.live = load_segment(p, it.w * 8 + gi, it.sg) && it.wok;
+        it.rec = epi.sinfo && it.w * 8 + gi < p.nseg ? epi.sinfo[it.w * 8 + gi] : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    It cur, nx;
+    if (n > 0) plan_of(0, cur);
+    for (int k = 0; k < n; ++k) {
+        const bool whole = cur.live && cur.sg.y < 0;
+        const float b = whole && epi.bias ? (epi.sinfo ? cur.rec.w : epi.bias[cur.sg.x]) : 0.f;
+        float acc[8] = {b, b, b, b, b, b, b, b};            // (the bias starts the sum)
+        const int2* q = cw + cur.wv.x + lane;
+        int2 nxt = cur.pr;
+        for (int j = 0, left = cur.wok ? cur.wv.y : 0; left > 0; ++j, left -= 8) {
+            int c[8];
+            float wt[8];
+            stage8(slots[grp], sub, nxt, c, wt);
+            if (left > 8) nxt = q[64 * (j + 1)];
+            u32x4 raw[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                raw[u] = u < left && (unsigned)c[u] < (unsigned)src_rows ? xs16[c[u] * 8 + sub] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int u = 0; u < 8; u += 2) fma_pair(wt[u], wt[u + 1], raw[u], raw[u + 1], acc);
+        }
+        if (k + 1 < n) plan_of(k + 1, nx);
+        if (cur.live) {
+            if (cur.sg.y >= 0) {
+                store8(part + ((size_t)tile * p.nslot + cur.sg.y) * TW16 + sub * 8, acc);
+            } else {
+                FwdIn16 in{};
+                in.g = cur.rec.x;
+                in.sp = cur.rec.y;
+                if (!epi.sinfo) {
+                    const float4 r = epi.info[cur.sg.x];
+                    in.g = r.x;
+                    in.sp = r.y;
+                }
+                fwd_finish16(epi, cur.sg.x, tile, sub, acc, in);
+            }
+        }
+        cur = nx;
+    }
+}
 
 // acc[0..8) += the n partial sums (8 samples each, slot stride TW16 floats from p) of slots y .., in slot order, 4
 // slots' loads in flight
@@ -539,6 +613,27 @@ hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* sr
         k_cfwd16<<<(unsigned)((long long)T * RB), WG, (size_t)(fw > 0 ? fw - 4 : 0) * 4, st>>>(
             p, cw, src, src_rows, epi, part, T, RB, src_fires, fw);
         hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (p.nsplit > 0) {
+        k_cfwd16_combine<<<nblocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, epi, T);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_fwd16c_lds(const Plan& p, const int2* cw, const unsigned short* src, int src_rows,
+                             const FwdEpi16& epi, float* part, int T, int S, hipStream_t st) {
+    const size_t lds = (size_t)src_rows * 128;
+    if (S < 1 || src_rows < 1 || lds > FWD_LDS_BYTES || epi.drive || !epi.info) return hipErrorInvalidValue;
+    S = std::max(S, (p.nwave + 64 * FWD_LDS_NW - 1) / (64 * FWD_LDS_NW));     // (at most 64 plan waves per wave)
+    if (p.nwave > 0) {
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_cfwd16_lds),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
+        if (attr != hipSuccess) return attr;
+        k_cfwd16_lds<<<(unsigned)((long long)T * S), FWD_LDS_NW * 64, lds, st>>>(p, cw, (const bf16_t*)src, src_rows,
+                                                                                   epi, part, T, S);
+        const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     if (p.nsplit > 0) {

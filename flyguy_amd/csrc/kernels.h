@@ -50,7 +50,8 @@ struct FwdEpi {
     const float* bias = nullptr;
     const float4* info = nullptr;
     const float4* sinfo = nullptr;    // the same records per segment of the product's plan: whole rows read these
-                                      // (k_fwd), split rows info (k_fwd_combine); both or neither are given
+                                      // (k_fwd), split rows info (k_fwd_combine); both or neither are given.  With
+                                      // a bias, whole rows take it from sinfo (the records' fourth field)
     const float* drive = nullptr;     // the sensory layer's drive, for re-drive rows (nullptr: none in this layer)
     Lay ldrive{};
     float* z = nullptr;               // the pre-activation: stored for the sensory layer (the drive) and raw products
@@ -115,6 +116,12 @@ hipError_t launch_pack_n(const PackJob* jobs, int n, hipStream_t st, bool bf16w 
 // layer's firing bitmaps (launch_fires_pack; fires_ld(src_rows) words per tile; tiled states only), or nullptr
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st, const unsigned* src_fires = nullptr);
+// The same over a tiled source whose tile slab (src_rows x 128 bytes) fits FWD_LDS_BYTES: each of the S workgroups
+// per tile stages the slab in LDS once and gathers from there (the plug: few source rows, each gathered many times)
+constexpr int FWD_LDS_NW = 8;                     // waves per workgroup
+constexpr size_t FWD_LDS_BYTES = 144 * 1024;      // largest slab
+hipError_t launch_fwd_lds(const Plan& p, const int2* cw, const float* src, int src_rows, const FwdEpi& epi, float* part,
+                          Lay lp, int T, int S, hipStream_t st);
 // A tile's firing bitmap: 4 header words (word 0: the number of rows that fire on no sample of the tile), then a
 // bit per row (row r: bit r % 32 of word 4 + r / 32), padded to whole 16-byte units.
 inline int fires_ld(int rows) { return 4 + ((rows + 31) / 32 + 3) / 4 * 4; }
@@ -207,6 +214,9 @@ struct BwdEpi16 {
 hipError_t launch_obs_in16(const float* obs, unsigned short* x, int obs_dim, int B, hipStream_t st);
 hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* src, int src_rows, const FwdEpi16& epi,
                          float* part, int T, hipStream_t st, const unsigned* src_fires = nullptr);
+// the same with each tile's source slab staged in LDS (launch_fwd_lds)
+hipError_t launch_fwd16c_lds(const Plan& p, const int2* cw, const unsigned short* src, int src_rows,
+                             const FwdEpi16& epi, float* part, int T, int S, hipStream_t st);
 // gwpart: per-position weight-gradient partials, gw_ld apart, one row per tile; with pair (a hop layer, mode 1) one
 // row per pair of tiles, ceil(T / 2) rows (the sensory layer, mode 2, always takes one tile per workgroup)
 hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
@@ -238,6 +248,7 @@ struct RowJob {
     // non-null: the records in the order of a row plan's segments instead (rows = the plan's segments, row = seg.x),
     // so that a wave's 8 rows read one 128-byte line (FwdEpi::sinfo)
     const int4* seg = nullptr;
+    const float* bias = nullptr;      // non-null: the records' fourth field is bias[row] (the plug's rows), else 0
 };
 constexpr int ROW_JOBS = 8;
 hipError_t launch_rowinfo_n(const RowJob* jobs, int n, const float* gain, const float* theta, hipStream_t st);

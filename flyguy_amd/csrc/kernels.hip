@@ -68,17 +68,18 @@ __global__ __launch_bounds__(WG) void k_pack(JobTable<PackJob, PACK_JOBS> t) {
 // latency hides behind the gathers.
 struct FwdIn {
     float4 dv;
-    float g, sp;
+    float g, sp, b;                             // b: the row's bias (the plug's records carry it)
 };
 // recs[i]: the row's record (FwdEpi::sinfo from the wave's first segment and i its group for a whole row, info and
 // the row for a split one; nullptr: none)
 __device__ __forceinline__ FwdIn fwd_inputs(const FwdEpi& e, const float4* recs, int i, int d, int tile, int sub) {
-    FwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f};
+    FwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f, 0.f};
     if (e.drive && d >= 0) in.dv = *at4u(e.drive, e.ldrive, tile, d, sub);
     if (recs) {
         const float4 r = recs[i];
         in.g = r.x;
         in.sp = r.y;
+        in.b = r.w;
     }
     return in;
 }
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
         if (left > 8) nxt = q[64 * (j + 1)];
         if (j == 0 && whole) {
             in = fwd_inputs(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub);
-            if (epi.bias) acc = splat(epi.bias[sg.x]);
+            if (epi.bias) acc = splat(epi.sinfo ? in.b : epi.bias[sg.x]);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     }
     if (whole && !(wok && wv.y > 0)) {          // a wave without edges
         in = fwd_inputs(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub);
-        if (epi.bias) acc = splat(epi.bias[sg.x]);
+        if (epi.bias) acc = splat(epi.sinfo ? in.b : epi.bias[sg.x]);
     }
     if (!live) return;
     if (sg.y >= 0) {
@@ -160,6 +161,84 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
         return;
     }
     fwd_finish(epi, sg.x, tile, sub, acc, in);
+}
+
+// The same product for a source slab small enough for the LDS (the plug: each sensory row reads 16 of the 517
+// observation rows, so each observation line of a tile is gathered about 500 times).  A workgroup copies the tile's
+// slab (src_rows lines of 128 bytes) into LDS once and then walks its share of the row plan, gathering from the LDS
+// instead of through the vector-memory path.  The sums are k_fwd's, term for term in the same order.  S workgroups
+// per tile; a wave takes plan waves w0 + k dw (w0 = s FWD_LDS_NW + its index, dw = S FWD_LDS_NW), k < n <= 64.
+// Stores count in the same vector-memory counter as loads, so a load issued after a store is waited for only
+// once the store is done: each plan wave's records and first pairs are therefore requested before the previous
+// plan wave's stores.  No re-drive rows (the plug has none).
+__global__ __launch_bounds__(FWD_LDS_NW * 64) void k_fwd_lds(Plan p, const int2* __restrict__ cw,
+                                                            const float* __restrict__ src, int src_rows, FwdEpi epi,
+                                                            float* __restrict__ part, Lay lp, int T, int S) {
+    __shared__ __align__(16) int2 slots[FWD_LDS_NW * 64 / LPR][LPR];
+    extern __shared__ __align__(16) float4 xs[];          // the tile's slab, src_rows x LPR float4
+    int s;
+    const int tile = tile_of(blockIdx.x, S, T, s);
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63, gi = grp & 7;
+    const int w0 = __builtin_amdgcn_readfirstlane(s * FWD_LDS_NW + (int)(threadIdx.x >> 6)), dw = S * FWD_LDS_NW;
+    const int n = w0 < p.nwave ? (p.nwave - 1 - w0) / dw + 1 : 0;
+    // lane k holds the record of the wave's k-th plan wave (a vector load: waiting for it waits for no LDS read)
+    const int2 wrec = lane < n ? p.wave[w0 + lane * dw] : make_int2(0, 0);
+    const float4* g = reinterpret_cast<const float4*>(src + (size_t)tile * src_rows * TW);
+    for (int i = threadIdx.x; i < src_rows * LPR; i += FWD_LDS_NW * 64) xs[i] = g[i];
+    __syncthreads();
+    struct It {
+        int w;
+        int2 wv, pr;
+        int4 sg;
+        float4 rec;
+        bool wok, live;
+    };
+    // the loads of plan wave k: its record (from wrec), first pairs, segment and row record (by plan position)
+    auto plan_of = [&](int k, It& it) {
+        it.w = w0 + k * dw;
+        const int2 v = make_int2(__builtin_amdgcn_readlane(wrec.x, k), __builtin_amdgcn_readlane(wrec.y, k));
+        it.wok = v.x >= 0 && v.y >= 0 && (long long)v.x + 64 * (((long long)v.y + 7) / 8) <= p.npos;
+        it.wv = it.wok ? v : make_int2(0, 0);
+        it.pr = (it.wok && it.wv.y > 0) ? cw[it.wv.x + lane] : make_int2(NO_ROW, 0);
+        it.live = load_segment(p, it.w * 8 + gi, it.sg) && it.wok;
+        it.rec = epi.sinfo && it.w * 8 + gi < p.nseg ? epi.sinfo[it.w * 8 + gi] : splat(0.f);
+    };
+    It cur, nx;
+    if (n > 0) plan_of(0, cur);
+    for (int k = 0; k < n; ++k) {
+        const bool whole = cur.live && cur.sg.y < 0;
+        float4 acc = splat(0.f);
+        if (whole && epi.bias) acc = splat(epi.sinfo ? cur.rec.w : epi.bias[cur.sg.x]);   // (the bias starts the sum)
+        const int2* q = cw + cur.wv.x + lane;
+        int2 nxt = cur.pr;
+        for (int j = 0, left = cur.wok ? cur.wv.y : 0; left > 0; ++j, left -= 8) {
+            int c[8];
+            float wt[8];
+            stage8(slots[grp], sub, nxt, c, wt);
+            if (left > 8) nxt = q[64 * (j + 1)];
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = u < left && (unsigned)c[u] < (unsigned)src_rows ? xs[c[u] * LPR + sub] : splat(0.f);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) fma4(wt[u], v[u], acc);
+        }
+        if (k + 1 < n) plan_of(k + 1, nx);
+        if (cur.live) {
+            if (cur.sg.y >= 0) {
+                *at4w(part, lp, tile, cur.sg.y, sub) = acc;
+            } else {
+                FwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), cur.rec.x, cur.rec.y, 0.f};
+                if (!epi.sinfo) {
+                    const float4 r = epi.info[cur.sg.x];
+                    in.g = r.x;
+                    in.sp = r.y;
+                }
+                fwd_finish(epi, cur.sg.x, tile, sub, acc, in);
+            }
+        }
+        cur = nx;
+    }
 }
 
 // split rows: partial sums in segment order, then the same finish
@@ -693,7 +772,7 @@ __global__ void k_adam(float* __restrict__ P, const float* __restrict__ G, float
     EMA[i] = fmaf(decay, EMA[i], (1.f - decay) * pi);
 }
 
-// per row of a layer: {gain[nid], softplus(theta[nid]), re-drive row (int bits, -1 none), 0}
+// per row of a layer: {gain[nid], softplus(theta[nid]), re-drive row (int bits, -1 none), bias of the row or 0}
 __global__ __launch_bounds__(WG) void k_rowinfo(JobTable<RowJob, ROW_JOBS> t, const float* __restrict__ gain,
                                                 const float* __restrict__ theta) {
     long long b0;
@@ -702,7 +781,8 @@ __global__ __launch_bounds__(WG) void k_rowinfo(JobTable<RowJob, ROW_JOBS> t, co
     if (r >= J.rows) return;
     const int row = J.seg ? J.seg[r].x : (int)r;
     const int n = J.nid[row];
-    J.info[r] = make_float4(gain[n], softplus_f(theta[n]), __int_as_float(J.drow ? J.drow[row] : -1), 0.f);
+    J.info[r] = make_float4(gain[n], softplus_f(theta[n]), __int_as_float(J.drow ? J.drow[row] : -1),
+                            J.bias ? J.bias[row] : 0.f);
 }
 
 // a state tensor (tiled) -> [rows][B] (tests and diagnostics)
@@ -748,6 +828,27 @@ hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, i
             k_fwd<false><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB,
                                                                        nullptr, 0);
         hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (p.nsplit > 0) {
+        k_fwd_combine<<<blocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, lp, epi, T);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_fwd_lds(const Plan& p, const int2* cw, const float* src, int src_rows, const FwdEpi& epi, float* part,
+                          Lay lp, int T, int S, hipStream_t st) {
+    const size_t lds = (size_t)src_rows * TW * 4;
+    if (S < 1 || src_rows < 1 || lds > FWD_LDS_BYTES || epi.drive || !epi.info) return hipErrorInvalidValue;
+    S = std::max(S, (p.nwave + 64 * FWD_LDS_NW - 1) / (64 * FWD_LDS_NW));     // (at most 64 plan waves per wave)
+    if (p.nwave > 0) {
+        // (above 64 kB of dynamic LDS the kernel must be told its size)
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_lds),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
+        if (attr != hipSuccess) return attr;
+        k_fwd_lds<<<(unsigned)((long long)T * S), FWD_LDS_NW * 64, lds, st>>>(p, cw, src, src_rows, epi, part, lp, T, S);
+        const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     if (p.nsplit > 0) {

@@ -95,6 +95,28 @@ def test_exact_forward_backward(gpu_lib, name, hops, fan):
         assert np.array_equal(g, w.astype(np.float32)), (n, rel(g, w))
 
 
+@pytest.mark.parametrize("fan,split", [(8, "1"), (24, "3")])
+def test_exact_plug_staged_in_lds(gpu_lib, monkeypatch, fan, split):
+    """The plug with each tile's observation slab staged in LDS (forced with FLYGUY_PLUG_LDS = workgroups per tile),
+    bit-exact at B = 192 (three tiles of 64 samples) against the oracle, as the plug that gathers through the
+    vector-memory path is.  With fan 24, above the least segment cap (16), the plug's rows are split over two
+    segments (partial sums, the combine kernel)."""
+    s, P, obs = _exact_case("b", 3, fan, 4)
+    obs = np.concatenate([obs, -obs[::-1], np.roll(obs, 5, axis=1)])
+    o = Core16(s, P)
+    want = o.forward(obs)
+    for layer, (h, _) in enumerate(o.states):
+        assert np.array_equal(bf16(h), h) and np.abs(h).max() < 256, layer
+    for mode in ("0", split):
+        monkeypatch.setenv("FLYGUY_PLUG_LDS", mode)
+        say(f"bf16 exact b hops 3 fan {fan}, B 192, plug staged in LDS {mode}")
+        core = Core(s, P, max_batch=192, flags=BF16)
+        assert np.array_equal(core.forward(obs), want.astype(np.float32))
+        assert np.array_equal(core.state(0, 1, s["sizes"][0], 192), o.drive.astype(np.float32))
+        assert np.array_equal(core.state(0, 0, s["sizes"][0], 192), o.states[0][0].astype(np.float32))
+        del core
+
+
 @pytest.mark.parametrize("tiles", ["1", "2"])
 @pytest.mark.parametrize("hops", [3, 4])
 def test_exact_one_and_two_tile_backward(gpu_lib, monkeypatch, tiles, hops):

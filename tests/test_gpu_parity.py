@@ -116,6 +116,30 @@ def test_one_and_two_tile_backward(gpu_lib, monkeypatch, tiles):
     check_backward(core, o64, s, got)
 
 
+@pytest.mark.parametrize("case,B,split", [("toy", 96, "1"), ("toy", 96, "3"), ("scaled", 160, "2")])
+def test_plug_staged_in_lds(gpu_lib, monkeypatch, case, B, split):
+    """The plug with each tile's observation slab staged in LDS (launch_fwd_lds: by default from 64 tiles up, forced
+    here with FLYGUY_PLUG_LDS = workgroups per tile) sums the same terms in the same order as the plug that gathers
+    through the vector-memory path: the sensory layer's drive and output and the logits are bit-identical, and both
+    match the oracle.  The toy has fan 24, above the least segment cap (16), so its plug rows are split over two
+    segments (partial sums, k_fwd_combine); the 1/16 benchmark shape has 5 tiles (not a multiple of 8)."""
+    if case == "toy":
+        s, params = toy_net("b", 3, 24)
+        assert int(np.diff(s["in_crow"]).max()) > 16
+    else:
+        s, params = scaled_3hop(16)
+    obs = np.random.default_rng(B + int(split)).standard_normal((B, 517)).astype(np.float32)
+    out = {}
+    for mode in ("0", split):
+        monkeypatch.setenv("FLYGUY_PLUG_LDS", mode)
+        say(f"{case}, B {B}: plug staged in LDS {mode}")
+        core, _, got, _ = check_forward(s, params, obs, states=True)
+        out[mode] = (got, core.state(0, 0, s["n_s"], B), core.state(0, 1, s["n_s"], B))
+        del core
+    for a, b in zip(out["0"], out[split]):
+        assert np.array_equal(a, b)
+
+
 @pytest.fixture(scope="module")
 def full():
     return synth_3hop()
