@@ -411,6 +411,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
     const bool quiet = epi.skip_silent && group_silent(bf16_lane_fires(hj));
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int j = 0, left = wok ? wv.y : 0;
+    float pend = 0.f;                           // (a step's partial is stored after the next step's gathers: k_bwd)
     auto step = [&](auto full) {               // (as in k_cfwd16: full steps, then the wave's last)
         constexpr bool FULL = decltype(full)::value;
         int c[8];
@@ -422,6 +423,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
             raw[s] = (FULL || s < left) ? gather16(rs, quiet ? NO_ROW : c[s], sub) : u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (FULL) nxt = q[64 * (j + 1)];
+        if (gwp && j > 0) gwp[64 * (j - 1)] = pend;
         __builtin_amdgcn_sched_barrier(0);
         float d[8];
 #pragma unroll
@@ -429,10 +431,11 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
             if (FULL || s < left) fma_pair(wt[s], wt[s + 1], raw[s], raw[s + 1], acc);
 #pragma unroll
         for (int s = 0; s < 8; ++s) d[s] = (FULL || s < left) ? dot8(hj, raw[s]) : 0.f;   // (0: no edge there)
-        if (gwp) gwp[64 * j] = rs8(d, sub);
+        if (gwp) pend = rs8(d, sub);
     };
     for (; left > 8; ++j, left -= 8) step(Full<true>{});
     if (left > 0) step(Full<false>{});
+    if (gwp && left > 0) gwp[64 * j] = pend;    // (the last step's)
     if (!live) return;
     if (sg.y >= 0) {
         store8(part + ((size_t)tile * p.nslot + sg.y) * TW16 + sub * 8, acc);
@@ -479,6 +482,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
     const bool quiet_b = epi.skip_silent && group_silent(bf16_lane_fires(hjb));
     float acca[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, accb[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int j = 0, left = wok ? wv.y : 0;
+    float pend = 0.f;                           // (a step's partial is stored after the next step's gathers: k_bwd)
     auto step = [&](auto full) {
         constexpr bool FULL = decltype(full)::value;
         int c[8];
@@ -493,6 +497,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
             vb[s] = (FULL || s < left) ? gather16(rbs, quiet_b ? NO_ROW : c[s], sub) : u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (FULL) nxt = q[64 * (j + 1)];
+        if (gwp && j > 0) gwp[64 * (j - 1)] = pend;
         __builtin_amdgcn_sched_barrier(0);
         float d[8];
 #pragma unroll
@@ -503,10 +508,11 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
             }
 #pragma unroll
         for (int s = 0; s < 8; ++s) d[s] = (FULL || s < left) ? dot8(hja, va[s]) + dot8(hjb, vb[s]) : 0.f;
-        if (gwp) gwp[64 * j] = rs8(d, sub);
+        if (gwp) pend = rs8(d, sub);
     };
     for (; left > 8; ++j, left -= 8) step(Full<true>{});
     if (left > 0) step(Full<false>{});
+    if (gwp && left > 0) gwp[64 * j] = pend;    // (the last step's)
     if (!live) return;
     if (sg.y >= 0) {
         store8(part + ((size_t)ta * p.nslot + sg.y) * TW16 + sub * 8, acca);

@@ -438,7 +438,11 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
     float4 acc = splat(0.f);
     const bool whole = live && sg.y < 0;
-    for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
+    // A step's weight-gradient partial is stored after the next step's gathers have gone out: loads and stores count
+    // in one vector-memory counter, so gathers issued after a store are waited for only once the store is done.
+    float pend = 0.f;
+    int j = 0;
+    for (int left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
         float wt[8];
         stage8(slots[grp], sub, nxt, c, wt);
@@ -447,6 +451,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
         for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(quiet ? NO_ROW : c[s], sub) : splat(0.f);
         __builtin_amdgcn_sched_barrier(0);
         if (left > 8) nxt = q[64 * (j + 1)];
+        if (gwp && j > 0) __builtin_nontemporal_store(pend, gwp + 64 * (j - 1));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 8; ++s) fma4(wt[s], v[s], acc);
@@ -454,9 +459,10 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
             float d[8];
 #pragma unroll
             for (int s = 0; s < 8; ++s) d[s] = dot4(hj, v[s]);
-            __builtin_nontemporal_store(rs8(d, sub), gwp + 64 * j);
+            pend = rs8(d, sub);
         }
     }
+    if (gwp && j > 0) __builtin_nontemporal_store(pend, gwp + 64 * (j - 1));
     if (!live) return;
     // the row's other inputs of the neuron backward, after the loop: live across it they would cost registers, and
     // with them waves per SIMD
@@ -501,7 +507,9 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
     float* gwp = gwpart ? gwpart + (size_t)pr * gw_ld + wv.x + lane : nullptr;
     float4 acca = splat(0.f), accb = splat(0.f);
     const bool whole = live && sg.y < 0;
-    for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
+    float pend = 0.f;                           // (a step's partial is stored after the next step's gathers: k_bwd)
+    int j = 0;
+    for (int left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
         float wt[8];
         stage8(slots[grp], sub, nxt, c, wt);
@@ -512,6 +520,7 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
         for (int s = 0; s < 8; ++s) vb[s] = (hasb && s < left) ? sb.get(quiet_b ? NO_ROW : c[s], sub) : splat(0.f);
         __builtin_amdgcn_sched_barrier(0);
         if (left > 8) nxt = q[64 * (j + 1)];
+        if (gwp && j > 0) __builtin_nontemporal_store(pend, gwp + 64 * (j - 1));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -522,9 +531,10 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
             float d[8];
 #pragma unroll
             for (int s = 0; s < 8; ++s) d[s] = dot4(hja, va[s]) + dot4(hjb, vb[s]);
-            __builtin_nontemporal_store(rs8(d, sub), gwp + 64 * j);
+            pend = rs8(d, sub);
         }
     }
+    if (gwp && j > 0) __builtin_nontemporal_store(pend, gwp + 64 * (j - 1));
     if (!live) return;
     BwdIn ina{}, inb{};                         // the rows' other inputs, after the loop (k_bwd)
     if (whole) {                                // (hs is the layer's h: the core's launches hand over e.h)
