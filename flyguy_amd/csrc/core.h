@@ -25,6 +25,7 @@ struct HopD {
     int *nid = nullptr, *drow = nullptr;
     bool has_drive = false;
     bool pair_bwd = false;           // the layer's backward takes two tiles per workgroup (pair_tiles in core.hip)
+    bool bwd_skip = true;            // the layer's backward skips silent source rows (bwd_skip_rows in core.hip)
     int gcols = 0;                   // the backward's gain / threshold partials of the layer below: plan columns
     int* gidx = nullptr;             //   (segments, then split rows) and each column's neuron (-1: none)
     // The reductions' indices, with the first writer of each gradient entry in a backward marked: -1 nothing,

@@ -206,6 +206,18 @@ static bool pair_tiles(const std::vector<int>& crow, int rows) {
     return 4 * s >= 3 * E;
 }
 
+// Whether a layer's backward skips the gathers of source rows that are silent on a tile (the test needs the row's own
+// h line first, so its gathers wait for that load): only where its waves walk more than two steps on average.  A
+// shorter wave is a chain of dependent loads, and the wait costs more than the skip saves.  FLYGUY_BWD_SKIP=0 or 1
+// overrides the choice (FLYGUY_SKIP_SILENT=0 turns off every skip).
+static bool bwd_skip_rows(const HostPlan& b) {
+    if (const char* f = std::getenv("FLYGUY_BWD_SKIP")) {
+        if (f[0] == '0') return false;
+        if (f[0] == '1') return true;
+    }
+    return (long long)b.pos.size() > 2LL * 64 * (long long)b.wave.size();
+}
+
 static bool distinct(const std::vector<int>& v, long long n, bool skip_negative) {
     std::vector<unsigned char> seen((size_t)std::max<long long>(n, 1), 0);
     for (int x : v) {
@@ -372,6 +384,7 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         }
         d.has_drive = std::any_of(h.drow.begin(), h.drow.end(), [](int v) { return v >= 0; });
         d.pair_bwd = pair_tiles(h.crow, d.rows);
+        d.bwd_skip = bwd_skip_rows(b);
         d.nid = upload(*c, h.nid);
         d.drow = upload(*c, h.drow);
         d.cw = dalloc<int2>(*c, (size_t)d.fp.npos);
@@ -684,7 +697,7 @@ bool backward(Core& c, const float* dlogits, int B, bool fresh) {
         HopD& d = c.hop[k - 1];
         BwdEpi e;
         e.gdrive = c.gdrive; e.lgd = tiled(c.n_s);
-        e.skip_silent = c.skip_silent;
+        e.skip_silent = c.skip_silent && d.bwd_skip;
         const float* hbelow;
         int rows_below;
         float *ggp, *gsp;
@@ -837,7 +850,7 @@ static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
         BwdEpi16 e;
         e.gdrive = c.gdrive;
         e.n_s = c.n_s;
-        e.skip_silent = c.skip_silent;
+        e.skip_silent = c.skip_silent && d.bwd_skip;
         int rows_below;
         float *ggp, *gsp;
         const int* nid_below;

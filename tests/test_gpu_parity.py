@@ -203,6 +203,7 @@ def test_skipping_silent_rows_changes_nothing(gpu_lib, monkeypatch, full, B, fla
     obs = rng.standard_normal((B, 517)).astype(np.float32)
     dl = (rng.standard_normal((B, 90)) / B).astype(np.float32)
     out = {}
+    monkeypatch.setenv("FLYGUY_BWD_SKIP", "1")                 # every layer's backward skips (short waves too)
     for mode in ("1", "0"):
         monkeypatch.setenv("FLYGUY_SKIP_SILENT", mode)
         core = Core(s, P, max_batch=B, flags=flags)
