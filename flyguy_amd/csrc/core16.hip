@@ -634,8 +634,8 @@ hipError_t launch_fwd16c_lds(const Plan& p, const int2* cw, const unsigned short
     if (S < 1 || src_rows < 1 || lds > FWD_LDS_BYTES || epi.drive || !epi.info) return hipErrorInvalidValue;
     S = std::max(S, (p.nwave + 64 * FWD_LDS_NW - 1) / (64 * FWD_LDS_NW));     // (at most 64 plan waves per wave)
     if (p.nwave > 0) {
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_cfwd16_lds),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
+        const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_cfwd16_lds),   // (k_fwd_lds)
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
         if (attr != hipSuccess) return attr;
         k_cfwd16_lds<<<(unsigned)((long long)T * S), FWD_LDS_NW * 64, lds, st>>>(p, cw, (const bf16_t*)src, src_rows,
                                                                                    epi, part, T, S);

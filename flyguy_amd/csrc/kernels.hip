@@ -853,9 +853,10 @@ hipError_t launch_fwd_lds(const Plan& p, const int2* cw, const float* src, int s
     if (S < 1 || src_rows < 1 || lds > FWD_LDS_BYTES || epi.drive || !epi.info) return hipErrorInvalidValue;
     S = std::max(S, (p.nwave + 64 * FWD_LDS_NW - 1) / (64 * FWD_LDS_NW));     // (at most 64 plan waves per wave)
     if (p.nwave > 0) {
-        // (above 64 kB of dynamic LDS the kernel must be told its size)
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_lds),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
+        // (above 64 kB of dynamic LDS the kernel must be told its size; set on every launch, so that it holds on
+        // whichever device is current)
+        const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_lds),
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
         if (attr != hipSuccess) return attr;
         k_fwd_lds<<<(unsigned)((long long)T * S), FWD_LDS_NW * 64, lds, st>>>(p, cw, src, src_rows, epi, part, lp, T, S);
         const hipError_t e = hipGetLastError();
