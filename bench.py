@@ -421,7 +421,8 @@ def hophip_leg(s, params, steps: int, warmup: int, B: int = 4096) -> dict:
 
     res = {"batch": B, "workload": "FlyActor forward / teaching step (KL, autograd backward, torch.optim.Adam) with "
                                    "its hop products on HopHip (float32: fh_to_tiled copies into fh_spmm_tiled / fh_spmm_bwd_tiled; "
-                                   "binary16 states: fh_spmm_h / fh_spmm_bwd_h), states [rows][B]"}
+                                   "binary16 states: fh_spmm_h / fh_spmm_bwd_h) and float32 activations on FireHip "
+                                   "(fh_fire / fh_fire_bwd), states [rows][B]"}
     for kernel in ("hip", "cuda16"):
         f.kernel = kernel
         out = {}

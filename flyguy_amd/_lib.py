@@ -40,6 +40,8 @@ _SIGS = {
     "fh_spmm_bwd": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp, vp]),
     "fh_to_half": (None, [vp, ci, ci, vp, vp, vp]),
     "fh_to_tiled": (None, [vp, ci, ci, vp, vp]),
+    "fh_fire": (None, [vp, vp, vp, ci, ci, vp, vp]),
+    "fh_fire_bwd": (None, [vp, vp, vp, vp, ci, ci, vp, vp, vp, vp]),
     "fh_spmm_tiled": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp, vp, vp]),
     "fh_spmm_bwd_tiled": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp,
                                  vp]),

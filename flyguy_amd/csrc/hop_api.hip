@@ -103,6 +103,76 @@ __global__ __launch_bounds__(WG) void k_to_tiled(const float* __restrict__ x, in
     reinterpret_cast<float4*>(out + (size_t)rt * TW)[sub] = v;
 }
 
+// The neuron activation of FlyActor's GPU path, h = relu(g z - t) per row of row-major [rows][B] states (g the
+// gain, t softplus(theta) of the row's neuron), in one pass instead of PyTorch's three (product, difference, relu),
+// rounded as PyTorch rounds them: the product, then the difference, no fused multiply-add.  relu passes a NaN on.
+__device__ __forceinline__ float pre1(float g, float z, float t) {
+#pragma clang fp contract(off)
+    return g * z - t;                           // (two roundings: the compiler may not fuse them here)
+}
+__device__ __forceinline__ float fire1(float g, float z, float t) {
+    const float a = pre1(g, z, t);
+    return a > 0.f ? a : (a != a ? a : 0.f);
+}
+
+// I: the index type (32-bit unless the states hold 2^31 float4 or more: its division is the cheaper one)
+template <class I>
+__global__ __launch_bounds__(WG) void k_fire(const float4* __restrict__ z, const float* __restrict__ g,
+                                             const float* __restrict__ t, I q, I n, float4* __restrict__ h) {
+    const I i = (I)blockIdx.x * WG + threadIdx.x;                           // q float4 per row
+    if (i >= n) return;
+    const int r = (int)(i / q);
+    const float gr = g[r], tr = t[r];
+    const float4 v = z[i];
+    h[i] = make_float4(fire1(gr, v.x, tr), fire1(gr, v.y, tr), fire1(gr, v.z, tr), fire1(gr, v.w, tr));
+}
+
+// Its backward, one workgroup per row: where g z - t is not <= 0 (positive, or NaN: PyTorch's relu passes the
+// gradient of a NaN on) gz = gh g, elsewhere 0, and the row's gradients of g and t, gg = sum gh z and gt = -sum gh
+// over those samples (each product rounded, as PyTorch forms them; the sums in this kernel's order)
+__global__ __launch_bounds__(WG) void k_fire_bwd(const float4* __restrict__ gh, const float4* __restrict__ z,
+                                                 const float* __restrict__ g, const float* __restrict__ t, int q,
+                                                 float4* __restrict__ gz, float* __restrict__ gg,
+                                                 float* __restrict__ gt) {
+    __shared__ float red[2][WG / 64];
+    const int r = blockIdx.x;
+    const float gr = g[r], tr = t[r];
+    float sz = 0.f, s1 = 0.f;
+    for (int k = threadIdx.x; k < q; k += WG) {
+        const size_t i = (size_t)r * q + k;
+        const float4 v = z[i], d = gh[i];
+        const float zv[4] = {v.x, v.y, v.z, v.w}, dv[4] = {d.x, d.y, d.z, d.w};
+        float o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const bool on = !(pre1(gr, zv[c], tr) <= 0.f);
+            o[c] = on ? __fmul_rn(dv[c], gr) : 0.f;
+            sz += on ? __fmul_rn(dv[c], zv[c]) : 0.f;
+            s1 += on ? dv[c] : 0.f;
+        }
+        gz[i] = make_float4(o[0], o[1], o[2], o[3]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        sz += __shfl_xor(sz, o, 64);
+        s1 += __shfl_xor(s1, o, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        red[0][threadIdx.x >> 6] = sz;
+        red[1][threadIdx.x >> 6] = s1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float a = 0.f, b = 0.f;
+        for (int w = 0; w < WG / 64; ++w) {
+            a += red[0][w];
+            b += red[1][w];
+        }
+        gg[r] = a;
+        gt[r] = -b;
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -195,6 +265,37 @@ void fh_spmm_bwd_tiled(const int* wave, int nwave, const int* seg, int nseg, con
     }
     spmm_bwd_run(wave, nwave, seg, nseg, split, nsplit, nslot, pcol, pidx, npos, w, gzt, h, gh, gw, n_rows, n_src, B,
                  (int2*)cw, gwpart, scratch, (hipStream_t)stream, true);
+}
+
+void fh_fire(const float* z, const float* g, const float* t, int rows, int B, float* h, void* stream) {
+    clear_error();
+    if (!z || !g || !t || !h || rows < 0 || B <= 0 || B % 4) {
+        set_error("fh_fire: bad argument");
+        return;
+    }
+    const long long n = (long long)rows * (B / 4);
+    if (n == 0) return;
+    const unsigned blocks = (unsigned)((n + WG - 1) / WG);
+    if (n < (1LL << 31))
+        k_fire<unsigned><<<blocks, WG, 0, (hipStream_t)stream>>>((const float4*)z, g, t, (unsigned)(B / 4), (unsigned)n,
+                                                                 (float4*)h);
+    else
+        k_fire<unsigned long long><<<blocks, WG, 0, (hipStream_t)stream>>>(
+            (const float4*)z, g, t, (unsigned long long)(B / 4), (unsigned long long)n, (float4*)h);
+    FG_CHECK(hipGetLastError(), );
+}
+
+void fh_fire_bwd(const float* gh, const float* z, const float* g, const float* t, int rows, int B, float* gz, float* gg,
+                 float* gt, void* stream) {
+    clear_error();
+    if (!gh || !z || !g || !t || !gz || !gg || !gt || rows < 0 || B <= 0 || B % 4) {
+        set_error("fh_fire_bwd: bad argument");
+        return;
+    }
+    if (rows == 0) return;
+    k_fire_bwd<<<(unsigned)rows, WG, 0, (hipStream_t)stream>>>((const float4*)gh, (const float4*)z, g, t, B / 4,
+                                                                (float4*)gz, gg, gt);
+    FG_CHECK(hipGetLastError(), );
 }
 
 }  // extern "C"

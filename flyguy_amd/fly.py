@@ -245,12 +245,14 @@ class FlyActor(nn.Module):
                               getattr(self, f"n{k}"), getattr(self, f"s{k}"), getattr(self, f"d{k}")))
         return out
 
-    def _walk(self, x: torch.Tensor, product, by_neuron: bool, watch=None) -> torch.Tensor:
+    def _walk(self, x: torch.Tensor, product, by_neuron: bool, watch=None, activate=None) -> torch.Tensor:
         """Logits of a batch: the plug's product plus bias gives the sensory drive, each hop's product (plus the
         drive of its re-driven sensory rows) the next layer's input, every neuron fires relu(gain z - softplus
         theta), and the read-out maps the descending rows to the actions (fly.py:286-305 / 170-185 / 252-284).
         States are [rows, B] when by_neuron, else [B, rows]; product(k, layer, weights, states) is layer k's sparse
-        product (k = 0: the plug).  watch(h) sees every layer's firing."""
+        product (k = 0: the plug).  activate(z, gain, threshold) computes the firing of [rows, B] states from the
+        rows' gains and thresholds (default: PyTorch's elementwise operations).  watch(h) sees every layer's
+        firing."""
         axis = 0 if by_neuron else 1
         thr = nn.functional.softplus(self.theta)
 
@@ -258,6 +260,8 @@ class FlyActor(nn.Module):
             return v[:, None] if by_neuron else v
 
         def fire(z, nid):
+            if activate is not None:
+                return activate(z, self.gain[nid], thr[nid])
             return torch.relu(per_row(self.gain[nid]) * z - per_row(thr[nid]))
 
         layers = self._layers()
@@ -268,7 +272,10 @@ class FlyActor(nn.Module):
         for k, layer in enumerate(layers[1:], start=1):
             z = product(k, layer, self.w[layer.edges], h)
             if len(layer.redriven):
-                z = z.index_add(axis, layer.redriven, drive.index_select(axis, layer.drive_rows))
+                add = drive.index_select(axis, layer.drive_rows)
+                # (the library's products return a new tensor of their own, which can take the sums in place; the
+                # PyTorch path's product is a view made inside its autograd function, which cannot)
+                z = z.index_add_(axis, layer.redriven, add) if by_neuron else z.index_add(axis, layer.redriven, add)
             h = fire(z, layer.nid)
             if watch is not None:
                 watch(h)
@@ -328,13 +335,14 @@ class FlyActor(nn.Module):
         if not obs.is_cuda and not torch.is_grad_enabled():
             return self._play(obs)
         if self.kernel != "torch" and obs.is_cuda and obs.shape[0] % 32 == 0:      # (at any batch size)
-            from .fly_hip import HopHip
+            from .fly_hip import FireHip, HopHip
             half = self.kernel == "cuda16"
 
             def on_library(k, layer, w, h):
                 p = layer.prod
                 return HopHip.apply(w, h, p.crow, p.ci, p.tcrow, p.tci, p.tperm, half and k > 0)
-            return self._walk(obs.t().contiguous(), on_library, by_neuron=True)
+            activate = FireHip.apply if self.w.dtype == torch.float32 else None
+            return self._walk(obs.t().contiguous(), on_library, by_neuron=True, activate=activate)
 
         few = obs.shape[0] * self.used <= self.gather_limit        # a few samples: gather / scatter products
 

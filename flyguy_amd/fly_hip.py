@@ -166,3 +166,36 @@ class HopHip(torch.autograd.Function):
                  gw.data_ptr() if gw is not None else None, ctx.n_rows, n_src, B, cw.data_ptr(),
                  gwpart.data_ptr() if gwpart is not None else None, scratch.data_ptr(), _stream(gz))
         return gw, (gh if ctx.needs_input_grad[1] else None), None, None, None, None, None, None
+
+
+class FireHip(torch.autograd.Function):
+    """h = relu(g z - t) per row of row-major [rows, B] float32 states on the library (fh_fire, fh_fire_bwd): the
+    neuron activation of FlyActor's GPU path (fly.py:296-304) in one pass each way instead of PyTorch's three.  g, t:
+    per row (the gain and softplus(theta) of the row's neuron).  h and the state gradient are PyTorch's bit for bit;
+    the per-row gradients of g and t are the same sums in another order."""
+
+    @staticmethod
+    def forward(ctx, z, g, t):
+        rows, B = z.shape
+        if z.dtype != torch.float32 or not z.is_cuda or B % 4:
+            raise ValueError("FireHip: z must be float32 [rows, B] on the GPU with B a multiple of 4")
+        z = z.contiguous()
+        g = g.detach().float().contiguous()
+        t = t.detach().float().contiguous()
+        if g.shape != (rows,) or t.shape != (rows,):
+            raise ValueError("FireHip: g and t must hold one value per row")
+        h = torch.empty_like(z)
+        call("fh_fire", z.data_ptr(), g.data_ptr(), t.data_ptr(), rows, B, h.data_ptr(), _stream(z))
+        ctx.save_for_backward(z, g, t)
+        return h
+
+    @staticmethod
+    def backward(ctx, gh):
+        z, g, t = ctx.saved_tensors
+        rows, B = z.shape
+        gh = gh.contiguous().float()
+        gz, gg, gt = torch.empty_like(z), torch.empty_like(g), torch.empty_like(t)
+        call("fh_fire_bwd", gh.data_ptr(), z.data_ptr(), g.data_ptr(), t.data_ptr(), rows, B, gz.data_ptr(),
+             gg.data_ptr(), gt.data_ptr(), _stream(gh))
+        return gz, gg, gt
+

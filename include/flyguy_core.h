@@ -183,6 +183,19 @@ void fh_spmm_bwd_tiled(const int* wave, int nwave, const int* seg, int nseg, con
                        float* gh, float* gw, int n_rows, int n_src, int B, void* cw, float* gwpart, float* scratch,
                        void* stream);
 
+/* ---- the neuron activation of FlyActor's GPU path, h = relu(g z - t) per row, for the PyTorch elementwise steps of
+ * fly.py:296-304 (fire).  No counterpart in the library of the reference: its GPU actor path (fly.py:170-185) forms
+ * it from three PyTorch operations, each a pass over the states.  z, h: [rows][B] row-major float32, B % 4 == 0;
+ * g, t: per row (the gain and softplus(theta) of the row's neuron).  The product and the difference are rounded
+ * separately, as PyTorch rounds them, so h is PyTorch's bit for bit. ---- */
+void fh_fire(const float* z, const float* g, const float* t, int rows, int B, float* h, void* stream);
+
+/* The backward of fh_fire from gh, the gradient of h: gz = gh g where g z - t is not <= 0 (PyTorch's relu passes a
+ * NaN's gradient on), else 0; per row the gradients of g and t, gg = sum of gh z and gt = -(sum of gh) over those
+ * samples. */
+void fh_fire_bwd(const float* gh, const float* z, const float* g, const float* t, int rows, int B, float* gz, float* gg,
+                 float* gt, void* stream);
+
 /* ---- 16-bit states (the reference's half path, fly_cuda.py:34-56, 93-115): products read states and gradients as
  * IEEE binary16 and accumulate in float32.  A 16-bit state tensor is tiled: [ceil(B/64)][rows][64] halves, samples
  * past B zero. ---- */
