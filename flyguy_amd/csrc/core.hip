@@ -721,10 +721,17 @@ bool backward(Core& c, const float* dlogits, int B, bool fresh) {
         }
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = d.gcols;
         e.sinfo = d.bsinfo;
+        // the plug's gradients in a kernel of their own with the observations in LDS, where the forward's plug is
+        // (plug_split): the sensory finish then leaves the drive's complete gradient in gdrive for it
+        const int ps = k == 1 ? plug_split(c, T) : 0;
+        if (ps) e.in_crow = nullptr;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
             FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart,
                                 d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st, d.pair_bwd), false);
+            if (ps)
+                FG_CHECK(launch_plug_bwd_lds(c.gdrive, c.x, c.obs_dim, c.in_crow, c.in_col, c.n_s, c.ginb, c.n_s, c.ginw,
+                                             c.E_in, T, ps, st), false);
         }
         Timed t(c, ST_REDUCE);
         // the layer's sums in one launch: each writes its own gradient array

@@ -86,7 +86,8 @@ struct BwdEpi {
     float* ggain_part = nullptr;  // [T][gp_ld]: sum over the tile of g * z, in plan columns: a whole row at its
     float* gsum_part = nullptr;   //   segment, split row i at nseg + i (the read-out kernel: the row itself);
     long long gp_ld = 0;          //   [T][gp_ld]: sum over the tile of g
-    // mode 2: the plug
+    // mode 2: the plug (in_crow nullptr: the finish stores the drive's complete gradient into gdrive instead, for
+    // launch_plug_bwd_lds)
     const int* in_crow = nullptr;     // the plug's CSR: connections in_crow[j] .. in_crow[j+1] of sensory row j
     const int* in_col = nullptr;      //   read observation rows in_col[f]
     const float* x = nullptr;         // the observations, tiled, x_rows of them
@@ -122,6 +123,12 @@ constexpr int FWD_LDS_NW = 8;                     // waves per workgroup
 constexpr size_t FWD_LDS_BYTES = 144 * 1024;      // largest slab
 hipError_t launch_fwd_lds(const Plan& p, const int2* cw, const float* src, int src_rows, const FwdEpi& epi, float* part,
                           Lay lp, int T, int S, hipStream_t st);
+// The plug's bias and per-connection gradient partials (ginb [T][gb_ld], ginw [T][gw_ld]) from the drive's complete
+// gradient gd ([T][n_s][32], left by a sensory-layer backward whose BwdEpi has no in_crow), with each tile's
+// observation slab (x_rows x 128 bytes) staged in LDS by each of its S workgroups
+hipError_t launch_plug_bwd_lds(const float* gd, const float* x, int x_rows, const int* in_crow, const int* in_col,
+                               int n_s, float* ginb, long long gb_ld, float* ginw, long long gw_ld, int T, int S,
+                               hipStream_t st);
 // A tile's firing bitmap: 4 header words (word 0: the number of rows that fire on no sample of the tile), then a
 // bit per row (row r: bit r % 32 of word 4 + r / 32), padded to whole 16-byte units.
 inline int fires_ld(int rows) { return 4 + ((rows + 31) / 32 + 3) / 4 * 4; }

@@ -241,6 +241,79 @@ __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_fwd_lds(Plan p, const int2*
     }
 }
 
+// The plug's gradients (flyguy_train.cu:158-167 and 174-179 on the plug's CSR) from the drive's complete gradient gd
+// [T][n_s][32], which the sensory layer's backward leaves in place of the drive's gradient: per (tile, sensory row j)
+// the bias partial ginb[tile][j] = the tile's sum of gd, and per connection f of the row ginw[tile][f] = the tile's
+// sum of gd x[in_col[f]].  These are the sums the sensory finish of k_bwd forms (a dot of 4 per lane, then rs8 over
+// the row's 8 lanes), term for term, with the tile's observation slab read from LDS (staged as in k_fwd_lds)
+// instead of gathered through the vector-memory path.  S workgroups per tile; 8-lane group g of workgroup s takes
+// rows s G + g, (S + s) G + g, ... (G groups per workgroup).  A row's gradient line and connection range are
+// requested two rows ahead and its first 16 columns one row ahead, all before the current row's stores.
+__global__ __launch_bounds__(FWD_LDS_NW * 64) void k_plug_bwd_lds(const float* __restrict__ gd,
+                                                                 const float* __restrict__ x, int x_rows,
+                                                                 const int* __restrict__ in_crow,
+                                                                 const int* __restrict__ in_col, int n_s,
+                                                                 float* __restrict__ ginb, long long gb_ld,
+                                                                 float* __restrict__ ginw, long long gw_ld, int T,
+                                                                 int S) {
+    extern __shared__ __align__(16) float4 xs[];          // the tile's observation slab, x_rows x LPR float4
+    constexpr int G = FWD_LDS_NW * 64 / LPR;
+    int s;
+    const int tile = tile_of(blockIdx.x, S, T, s);
+    const float4* gx = reinterpret_cast<const float4*>(x + (size_t)tile * x_rows * TW);
+    for (int i = threadIdx.x; i < x_rows * LPR; i += FWD_LDS_NW * 64) xs[i] = gx[i];
+    __syncthreads();
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7;
+    const float4* gdt = reinterpret_cast<const float4*>(gd + (size_t)tile * n_s * TW);
+    float* wo = ginw + (size_t)tile * gw_ld;
+    struct Row {
+        float4 g;
+        int f0, f1, c0, c1;
+    };
+    auto fetch = [&](int j, Row& r) {          // its gradient line and connection range
+        const bool ok = j < n_s;
+        r.g = ok ? gdt[(size_t)j * LPR + sub] : splat(0.f);
+        r.f0 = ok ? in_crow[j] : 0;
+        r.f1 = ok ? in_crow[j + 1] : 0;
+    };
+    auto cols = [&](Row& r) {                  // its first 16 columns (NO_ROW past the row's end)
+        r.c0 = r.f0 + sub < r.f1 ? in_col[r.f0 + sub] : NO_ROW;
+        r.c1 = r.f0 + 8 + sub < r.f1 ? in_col[r.f0 + 8 + sub] : NO_ROW;
+    };
+    // the connections of 8 columns (one per lane) against the row's line: lane l ends with column l's sum
+    auto chunk = [&](const float4& g, int mc) {
+        int c[8];
+        c[0] = bcast8<0>(mc); c[1] = bcast8<1>(mc); c[2] = bcast8<2>(mc); c[3] = bcast8<3>(mc);
+        c[4] = bcast8<4>(mc); c[5] = bcast8<5>(mc); c[6] = bcast8<6>(mc); c[7] = bcast8<7>(mc);
+        float dd[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            dd[u] = (unsigned)c[u] < (unsigned)x_rows ? dot4(g, xs[c[u] * LPR + sub]) : 0.f;
+        return rs8(dd, sub);
+    };
+    const int step = S * G;
+    int j = s * G + grp;
+    Row cur, nx, nn;
+    fetch(j, cur);
+    cols(cur);
+    fetch(j + step, nx);
+    for (; j < n_s; j += step) {
+        fetch(j + 2 * step, nn);
+        cols(nx);
+        const float pb = gsum8(hsum4(cur.g));
+        const float p0 = chunk(cur.g, cur.c0), p1 = chunk(cur.g, cur.c1);
+        if (sub == 0) ginb[(size_t)tile * gb_ld + j] = pb;
+        if (cur.f0 + sub < cur.f1) wo[cur.f0 + sub] = p0;
+        if (cur.f0 + 8 + sub < cur.f1) wo[cur.f0 + 8 + sub] = p1;
+        for (int f = cur.f0 + 16; f < cur.f1; f += 8) {    // (rows of more than 16 connections)
+            const float p = chunk(cur.g, f + sub < cur.f1 ? in_col[f + sub] : NO_ROW);
+            if (f + sub < cur.f1) wo[f + sub] = p;
+        }
+        cur = nx;
+        nx = nn;
+    }
+}
+
 // split rows: partial sums in segment order, then the same finish
 // acc += the n partial sums of (slots y .., tile), in slot order, 8 loads in flight
 __device__ __forceinline__ void add_parts(const float* __restrict__ part, Lay lp, int tile, int y, int n, int sub,
@@ -389,6 +462,10 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     // the sensory layer: the drive's gradient is complete now -> the plug's bias and per-connection gradients
     float4 gd = in.gd;
     add4(gzv, gd);
+    if (!e.in_crow) {                           // (they come from k_plug_bwd_lds, which reads gd back from here)
+        st_stream(at4uw(e.gdrive, e.lgd, tile, j, sub), gd);
+        return;
+    }
     const float pb = gsum8(hsum4(gd));
     if (sub == 0) e.ginb_part[(size_t)tile * e.gb_ld + j] = pb;
     // connections 8 at a time: each lane fetches one column, the group shares them, gathers the 8 observation rows
@@ -867,6 +944,21 @@ hipError_t launch_fwd_lds(const Plan& p, const int2* cw, const float* src, int s
         return hipGetLastError();
     }
     return hipSuccess;
+}
+
+hipError_t launch_plug_bwd_lds(const float* gd, const float* x, int x_rows, const int* in_crow, const int* in_col,
+                               int n_s, float* ginb, long long gb_ld, float* ginw, long long gw_ld, int T, int S,
+                               hipStream_t st) {
+    const size_t lds = (size_t)x_rows * TW * 4;
+    if (S < 1 || x_rows < 1 || lds > FWD_LDS_BYTES || !gd || !x || !in_crow || !in_col || !ginb || !ginw)
+        return hipErrorInvalidValue;
+    if (n_s <= 0 || T <= 0) return hipSuccess;
+    const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_plug_bwd_lds),    // (k_fwd_lds)
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
+    if (attr != hipSuccess) return attr;
+    k_plug_bwd_lds<<<(unsigned)((long long)T * S), FWD_LDS_NW * 64, lds, st>>>(gd, x, x_rows, in_crow, in_col, n_s, ginb,
+                                                                               gb_ld, ginw, gw_ld, T, S);
+    return hipGetLastError();
 }
 
 template <bool TILED, int MODE>

@@ -118,11 +118,13 @@ def test_one_and_two_tile_backward(gpu_lib, monkeypatch, tiles):
 
 @pytest.mark.parametrize("case,B,split", [("toy", 96, "1"), ("toy", 96, "3"), ("scaled", 160, "2")])
 def test_plug_staged_in_lds(gpu_lib, monkeypatch, case, B, split):
-    """The plug with each tile's observation slab staged in LDS (launch_fwd_lds: by default from 64 tiles up, forced
-    here with FLYGUY_PLUG_LDS = workgroups per tile) sums the same terms in the same order as the plug that gathers
-    through the vector-memory path: the sensory layer's drive and output and the logits are bit-identical, and both
-    match the oracle.  The toy has fan 24, above the least segment cap (16), so its plug rows are split over two
-    segments (partial sums, k_fwd_combine); the 1/16 benchmark shape has 5 tiles (not a multiple of 8)."""
+    """The plug with each tile's observation slab staged in LDS (launch_fwd_lds, and its gradients through
+    launch_plug_bwd_lds: by default from 64 tiles up, forced here with FLYGUY_PLUG_LDS = workgroups per tile) sums the
+    same terms in the same order as the plug that gathers through the vector-memory path: the sensory layer's drive
+    and output, the logits and all seven gradients are bit-identical, and both match the oracle.  The toy has fan 24,
+    above the least segment cap (16), so its plug rows are split over two segments (partial sums, k_fwd_combine) and
+    take a third chunk of 8 columns in the gradient kernel; the 1/16 benchmark shape has 5 tiles (not a multiple of
+    8)."""
     if case == "toy":
         s, params = toy_net("b", 3, 24)
         assert int(np.diff(s["in_crow"]).max()) > 16
@@ -133,8 +135,9 @@ def test_plug_staged_in_lds(gpu_lib, monkeypatch, case, B, split):
     for mode in ("0", split):
         monkeypatch.setenv("FLYGUY_PLUG_LDS", mode)
         say(f"{case}, B {B}: plug staged in LDS {mode}")
-        core, _, got, _ = check_forward(s, params, obs, states=True)
-        out[mode] = (got, core.state(0, 0, s["n_s"], B), core.state(0, 1, s["n_s"], B))
+        core, o64, got, _ = check_forward(s, params, obs, states=True)
+        check_backward(core, o64, s, got)
+        out[mode] = (got, core.state(0, 0, s["n_s"], B), core.state(0, 1, s["n_s"], B), *core.get(4))
         del core
     for a, b in zip(out["0"], out[split]):
         assert np.array_equal(a, b)
