@@ -98,15 +98,19 @@ def test_exact_forward_backward(gpu_lib, name, hops, fan):
 @pytest.mark.parametrize("fan,split", [(8, "1"), (24, "3")])
 def test_exact_plug_staged_in_lds(gpu_lib, monkeypatch, fan, split):
     """The plug with each tile's observation slab staged in LDS (forced with FLYGUY_PLUG_LDS = workgroups per tile),
-    bit-exact at B = 192 (three tiles of 64 samples) against the oracle, as the plug that gathers through the
-    vector-memory path is.  With fan 24, above the least segment cap (16), the plug's rows are split over two
-    segments (partial sums, the combine kernel)."""
+    bit-exact at B = 192 (three tiles of 64 samples) against the oracle, logits, sensory states and all seven
+    gradients, as with the plug that gathers through the vector-memory path.  With fan 24, above the least segment
+    cap (16), the plug's rows are split over two segments (partial sums, the combine kernel) and its gradient takes
+    a third chunk of columns.  (The bfloat16 core keeps the plug's gradients in the sensory finish: a separate
+    kernel as in float32 was slower here, its float32 drive gradient at B=16384 being 1.1 GB to write and read.)"""
     s, P, obs = _exact_case("b", 3, fan, 4)
     obs = np.concatenate([obs, -obs[::-1], np.roll(obs, 5, axis=1)])
     o = Core16(s, P)
     want = o.forward(obs)
     for layer, (h, _) in enumerate(o.states):
         assert np.array_equal(bf16(h), h) and np.abs(h).max() < 256, layer
+    dl = np.random.default_rng(11).choice([-1.0, 0.0, 1.0], want.shape).astype(np.float32)
+    want_g = o.backward(dl)
     for mode in ("0", split):
         monkeypatch.setenv("FLYGUY_PLUG_LDS", mode)
         say(f"bf16 exact b hops 3 fan {fan}, B 192, plug staged in LDS {mode}")
@@ -114,6 +118,10 @@ def test_exact_plug_staged_in_lds(gpu_lib, monkeypatch, fan, split):
         assert np.array_equal(core.forward(obs), want.astype(np.float32))
         assert np.array_equal(core.state(0, 1, s["sizes"][0], 192), o.drive.astype(np.float32))
         assert np.array_equal(core.state(0, 0, s["sizes"][0], 192), o.states[0][0].astype(np.float32))
+        core.zero_grad()
+        core.backward(dl)
+        for n, g, w in zip(NAMES, core.get(4), want_g):
+            assert np.array_equal(g, w.astype(np.float32)), (n, rel(g, w))
         del core
 
 
