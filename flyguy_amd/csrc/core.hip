@@ -580,15 +580,17 @@ static hipError_t derive_backward(Core& c, bool bf16w, const float* gain, const 
 static bool forward16(Core& c, const float* obs, int B, float* logits, int set);
 static bool backward16(Core& c, const float* dlogits, int B, bool fresh);
 
-// Workgroups per tile of the plug staged in LDS (launch_fwd_lds), or 0 for launch_fwd.  The staging pays when the
-// workgroups have plan waves enough to walk after copying the slab: at 64 tiles or more (B >= 2048), about 2048
-// workgroups in all (measured at B=4096 on the benchmark network, plug 0.191 ms through launch_fwd: 4 / 8 / 12 /
-// 16 / 32 / 64 workgroups per tile 0.202 / 0.153 / 0.153 / 0.154 / 0.164 / 0.179 ms).  FLYGUY_PLUG_LDS=0 turns it
+// Workgroups per tile of the plug staged in LDS (launch_fwd_lds; launch_plug_bwd_lds for its gradients), or 0 for
+// the plug through launch_fwd (its gradients in the sensory finish).  The staging pays when the workgroups have rows
+// enough to walk after copying the slab: at 64 tiles or more (B >= 2048), about `total` workgroups in all.  Measured
+// at B=4096 on the benchmark network: the forward's plug, 0.191 ms through launch_fwd, took 0.202 / 0.153 / 0.153 /
+// 0.154 / 0.164 / 0.179 ms at 4 / 8 / 12 / 16 / 32 / 64 workgroups per tile (total 2048); hop 1's backward with the
+// gradient kernel 1.409 / 1.418 / 1.429 / 1.442 ms at 8 / 16 / 24 / 32 (total 1024).  FLYGUY_PLUG_LDS=0 turns both
 // off, =S forces S workgroups per tile.
-static int plug_split(const Core& c, int T) {
+static int plug_split(const Core& c, int T, int total = 2048) {
     if ((size_t)c.obs_dim * TW * 4 > FWD_LDS_BYTES || c.plug_lds == 0) return 0;
     if (c.plug_lds > 0) return c.plug_lds;
-    return T >= 64 ? std::max(1, 2048 / T) : 0;
+    return T >= 64 ? std::max(1, total / T) : 0;
 }
 
 bool forward(Core& c, const float* obs, int B, float* logits, int set) {
@@ -723,7 +725,7 @@ bool backward(Core& c, const float* dlogits, int B, bool fresh) {
         e.sinfo = d.bsinfo;
         // the plug's gradients in a kernel of their own with the observations in LDS, where the forward's plug is
         // (plug_split): the sensory finish then leaves the drive's complete gradient in gdrive for it
-        const int ps = k == 1 ? plug_split(c, T) : 0;
+        const int ps = k == 1 ? plug_split(c, T, 1024) : 0;
         if (ps) e.in_crow = nullptr;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
