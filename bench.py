@@ -593,13 +593,14 @@ def main() -> int:
     ach_f = ab["hop_fwd"][kf] / (dom_f_ms * 1e-3)
     kb = int(dom_b[3]) - 1
     ach_b = ab["hop_bwd"][kb] / (dom_b_ms * 1e-3)
-    traffic, traffic_note = None, "no counter run recorded"
+    traffic, traffic_b, traffic_note = None, None, "no counter run recorded"
     tfile = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_synth3hop_b4096.json")
     if os.path.exists(tfile):
         with open(tfile) as fh:
             tj = json.load(fh)
         if tj.get("sources_sha256") == kernel_sources_sha():
             traffic, traffic_note = tj.get("k_fwd " + dom_f), tj.get("command", "")
+            traffic_b = tj.get(("k_bwd2 " if bwd_pairs(s["hop"][kb]["crow"]) else "k_bwd ") + dom_b)
         else:
             traffic_note = "the counter run predates the current kernel sources (profiles/traffic_synth3hop_b4096.json)"
 
@@ -678,6 +679,7 @@ def main() -> int:
                   "roofline": {"bound": "hbm", "kernel": ("k_bwd2 " if bwd_pairs(s["hop"][kb]["crow"]) else "k_bwd ")
                                                          + dom_b, "achieved": round(ach_b / 1e9, 1),
                                "peak": 8000.0, "unit": "GB/s", "frac": round(ach_b / PEAK_HBM, 4),
+                               "traffic": traffic_b, "traffic_source": traffic_note,
                                "algorithmic_bytes_per_launch": ab["hop_bwd"][kb],
                                "mean_launch_ms": round(dom_b_ms, 4),
                                "whole_step_frac": round(ab["train"] / (t_train / K) / PEAK_HBM, 4),
