@@ -96,3 +96,23 @@ def test_malformed_networks_are_refused_on_the_host():
     tc[[0, i]] = tc[[i, 0]]
     s6["hop"][2]["tcol"] = tc
     assert "not the transpose" in _bad(net_bytes(s6))
+
+
+def test_hop_boundary_refuses_bad_arguments_on_the_host():
+    """The HopCuda-boundary additions (tiled products, the fused activation) check their arguments before any
+    device call: each refusal below names its entry point, on a machine without a GPU."""
+    from flyguy_amd._lib import LibraryError, call
+    x = ctypes.c_void_p(64)                                     # (never dereferenced: the checks fail first)
+    with pytest.raises(LibraryError, match="fh_to_tiled"):
+        call("fh_to_tiled", x, 4, 48, x, None)                  # B not a multiple of 32
+    with pytest.raises(LibraryError, match="fh_fire"):
+        call("fh_fire", x, x, None, 4, 32, x, None)             # no thresholds
+    with pytest.raises(LibraryError, match="fh_fire"):
+        call("fh_fire", x, x, x, 4, 30, x, None)                # B not a multiple of 4
+    with pytest.raises(LibraryError, match="fh_fire_bwd"):
+        call("fh_fire_bwd", x, x, x, x, 4, 32, x, None, x, None)   # no gain gradient
+    plan = (x, 1, x, 9, None, 0, 0, x, x, 64)                   # 9 segments for 1 wave (at most 8)
+    with pytest.raises(LibraryError, match="fh_spmm_tiled"):
+        call("fh_spmm_tiled", *plan, x, x, x, 4, 4, 32, x, None, None)
+    with pytest.raises(LibraryError, match="fh_spmm_bwd_tiled"):
+        call("fh_spmm_bwd_tiled", *plan, x, x, x, x, None, 4, 4, 32, x, None, None, None)
