@@ -599,6 +599,8 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     hipStream_t st = c.st;
     { Timed t(c, ST_OBS); FG_CHECK(launch_obs_in(obs, c.x, c.obs_dim, B, st), false); }
     const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
+    // tables made in an earlier pass: the caches have moved on since (see the plug below)
+    const bool old_tables = c.made_fpairs.same(set, c.wver[set]) && c.made_info.same(set, c.wver[set]);
     {
         Timed t(c, ST_PACK);
         FG_CHECK(derive_forward(c, set, false, gain, theta), false);
@@ -615,7 +617,20 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     e0.fires = bytes(0);
     {
         Timed t(c, ST_PLUG);
-        if (const int S = plug_split(c, T))
+        const int S = plug_split(c, T);
+        if (S && old_tables) {
+            // Every workgroup of the LDS plug starts on the plug's plan at once; tables made in an earlier pass come
+            // from HBM then, tables just made (a teaching step's) from the infinity cache.  Reading them into every
+            // XCD's L2 first took repeated forwards at B=4096 from 3.085 to 3.071 ms (the plug with the read from
+            // 0.183 to 0.167 ms); in a teaching step it would only cost its launch.
+            TouchJob tj;
+            tj.p[0] = reinterpret_cast<const uint4*>(c.in_cw); tj.n[0] = c.pp.npos / 2;
+            tj.p[1] = reinterpret_cast<const uint4*>(c.sinfo0); tj.n[1] = c.pp.nseg;
+            tj.p[2] = reinterpret_cast<const uint4*>(c.pp.seg); tj.n[2] = c.pp.nseg;
+            tj.p[3] = reinterpret_cast<const uint4*>(c.pp.wave); tj.n[3] = c.pp.nwave / 2;
+            FG_CHECK(launch_touch(tj, st), false);
+        }
+        if (S)
             FG_CHECK(launch_fwd_lds(c.pp.view(), c.in_cw, c.x, c.obs_dim, e0, c.part, tiled(c.pp.nslot), T, S, st), false);
         else
             FG_CHECK(launch_fwd(c.pp.view(), c.in_cw, c.x, tiled(c.obs_dim), c.obs_dim, e0, c.part, tiled(c.pp.nslot), T, st),

@@ -117,6 +117,13 @@ hipError_t launch_pack_n(const PackJob* jobs, int n, hipStream_t st, bool bf16w 
 // layer's firing bitmaps (launch_fires_pack; fires_ld(src_rows) words per tile; tiled states only), or nullptr
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st, const unsigned* src_fires = nullptr);
+// Tables to bring into every XCD's L2 ahead of a kernel (launch_touch): n[k] 16-byte words at p[k] (n 0: none)
+constexpr int TOUCH_JOBS = 4;
+struct TouchJob {
+    const uint4* p[TOUCH_JOBS] = {};
+    long long n[TOUCH_JOBS] = {};
+};
+hipError_t launch_touch(const TouchJob& j, hipStream_t st);
 // The same over a tiled source whose tile slab (src_rows x 128 bytes) fits FWD_LDS_BYTES: each of the S workgroups
 // per tile stages the slab in LDS once and gathers from there (the plug: few source rows, each gathered many times)
 constexpr int FWD_LDS_NW = 8;                     // waves per workgroup

@@ -314,6 +314,19 @@ __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_plug_bwd_lds(const float* _
     }
 }
 
+// Reads the given tables (16-byte words) and keeps nothing: brings them into the L2 of every XCD before a kernel
+// whose workgroups all start by reading them.  Block b reads for XCD b & 7 (the hardware deals blocks to the XCDs in
+// turn), so each XCD's blocks together read every table once.
+__global__ __launch_bounds__(WG) void k_touch(TouchJob j) {
+    const long long per = ((long long)gridDim.x / 8) * WG;        // threads per XCD
+    const long long i0 = (long long)(blockIdx.x >> 3) * WG + threadIdx.x;
+    unsigned acc = 0;
+#pragma unroll
+    for (int k = 0; k < TOUCH_JOBS; ++k)
+        for (long long i = i0; i < j.n[k]; i += per) acc ^= j.p[k][i].x;
+    asm volatile("" ::"v"(acc));                                   // (the loads are kept; nothing is stored)
+}
+
 // split rows: partial sums in segment order, then the same finish
 // acc += the n partial sums of (slots y .., tile), in slot order, 8 loads in flight
 __device__ __forceinline__ void add_parts(const float* __restrict__ part, Lay lp, int tile, int y, int n, int sub,
@@ -958,6 +971,18 @@ hipError_t launch_plug_bwd_lds(const float* gd, const float* x, int x_rows, cons
     if (attr != hipSuccess) return attr;
     k_plug_bwd_lds<<<(unsigned)((long long)T * S), FWD_LDS_NW * 64, lds, st>>>(gd, x, x_rows, in_crow, in_col, n_s, ginb,
                                                                                gb_ld, ginw, gw_ld, T, S);
+    return hipGetLastError();
+}
+
+hipError_t launch_touch(const TouchJob& j, hipStream_t st) {
+    long long most = 0;
+    for (int k = 0; k < TOUCH_JOBS; ++k) {
+        if (j.n[k] > 0 && !j.p[k]) return hipErrorInvalidValue;
+        most = std::max(most, j.n[k]);
+    }
+    if (most == 0) return hipSuccess;
+    const long long per_xcd = std::min<long long>((most + WG - 1) / WG, 32);      // blocks per XCD
+    k_touch<<<(unsigned)(8 * per_xcd), WG, 0, st>>>(j);
     return hipGetLastError();
 }
 
