@@ -203,7 +203,7 @@ __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_fwd_lds(Plan p, const int2*
         it.live = load_segment(p, it.w * 8 + gi, it.sg) && it.wok;
         it.rec = epi.sinfo && it.w * 8 + gi < p.nseg ? epi.sinfo[it.w * 8 + gi] : splat(0.f);
     };
-    It cur, nx;
+    It cur{}, nx{};                            // (nx stays unused after the last plan wave)
     if (n > 0) plan_of(0, cur);
     for (int k = 0; k < n; ++k) {
         const bool whole = cur.live && cur.sg.y < 0;
