@@ -101,8 +101,8 @@ NO_ROW = 0x01FFFFFF      # the source index of a plan position no edge uses (gat
 
 def seg_cap(n_edges: int) -> int:
     """The segment length cap the library uses for a product of n_edges edges: at least 4096 segments per tile
-    (so that a tile's workgroups fill an XCD), between 16 and 256 edges."""
-    return int(min(256, max(16, -(-int(n_edges) // 4096))))
+    (so that a tile's workgroups fill an XCD), between 16 and 512 edges."""
+    return int(min(512, max(16, -(-int(n_edges) // 4096))))
 
 
 def bwd_pairs(crow) -> bool:

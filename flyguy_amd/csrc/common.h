@@ -19,7 +19,7 @@ constexpr int LPR = TW / 4;     // lanes per row: each lane holds a float4 of th
 constexpr int RPW = 64 / LPR;   // rows per wave (8)
 constexpr int WG = 256;         // threads per workgroup
 constexpr int RPG = WG / LPR;   // rows per workgroup (32)
-constexpr int SEG_MAX = 256;    // longest run of edges one lane group sums before a row is split into segments
+constexpr int SEG_MAX = 512;    // longest run of edges one lane group sums before a row is split into segments
 constexpr int SEG_MIN_PER_TILE = 4096;   // segments a product should have per tile: >= 128 workgroups, so that the
                                          // workgroups resident on an XCD work on one or two tiles at a time (4096
                                          // measured 2-4% faster than 8192 and 2048 on the 3-hop benchmark network:

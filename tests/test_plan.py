@@ -78,8 +78,8 @@ def test_plan_synthetic_graph():
 
 
 def test_seg_cap():
-    assert seg_cap(0) == 16 and seg_cap(292_734) == 72 and seg_cap(600_000) == 147 and seg_cap(1_200_000) == 256
-    assert seg_cap(10 ** 9) == 256
+    assert seg_cap(0) == 16 and seg_cap(292_734) == 72 and seg_cap(600_000) == 147 and seg_cap(1_200_000) == 293
+    assert seg_cap(1_500_000) == 367 and seg_cap(10 ** 9) == 512
 
 
 def test_whole_connectome_generator_small():
