@@ -3,7 +3,7 @@
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--batch 4096] [--cpu-sample 8192] [--cpu-train-batch 4096]
                     [--no-cpu] [--no-floor] [--latency-calls 200] [--trainer-steps 60] [--bf16-steps 10]
-                    [--connectome-steps 10] [--hophip-steps 5]
+                    [--connectome-steps 10] [--hophip-steps 5] [--shipped-steps 20]
 
 Workload: the synthetic 3-hop network of the benchmark shape (16,894 -> 46,393 -> 37,748 -> 1,332 rows; 1.2M /
 1.5M / 292,734 connections = 2,992,734 strengths; lognormal(1.5) in-degree; re-drive rows 12,698 / 5,278 / 12),
@@ -23,6 +23,9 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
   decision_latency_gpu: one fc_forward of a 32-sample tile (a batch-1 decision padded), synchronised per call;
   bf16_b16384: the bfloat16-state core at B = 16384 (forward and teaching step) on the same network and on its
            Erdos-Renyi control;
+  shipped_b4096: the reference's shipped network (its 3-hop graph and trained model.pt, copied into oracle/_ref/shipped
+           as data) at B = 4096: forward and teaching step, the dominant hop's roofline, per layer the share of silent
+           (row, tile) lines, and the reference's CPU forward on it (cpu_baseline, one core);
   whole_connectome_b1024: forward and teaching step at B = 1024 on a graph of the whole connectome's size (166,700
            neurons, 15.3M connections) indexed by FlyActor, with roofline fractions on the pruned hops' bytes;
   hophip_b4096: the HopCuda-style path at B = 4096: FlyActor's forward and a teaching step through PyTorch autograd
@@ -393,6 +396,164 @@ def connectome_leg(steps: int, warmup: int, B: int = 1024) -> dict:
     return res
 
 
+SHIPPED_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "_ref", "shipped")
+
+
+def stage_timing(core, fn, stage: str, steps: int) -> tuple[float, float]:
+    """`steps` calls of fn bracketed by synchronisations, with only `stage` bracketed by HIP events on the library's
+    stream (fc_profile 2 + stage): (seconds for all calls, that stage's mean ms per launch)."""
+    import torch
+    from flyguy_amd._lib import STAGES, call, profile_read
+    stage_of = {name: i for i, name in STAGES.items()}
+    call("fc_profile", core, 2 + stage_of[stage])
+    profile_read(core, reset=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    t = time.perf_counter() - t0
+    prof = profile_read(core, reset=True)
+    call("fc_profile", core, 0)
+    tot, n = prof.get(stage, (0.0, 0))
+    return t, (tot / n if n else float("nan"))
+
+
+def stages_profiled(core, fn, n: int = 5) -> dict:
+    """n calls with every stage bracketed by HIP events (fc_profile 1), outside any timed region: {stage: mean ms}."""
+    import torch
+    from flyguy_amd._lib import call, profile_read
+    call("fc_profile", core, 1)
+    profile_read(core, reset=True)
+    for _ in range(n):
+        fn()
+    torch.cuda.synchronize()
+    prof = profile_read(core, reset=True)
+    call("fc_profile", core, 0)
+    return {k: v[0] / v[1] for k, v in prof.items()}
+
+
+def shipped_leg(steps: int, warmup: int, B: int = 4096, cpu_sample: int = 0) -> dict:
+    """The shipped network: the reference's 3-hop graph (male_cns_min2_3hop.npz) with its trained actor (model.pt),
+    indexed by FlyActor; forward and teaching step at B = 4096, observations ~N(0,1), teacher logits ~N(0,2).  The
+    roofline of the dominant hop launch on the same compulsory-traffic model as the synthetic network (here with
+    strengths shared between hops, so (col, widx) per connection and each strength read once), and per layer the share
+    of (row, 32-sample tile) lines that are silent (h = 0 on the whole tile: gathers the library skips), plain and
+    weighted by how often the next hop gathers each row.  cpu_sample > 0: the reference's CPU forward (fly_infer.cpp,
+    oracle/_ref) on that many batch-1 decisions of the same network, one core, and the median of 300 one-call
+    decisions, as its cpu_baseline."""
+    import numpy as np
+    import torch
+    from flyguy_amd._lib import bwd_pairs, call, lib
+    from flyguy_amd.export import actor_of, net_bytes, params_from_torch, structure
+
+    graph, model = os.path.join(SHIPPED_DIR, "male_cns_min2_3hop.npz"), os.path.join(SHIPPED_DIR, "model.pt")
+    if not (os.path.exists(graph) and os.path.exists(model)):
+        return {"skipped": "the shipped graph and model.pt are not in oracle/_ref/shipped (make -C oracle shipped)"}
+    f = actor_of(torch.load(model, map_location="cpu", weights_only=True), graph=graph)
+    s = structure(f)
+    params = params_from_torch(f, s)
+    raw = net_bytes(s)
+    core = lib().fc_create_from_memory(raw, len(raw), B)
+    if not core:
+        call("fc_create_from_memory")
+    dev = torch.device("cuda:0")
+    tens = [torch.as_tensor(p).to(dev).contiguous() for p in params]
+    ptrs = (ctypes.c_void_p * 7)(*[t.data_ptr() for t in tens])
+    call("fc_copy", core, 0, 1, ptrs)
+    call("fc_copy", core, 1, 1, ptrs)
+    g = torch.Generator(device=dev).manual_seed(0)
+    obs = torch.randn(B, s["obs_dim"], device=dev, generator=g)
+    teacher = torch.randn(B, s["n_act"], device=dev, generator=g) * 2.0
+    logits = torch.empty(B, s["n_act"], device=dev)
+    stats = torch.zeros(2, device=dev)
+    ab = algorithmic_bytes(s, B)
+    res = {"batch": B, "rows": s["sizes"], "connections": [len(h["col"]) for h in s["hop"]], "strengths": s["n_w"],
+           "redrive_rows": [int((h["drow"] >= 0).sum()) for h in s["hop"]], "weights": "bot/model.pt (trained)",
+           "algorithmic_kB_per_decision": round(ab["infer"] / B / 1e3, 1),
+           "algorithmic_kB_per_sample": round(ab["train"] / B / 1e3, 1)}
+
+    def fwd():
+        call("fc_forward", core, obs.data_ptr(), B, logits.data_ptr(), 0)
+
+    def teach():
+        call("fc_teach_step", core, obs.data_ptr(), teacher.data_ptr(), B, 1.0, 1e-4, 3e-5, 1e-4, 0.0, 0.999,
+             stats.data_ptr())
+
+    for _ in range(warmup):
+        fwd()
+    # silent lines per layer, of the forward the timed passes run (the weights do not change during the forwards)
+    silent = []
+    for layer in range(s["hops"] + 1):
+        rows = s["sizes"][layer]
+        h = torch.empty(rows, B, device=dev)
+        call("fc_export_state", core, layer, 0, h.data_ptr(), B)
+        quiet = (h.view(rows, B // 32, 32) <= 0).all(-1).float()
+        entry = {"layer": layer, "silent_lines": round(float(quiet.mean()), 4)}
+        if layer < s["hops"]:
+            deg = torch.as_tensor(np.bincount(s["hop"][layer]["col"], minlength=rows).astype(np.float32), device=dev)
+            entry["silent_gathers_next_hop"] = round(float((quiet * deg[:, None]).sum() / (deg.sum() * (B // 32))), 4)
+        silent.append(entry)
+        del h, quiet
+    res["silent"] = silent
+    for what, fn, kind in (("forward", fwd, "fwd"), ("train", teach, "bwd")):
+        for _ in range(warmup):
+            fn()
+        prof = stages_profiled(core, fn)
+        hops = {f"hop{k + 1} {kind}": prof.get(f"hop{k + 1} {kind}", 0.0) for k in range(s["hops"])}
+        dom = max(hops, key=hops.get)
+        t, dom_ms = stage_timing(core, fn, dom, steps)
+        t /= steps
+        k = int(dom[3]) - 1
+        per_launch = ab["hop_fwd" if kind == "fwd" else "hop_bwd"][k]
+        byts = ab["infer" if what == "forward" else "train"]
+        kern = "k_fwd " if kind == "fwd" else ("k_bwd2 " if bwd_pairs(s["hop"][k]["crow"]) else "k_bwd ")
+        res[what] = {"value": round(B / t, 1), "unit": "decisions/s" if what == "forward" else "samples/s",
+                     "ms_per_step": round(1e3 * t, 4), "algorithmic_bytes": byts,
+                     "whole_batch_frac": round(byts / t / PEAK_HBM, 4),
+                     "roofline": {"bound": "hbm", "kernel": kern + dom, "mean_launch_ms": round(dom_ms, 4),
+                                  "algorithmic_bytes_per_launch": per_launch,
+                                  "achieved": round(per_launch / (dom_ms * 1e-3) / 1e9, 1), "peak": 8000.0,
+                                  "unit": "GB/s", "frac": round(per_launch / (dom_ms * 1e-3) / PEAK_HBM, 4)},
+                     "stages_ms": {k_: round(v, 4) for k_, v in prof.items()}}
+    assert torch.isfinite(logits).all() and np.isfinite(float(stats[0]))
+    print(f"# shipped network B={B}: forward {res['forward']['ms_per_step']:.3f} ms "
+          f"({res['forward']['value']:,.0f}/s), train {res['train']['ms_per_step']:.3f} ms "
+          f"({res['train']['value']:,.0f}/s); silent lines {[e['silent_lines'] for e in silent]}",
+          file=sys.stderr, flush=True)
+    lib().fc_free(core)
+    del tens, obs, teacher, logits
+    torch.cuda.empty_cache()
+    if cpu_sample > 0:
+        res["cpu_baseline"] = shipped_cpu_baseline(s, params, cpu_sample)
+    return res
+
+
+def shipped_cpu_baseline(s, params, sample: int) -> dict | None:
+    """The reference's compiled CPU forward on the shipped network: `sample` batch-1 decisions in one call (one
+    core), and one decision per call, median over 300."""
+    import numpy as np
+    from oracle import refinfer
+    if not refinfer.available():
+        return None
+    ref = refinfer.RefInfer(s, params)
+    rng = np.random.default_rng(3)
+    obs = rng.standard_normal((sample, s["obs_dim"])).astype(np.float32)
+    ref.forward(obs[:8])
+    t0 = time.perf_counter()
+    ref.forward(obs)
+    dt = time.perf_counter() - t0
+    lat = []
+    for i in range(300):
+        t1 = time.perf_counter()
+        ref.forward(obs[i:i + 1])
+        lat.append(time.perf_counter() - t1)
+    return {"value": round(sample / dt, 1), "unit": "decisions/s", "cores": 1, "kind": "reference",
+            "batch1_median_ms": round(1e3 * float(np.median(lat)), 4),
+            "sample": f"{sample} batch-1 decisions of the shipped network (model.pt weights) through fly_infer.cpp "
+                      f"(compiled from the reference), {dt:.1f} s; then 300 one-call decisions"}
+
+
 def hophip_leg(s, params, steps: int, warmup: int, B: int = 4096) -> dict:
     """The HopCuda-style path (fly_cuda.py's, fly.py:170-185): FlyActor's own forward with its hop products on the
     fh_* kernels (HopHip, states [rows][B], PyTorch autograd between the hops), KL against teacher logits, backward
@@ -460,6 +621,8 @@ def main() -> int:
                     help="timed steps of the HopCuda-style path (FlyActor over HopHip) at B=4096 (0: skip)")
     ap.add_argument("--connectome-steps", type=int, default=10,
                     help="timed whole-connectome B=1024 batches and steps (0: skip; its index build takes ~20 s)")
+    ap.add_argument("--shipped-steps", type=int, default=20,
+                    help="timed B=4096 batches and steps on the shipped network (graph + model.pt; 0: skip)")
     ap.add_argument("--no-floor", action="store_true",
                     help="skip the silent-source re-timing of the dominant hops (a counter run then sees only the "
                          "benchmark's own launches)")
@@ -641,6 +804,9 @@ def main() -> int:
         bf16 = bf16_leg(args.bf16_steps, W)
         bf16["workload"] = ("bfloat16 states (x, drive, every layer's h, gathered gz), float32 sums, gradients and "
                                "Adam; B=16384; the synthetic network (lognormal in-degree) and its Erdos-Renyi control")
+    shipped = None
+    if args.shipped_steps > 0:
+        shipped = shipped_leg(args.shipped_steps, W, B, 0 if args.no_cpu else min(args.cpu_sample, 2048))
     connectome = connectome_leg(args.connectome_steps, W) if args.connectome_steps > 0 else None
     hophip = hophip_leg(s, params, args.hophip_steps, W) if args.hophip_steps > 0 else None
     trainer = None
@@ -688,6 +854,7 @@ def main() -> int:
                   "cpu_baseline": cpu_t},
         "trainer": trainer,
         "bf16_b16384": bf16,
+        "shipped_b4096": shipped,
         "whole_connectome_b1024": connectome,
         "hophip_b4096": hophip,
         "stages_ms": {"forward": {k: round(v[0] / v[1], 4) for k, v in prof_fwd.items()},

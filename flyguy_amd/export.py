@@ -142,7 +142,8 @@ USAGE = """python -m flyguy_amd.export COMMAND ...  (the converter of flyguy/nat
         path's answer on it, printed as `flyguy_train --check NET PARAMS BATCH` prints the library's
 
 A checkpoint is read with torch.load(weights_only=True): its "model" holds the actor.* weights, and its
-config.model.fly_graph / fly_hops name the graph and hop count unless --graph / --hops are given."""
+config.model.fly_graph / fly_hops / fly_fan name the graph, hop count and plug fan unless --graph / --hops / --fan
+are given."""
 
 ARRAY_NAMES = ("W", "gain", "theta", "in_w", "in_b", "out_w", "out_b")
 
@@ -154,8 +155,11 @@ def _graph_path(p) -> str:
     return str(q.resolve()) if q.exists() else str(p)
 
 
-def actor_of(ck: dict, graph: str | None = None, hops: int | None = None, fan: int = 16, obs_dim: int = 517):
-    """The FlyActor of a checkpoint dict: built on its graph, with its actor.* weights loaded."""
+def actor_of(ck: dict, graph: str | None = None, hops: int | None = None, fan: int | None = None,
+             obs_dim: int = 517, cls=None, **kw):
+    """The actor of a checkpoint dict: built on its graph with its hop count and plug fan (config.model.fly_graph,
+    fly_hops, fly_fan, unless given), with its actor.* weights loaded.  `cls` is FlyActor or a subclass of it
+    (NativeFlyActor, with its own keyword arguments in kw)."""
     from .fly import FlyActor
     cfg = (ck.get("config") or {}).get("model") or {}
     g = graph or cfg.get("fly_graph")
@@ -165,7 +169,8 @@ def actor_of(ck: dict, graph: str | None = None, hops: int | None = None, fan: i
     if "in_w" not in weights:
         raise SystemExit("the checkpoint holds no fly actor (no actor.in_w)")
     n_act = int(weights["out.bias"].numel()) if "out.bias" in weights else 90
-    f = FlyActor(_graph_path(g), obs_dim, n_act, hops=int(hops or cfg.get("fly_hops", 3)), fan=fan)
+    f = (cls or FlyActor)(_graph_path(g), obs_dim, n_act, hops=int(hops or cfg.get("fly_hops", 3)),
+                          fan=int(fan or cfg.get("fly_fan", 16)), **kw)
     f.load_state_dict(weights, strict=False)
     return f
 
@@ -176,7 +181,7 @@ def _load(path) -> dict:
 
 def _cmd_net(a) -> str:
     from .fly import FlyActor
-    f = FlyActor(_graph_path(a.args[0]), a.obs, 90, hops=a.hops or 3, fan=a.fan)
+    f = FlyActor(_graph_path(a.args[0]), a.obs, 90, hops=a.hops or 3, fan=a.fan or 16)
     out = Path(a.args[1])
     s = write_net(f, out)
     write_params(params_from_torch(f, s), out.with_suffix(".init.bin"))
@@ -247,7 +252,7 @@ def main(argv=None) -> int:
     ap.add_argument("args", nargs="+")
     ap.add_argument("--graph", default=None)
     ap.add_argument("--hops", type=int, default=None)
-    ap.add_argument("--fan", type=int, default=16)
+    ap.add_argument("--fan", type=int, default=None, help="plug fan (default: the checkpoint's fly_fan, else 16)")
     ap.add_argument("--obs", type=int, default=517)
     ap.add_argument("--n", type=int, default=64)
     a = ap.parse_args(argv)

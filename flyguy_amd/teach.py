@@ -100,7 +100,7 @@ class Teacher:
             ck = torch.load(checkpoint, map_location="cpu", weights_only=True)
             cfg = (ck.get("config") or {}).get("model", {})
             net = FlyActor(graph or cfg.get("fly_graph") or fallback_graph, data.obs_dim, 90,
-                           hops=int(cfg.get("fly_hops", hops)))
+                           hops=int(cfg.get("fly_hops", hops)), fan=int(cfg.get("fly_fan", 16)))
             net.load_state_dict(_actor_weights(ck), strict=False)
             self.net = net.to(device).eval()
             self.name = checkpoint.name
@@ -167,10 +167,11 @@ def score(shown: FlyActor, teacher: Teacher, data: Moments, temp: float, device)
 
 def _make_student(args, obs_dim: int, n_act: int) -> tuple[FlyActor, int]:
     if args.start == "fresh":
-        return FlyActor(args.graph, obs_dim, n_act, hops=args.hops, fan=args.fan), 0
+        return FlyActor(args.graph, obs_dim, n_act, hops=args.hops, fan=args.fan or 16), 0
     ck = torch.load(args.start, map_location="cpu", weights_only=True)
     cfg = (ck.get("config") or {}).get("model", {})
-    net = FlyActor(args.graph, obs_dim, n_act, hops=int(cfg.get("fly_hops", args.hops)), fan=args.fan)
+    net = FlyActor(args.graph, obs_dim, n_act, hops=int(cfg.get("fly_hops", args.hops)),
+                   fan=int(args.fan or cfg.get("fly_fan", 16)))
     net.load_state_dict(_actor_weights(ck), strict=False)
     return net, int(ck.get("taught_steps", 0))
 
@@ -183,7 +184,7 @@ def main(argv=None) -> int:
     ap.add_argument("--teacher-graph", default="")
     ap.add_argument("--start", default="fresh")
     ap.add_argument("--hops", type=int, default=3)
-    ap.add_argument("--fan", type=int, default=16)
+    ap.add_argument("--fan", type=int, default=None, help="plug fan (default: the --start checkpoint's fly_fan, else 16)")
     ap.add_argument("--steps", type=int, default=3000)
     ap.add_argument("--batch", type=int, default=128)
     ap.add_argument("--lr", type=float, default=4e-4,
@@ -206,11 +207,11 @@ def main(argv=None) -> int:
     net, step0 = _make_student(args, data.obs_dim, teacher.n_act)
     net.kernel = "torch" if args.kernel == "torch" else "hip"
     net = net.to(device)
-    shown = FlyActor(args.graph, data.obs_dim, teacher.n_act, hops=net.hops, fan=args.fan).to(device).eval()
+    shown = FlyActor(args.graph, data.obs_dim, teacher.n_act, hops=net.hops, fan=net.fan).to(device).eval()
     shown.load_state_dict(net.state_dict())
     print(net.describe(), flush=True)
     student = Student(net, shown, args.lr, args.steps, args.average)
-    saved_cfg = {"fly_graph": str(args.graph), "fly_hops": net.hops, "fly_kernel": "torch"}
+    saved_cfg = {"fly_graph": str(args.graph), "fly_hops": net.hops, "fly_fan": net.fan, "fly_kernel": "torch"}
 
     first, first_kl = score(shown, teacher, data, args.temp, device)
     agree = first

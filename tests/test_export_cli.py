@@ -96,3 +96,18 @@ def test_batch_file_and_the_pytorch_answer(tmp_path, capsys):
     assert m and abs(float(m.group(1)) - loss) <= 1e-5 * max(1.0, abs(loss))
     for name in ("W", "gain", "theta", "in_w", "in_b", "out_w", "out_b"):
         assert re.search(rf"grad {name}\s+norm [-0-9.e+]+ sum [-+0-9.e]+", out), name
+
+
+def test_checkpoint_fan_comes_from_its_config(tmp_path):
+    """A checkpoint trained with another plug fan (config.model.fly_fan) converts without --fan."""
+    torch.manual_seed(4)
+    f = FlyActor(str(GRAPH), 517, 90, hops=3, fan=8)
+    s = structure(f)
+    ck = {"model": {"actor." + k: v.detach().clone() for k, v in f.state_dict().items()},
+          "config": {"model": {"fly_graph": str(GRAPH), "fly_hops": 3, "fly_fan": 8}}, "steps": 5}
+    torch.save(ck, tmp_path / "ck8.pt")
+    assert main(["params", str(tmp_path / "ck8.pt"), str(tmp_path / "p8.bin")]) == 0
+    step, P = read_params(tmp_path / "p8.bin", s)
+    assert s["fan"] == 8 and P[3].size == 8 * s["n_s"]
+    for a, b in zip(P, params_from_torch(f, s)):
+        assert np.array_equal(a, b)

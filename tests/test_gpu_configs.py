@@ -6,6 +6,8 @@
   * bfloat16 states on the full-size synthetic network and on its Erdos-Renyi control: logits and all seven
     gradients against the bfloat16 restatement (oracle/core16.py) at B = 128; at B = 16384 (the bfloat16 benchmark
     batch) batch independence of the logits and additivity of the gradients over four pieces of 4096;
+  * the whole-connectome graph at its configured B = 1024: batch independence bit-exact against 64-sample slices,
+    gradient additivity of four pieces of 256;
   * NativeFlyActor on the whole-connectome graph at B = 1 and B = 37: batches that are padded to 32 in the forward
     (the last observation repeated) and in the backward (zero rows), fly_native.py:53,200, against the float64
     oracle at the unpadded batch;
@@ -69,10 +71,11 @@ def _flipped(core: Core, o: Oracle, s: dict, B: int) -> np.ndarray:
 
 def test_fp32_b4096_teaching_step_against_oracle(gpu_lib, lognormal):
     """The benchmark's teaching step at its batch: forward, KL loss, backward.  Logits and the loss against the
-    oracle; the gradients against the float64 oracle on the samples whose firing pattern the two forward passes share
-    (at B = 4096 a handful of (neuron, sample) pre-activations sit within rounding of the threshold, and the
-    reference's own float32 arithmetic flips them too: its gradients then differ from float64 by 2e-4), and over the
-    whole batch no further from float64 than the float32 oracle is."""
+    oracle; the gradients against the float64 and the float32 oracle on the samples whose firing pattern the library
+    and both oracles share (at B = 4096 a handful of (neuron, sample) pre-activations sit within rounding of the
+    threshold, and the reference's own float32 arithmetic flips them too: its gradients then differ from float64 by
+    up to 9e-4), and over the whole batch within 1e-4 of float64 or no further from it than 1.1 x the float32
+    oracle's own distance + 1e-6."""
     s, params = lognormal
     B = 4096
     rng = np.random.default_rng(40)
@@ -101,19 +104,21 @@ def test_fp32_b4096_teaching_step_against_oracle(gpu_lib, lognormal):
     bad = _flipped(core, o64, s, B)
     bad32 = _flipped_oracles(o32, o64, s, B)
     say(f"   samples with a neuron on the other side of its threshold: {int(bad.sum())} (library), "
-        f"{int(bad32.sum())} (float32 oracle), of {B}")
+        f"{int(bad32.sum())} (float32 oracle), {int((bad | bad32).sum())} (either), of {B}")
     assert bad.sum() <= B // 100
-    # (1) the samples whose firing pattern agrees: the gradients to the 1e-4 bar
+    # (1) the samples whose firing pattern the library and both oracles share: the gradients to the 1e-4 bar against
+    # float64, and against the float32 oracle (the reference's own arithmetic) directly
     d = got_dl.copy()
-    d[bad] = 0.0
+    d[bad | bad32] = 0.0
     core.zero_grad()
     core.backward(d)
-    say("fp32 B 4096: float64 oracle backward, shared firing pattern")
-    for name, g, w in zip(NAMES, core.get(4), o64.backward(d)):
-        r = rel(g, w)
-        say(f"   grad {name:6s} rel {r:.2e}")
-        assert r <= 1e-4, (name, r)
-    # (2) the whole batch: as close to float64 as the reference's own float32 arithmetic
+    say("fp32 B 4096: oracles backward, shared firing pattern")
+    for name, g, a, w in zip(NAMES, core.get(4), o32.backward(d), o64.backward(d)):
+        r, r_32 = rel(g, w), rel(g, a)
+        say(f"   grad {name:6s} rel {r:.2e} (float64), {r_32:.2e} (float32 oracle)")
+        assert r <= 1e-4 and r_32 <= 1e-4, (name, r, r_32)
+    # (2) the whole batch: within 1e-4 of float64, or no further from it than the reference's own float32 arithmetic
+    # is (1.1 x its distance + 1e-6): a threshold flip changes a gradient by the neuron's whole term
     core.zero_grad()
     core.backward(got_dl)
     got = core.get(4)
@@ -121,7 +126,7 @@ def test_fp32_b4096_teaching_step_against_oracle(gpu_lib, lognormal):
     for name, g, a, w in zip(NAMES, got, o32.backward(got_dl), o64.backward(got_dl)):
         r, r_ref = rel(g, w), rel(a, w)
         say(f"   grad {name:6s} rel {r:.2e} (float32 oracle {r_ref:.2e})")
-        assert r <= max(3 * r_ref, 1e-4), (name, r, r_ref)
+        assert r <= 1e-4 or r <= 1.1 * r_ref + 1e-6, (name, r, r_ref)
 
 
 def _flipped_oracles(a: Oracle, b: Oracle, s: dict, B: int) -> np.ndarray:
@@ -236,6 +241,35 @@ def test_whole_connectome_against_oracle(gpu_lib, connectome):
         r = rel(g, w)
         say(f"   grad {name:6s} rel {r:.2e}")
         assert r <= 1e-4, (name, r)
+
+
+def test_whole_connectome_b1024_independence_and_additivity(gpu_lib, connectome):
+    """The whole-connectome case at its configured batch, B = 1024: 64-sample slices give the logits of the whole
+    batch bit for bit (so do a permuted batch's), and the gradients of four pieces of 256 add up to the whole
+    batch's within 1e-5 (relative to the largest entry)."""
+    f, s, params = connectome
+    B = 1024
+    say(f"whole connectome, B {B}")
+    core = Core(s, params, max_batch=B)
+    rng = np.random.default_rng(23)
+    obs = rng.standard_normal((B, 517)).astype(np.float32)
+    big = core.forward(obs)
+    assert np.isfinite(big).all()
+    for start in range(0, B, 64):
+        assert np.array_equal(core.forward(obs[start:start + 64]), big[start:start + 64]), start
+    perm = rng.permutation(B)
+    assert np.array_equal(core.forward(obs[perm]), big[perm])
+    dl = ((rng.standard_normal((B, 90)) + 0.2 * big) / B).astype(np.float32)
+    core.forward(obs)
+    whole = _grads(core, dl)
+    core.zero_grad()
+    for i in range(0, B, 256):
+        core.forward(obs[i:i + 256])
+        core.backward(dl[i:i + 256])
+    for name, a, b in zip(NAMES, core.get(4), whole):
+        r = rel(a, b)
+        say(f"   grad {name:6s} 4 x 256 vs 1024 rel {r:.2e}")
+        assert r <= 1e-5, (name, r)
 
 
 @pytest.mark.parametrize("B", [1, 37])
