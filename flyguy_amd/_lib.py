@@ -35,6 +35,8 @@ _SIGS = {
     "fc_profile": (None, [vp, ci]),
     "fc_profile_read": (ci, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(cll), ci, ci]),
     "fc_plan_rows": (ci, [vp, ci, ci, vp, cll, vp, cll, vp, cll, vp, cll, ctypes.POINTER(cll)]),
+    "fc_net_plan": (ci, [ctypes.c_char_p, cll, ci, ci, vp, cll, vp, cll, vp, cll, vp, cll, ctypes.POINTER(cll)]),
+    "fc_net_marks": (cll, [ctypes.c_char_p, cll, ci, ci, vp, cll]),
     "fh_spmm": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp, vp, vp]),
     "fh_spmm_static": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, ci, ci, ci, vp]),
     "fh_spmm_bwd": (None, [vp, ci, vp, ci, vp, ci, ci, vp, vp, cll, vp, vp, vp, vp, vp, ci, ci, ci, vp, vp, vp, vp]),
@@ -141,6 +143,44 @@ def plan_rows(rowptr, seg_max: int | None = None) -> dict:
         check("fc_plan_rows")
         raise LibraryError("fc_plan_rows failed")
     return {"wave": wave[:nw], "seg": seg[:ns], "split": split[:nsp], "nslot": nslot, "pos": pos[:npos]}
+
+
+def net_plan(net: bytes, product: int, backward: bool = False) -> dict:
+    """The plan a handle of this network (NET.bin bytes) runs for one product (0 the plug, k hop k; backward: the
+    hop's CSC rows), computed on the host by fc_net_plan; the same dict as plan_rows."""
+    import numpy as np
+    counts = (cll * 5)(-1, -1, -1, -1, -1)         # (written only once the network is read and planned)
+    lib().fc_net_plan(net, len(net), product, int(backward), None, 0, None, 0, None, 0, None, 0, counts)
+    if counts[0] < 0:
+        check("fc_net_plan")
+        raise LibraryError("fc_net_plan failed")
+    lib().fc_clear_error()                         # (the capacity error of the sizing call)
+    nw, ns, nsp, nslot, npos = (int(counts[i]) for i in range(5))
+    wave = np.zeros((max(nw, 1), 2), np.int32)
+    seg = np.zeros((max(ns, 1), 4), np.int32)
+    split = np.zeros((max(nsp, 1), 4), np.int32)
+    pos = np.zeros(max(npos, 1), np.int32)
+    rc = lib().fc_net_plan(net, len(net), product, int(backward), wave.ctypes.data, nw, seg.ctypes.data, ns,
+                           split.ctypes.data, nsp, pos.ctypes.data, npos, counts)
+    if rc != 0:
+        check("fc_net_plan")
+        raise LibraryError("fc_net_plan failed")
+    return {"wave": wave[:nw], "seg": seg[:ns], "split": split[:nsp], "nslot": nslot, "pos": pos[:npos]}
+
+
+def net_marks(net: bytes, hop: int, which: int):
+    """The backward's reduction table `which` of hop `hop` (fc_net_marks): 0 column neurons, 1 strength marks per
+    backward position, 2 column marks, 3 the top layer's marks."""
+    import numpy as np
+    n = int(lib().fc_net_marks(net, len(net), hop, which, None, 0))
+    if n < 0:
+        check("fc_net_marks")
+        raise LibraryError("fc_net_marks failed")
+    out = np.zeros(max(n, 1), np.int32)
+    if int(lib().fc_net_marks(net, len(net), hop, which, out.ctypes.data, n)) != n:
+        check("fc_net_marks")
+        raise LibraryError("fc_net_marks failed")
+    return out[:n]
 
 
 STAGES = {0: "obs transpose", 1: "pack", 2: "plug", 11: "logits", 12: "loss", 13: "readout bwd", 22: "reduce",

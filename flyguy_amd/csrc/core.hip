@@ -94,6 +94,27 @@ static bool make_plan(const int* rowptr, int rows, int seg_max, const int* drow,
     return true;
 }
 
+// a plan into caller-owned arrays (fc_plan_rows, fc_net_plan): counts[0..4] = waves, segments, split rows, slots,
+// positions; 0, or -1 when a capacity is too small
+static int plan_out(const HostPlan& p, const char* who, int* wave_out, long long wave_cap, int* seg_out,
+                    long long seg_cap, int* split_out, long long split_cap, int* pos_out, long long pos_cap,
+                    long long* counts) {
+    if (counts) {
+        counts[0] = (long long)p.wave.size(); counts[1] = (long long)p.seg.size(); counts[2] = (long long)p.split.size();
+        counts[3] = p.nslot; counts[4] = (long long)p.pos.size();
+    }
+    if ((long long)p.wave.size() > wave_cap || (long long)p.seg.size() > seg_cap || (long long)p.split.size() > split_cap ||
+        (long long)p.pos.size() > pos_cap) {
+        set_error(std::string(who) + ": capacity");
+        return -1;
+    }
+    if (wave_out && !p.wave.empty()) std::memcpy(wave_out, p.wave.data(), p.wave.size() * sizeof(int2));
+    if (seg_out && !p.seg.empty()) std::memcpy(seg_out, p.seg.data(), p.seg.size() * sizeof(int4));
+    if (split_out && !p.split.empty()) std::memcpy(split_out, p.split.data(), p.split.size() * sizeof(int4));
+    if (pos_out && !p.pos.empty()) std::memcpy(pos_out, p.pos.data(), p.pos.size() * sizeof(int));
+    return 0;
+}
+
 template <class T>
 static T* upload(Core& c, const std::vector<T>& v) {
     T* p = dalloc<T>(c, v.size());
@@ -251,6 +272,151 @@ static bool transposes(const std::vector<int>& crow, const std::vector<int>& col
     return ok;
 }
 
+// ------------------------------------------------------------------------------------------------ the host half
+// NET.bin's arrays after every check, and the plans made from them: everything a handle holds that needs no device.
+// build() uploads it; fc_net_plan / fc_net_marks hand it to the host (the plans the kernels run, for tests).
+struct HopHost { std::vector<int> nid, crow, col, widx, tcrow, tcol, twidx, drow; };
+struct NetHost {
+    int obs_dim = 0, n_act = 0, hops = 0, n_neurons = 0, n_w = 0, n_s = 0, fan = 0, n_dn = 0, E_in = 0;
+    std::vector<int> sizes, E, in_crow, in_col, n0, dn;
+    std::vector<HopHost> hop;
+};
+
+static bool read_net(const unsigned char* bytes, long long len, NetHost& n) {
+    if (!bytes || len < 36 || std::memcmp(bytes, "FLY1", 4) != 0) {
+        set_error("not a FLY1 network file");
+        return false;
+    }
+    Reader r{bytes, len, 4};
+    auto hd = r.ints(8);
+    if (!r.ok) { set_error("short network file (header)"); return false; }
+    n.obs_dim = hd[0]; n.n_act = hd[1]; n.hops = hd[2]; n.n_neurons = hd[3];
+    n.n_w = hd[4]; n.n_s = hd[5]; n.fan = hd[6]; n.n_dn = hd[7];
+    if (n.obs_dim <= 0 || n.n_act <= 0 || n.hops <= 0 || n.hops > 64 || n.n_neurons <= 0 || n.n_w < 0 ||
+        n.n_s <= 0 || n.fan <= 0 || n.n_dn <= 0) {
+        set_error("bad network header");
+        return false;
+    }
+    const int K = n.hops;
+    n.sizes = r.ints(K + 1);
+    n.E = r.ints(K);
+    if (!r.ok) { set_error("short network file (sizes)"); return false; }
+    if (n.sizes[0] != n.n_s) { set_error("sizes[0] != n_s"); return false; }
+    for (int k = 0; k <= K; ++k)
+        if (n.sizes[k] <= 0) { set_error("empty layer"); return false; }
+    for (int k = 0; k < K; ++k)
+        if (n.E[k] < 0) { set_error("negative edge count"); return false; }
+    n.E_in = n.n_s * n.fan;
+    n.in_crow = r.ints(n.n_s + 1);
+    n.in_col = r.ints(n.E_in);
+    r.ints(n.obs_dim + 1); r.ints(n.E_in); r.ints(n.E_in);      // the plug's transposed form: not used here
+    n.n0 = r.ints(n.n_s);
+    if (!r.ok) { set_error("short network file (plug)"); return false; }
+    if (!rowptr_ok(n.in_crow, n.E_in) || !in_range(n.in_col, 0, n.obs_dim) || !distinct(n.n0, n.n_neurons, false)) {
+        set_error("bad plug index arrays");
+        return false;
+    }
+    n.hop.resize(K);
+    std::vector<int> edge_of;                                       // (scratch of transposes())
+    for (int k = 0; k < K; ++k) {
+        HopHost& h = n.hop[k];
+        const int rows = n.sizes[k + 1], src = n.sizes[k], E = n.E[k];
+        h.nid = r.ints(rows); h.crow = r.ints(rows + 1); h.col = r.ints(E); h.widx = r.ints(E);
+        h.tcrow = r.ints(src + 1); h.tcol = r.ints(E); h.twidx = r.ints(E); h.drow = r.ints(rows);
+        if (!r.ok) { set_error("short network file (hop " + std::to_string(k + 1) + ")"); return false; }
+        bool ok = distinct(h.nid, n.n_neurons, false) && rowptr_ok(h.crow, E) && in_range(h.col, 0, src) &&
+                  distinct(h.widx, n.n_w, false) && rowptr_ok(h.tcrow, E) && in_range(h.tcol, 0, rows) &&
+                  distinct(h.twidx, n.n_w, false) && in_range(h.drow, -1, n.n_s) && distinct(h.drow, n.n_s, true);
+        if (!ok) { set_error("bad index arrays in hop " + std::to_string(k + 1)); return false; }
+        if (!transposes(h.crow, h.col, h.widx, h.tcrow, h.tcol, h.twidx, n.n_w, edge_of)) {
+            set_error("hop " + std::to_string(k + 1) + ": the by-source form (tcrow, tcol, twidx) is not the transpose "
+                      "of the by-target form (crow, col, widx)");
+            return false;
+        }
+    }
+    n.dn = r.ints(n.n_dn);
+    r.ints(n.n_w);                                                  // wmap: the caller's business
+    if (!r.ok) { set_error("short network file (read-out)"); return false; }
+    if (!distinct(n.dn, n.sizes[K], false)) { set_error("bad read-out rows"); return false; }
+    return true;
+}
+
+// The plans of every product and the backward's per-column and first-write tables.
+struct NetPlans {
+    HostPlan plug;                          // the plug's rows (its forward and its gradients' pass)
+    std::vector<HostPlan> fwd, bwd;         // per hop: CSR rows (forward), CSC rows = the layer below (backward)
+    std::vector<std::vector<int>> gidx;     // per hop: neuron of each gain / threshold partial column of the backward
+    std::vector<std::vector<int>> ridx;     // per hop: strength of each backward plan position, first writes marked
+    std::vector<std::vector<int>> gridx;    // per hop: gidx with first writes marked
+    std::vector<int> top_ridx;              // the top layer's neurons, first writes marked
+};
+
+static bool plan_net(const NetHost& n, NetPlans& p) {
+    const int K = n.hops;
+    if (!make_plan(n.in_crow.data(), n.n_s, seg_cap(n.E_in), nullptr, p.plug)) return false;
+    // The re-drive field of the transposed plans' segments, which is read by the backward only.  The backward writes
+    // the drive's gradient layer by layer from the top, so the top layer writes each of its re-drive rows first and
+    // a lower layer's row writes its re-drive row first when no layer above re-drives that row (a sensory row
+    // appears at most once per layer).  A first write starts from zero and reads nothing: its row is encoded as
+    // -(d + 3).  A sensory row that no layer re-drives reads zero: it is encoded -2 (others -1).  The gradient
+    // buffer then needs no clearing before a backward.
+    std::vector<std::vector<int>> bwd_drow(K);
+    std::vector<char> touched(n.n_s, 0);
+    for (int L = K; L >= 1; --L) {
+        const std::vector<int>& dr = n.hop[L - 1].drow;
+        if (L < K) {
+            bwd_drow[L - 1].resize(dr.size());
+            for (size_t r = 0; r < dr.size(); ++r)
+                bwd_drow[L - 1][r] = dr[r] >= 0 && !touched[dr[r]] ? -(dr[r] + 3) : dr[r];
+        }
+        for (int v : dr)
+            if (v >= 0) touched[v] = 1;
+    }
+    std::vector<int> sensory_drow(n.n_s);
+    for (int j = 0; j < n.n_s; ++j) sensory_drow[j] = touched[j] ? -1 : -2;
+    p.fwd.resize(K); p.bwd.resize(K); p.gidx.resize(K); p.ridx.resize(K); p.gridx.resize(K);
+    std::vector<std::vector<int>> bwd_w(K);            // per hop: strength per backward position
+    for (int k = 0; k < K; ++k) {
+        const HopHost& h = n.hop[k];
+        const int rows = n.sizes[k + 1], src = n.sizes[k], E = n.E[k];
+        // the transposed plan's rows are the layer below, with their re-drive fields as above
+        const int* below_drow = k >= 1 ? bwd_drow[k - 1].data() : sensory_drow.data();
+        HostPlan& f = p.fwd[k];
+        HostPlan& b = p.bwd[k];
+        if (!make_plan(h.crow.data(), rows, seg_cap(E), h.drow.data(), f) ||
+            !make_plan(h.tcrow.data(), src, seg_cap(E), below_drow, b))
+            return false;
+        // the backward stores the layer below's gain and threshold partials in plan columns: a whole row at its
+        // segment, split row i after the segments (coalesced stores); each column's neuron, for the reduction
+        const std::vector<int>& nid_below = k >= 1 ? n.hop[k - 1].nid : n.n0;
+        std::vector<int>& gidx = p.gidx[k];
+        gidx.assign(b.seg.size() + b.split.size(), -1);
+        for (size_t si = 0; si < b.seg.size(); ++si)
+            if (b.seg[si].y < 0) gidx[si] = nid_below[(size_t)b.seg[si].x];
+        for (size_t i = 0; i < b.split.size(); ++i) gidx[b.seg.size() + i] = nid_below[(size_t)b.split[i].x];
+        bwd_w[k].resize(b.pos.size());
+        for (size_t i = 0; i < b.pos.size(); ++i) bwd_w[k][i] = b.pos[i] >= 0 ? h.twidx[(size_t)b.pos[i]] : -1;
+    }
+    // the first sum into each gradient entry in a backward's order of reductions: the top layer's neurons, then
+    // hop K's strengths and the layer below's neurons, ..., hop 1's (a teaching step stores those sums)
+    auto mark = [](const std::vector<int>& idx, std::vector<unsigned char>& seen) {
+        std::vector<int> m(idx.size());
+        for (size_t i = 0; i < idx.size(); ++i) {
+            const int v = idx[i];
+            m[i] = v < 0 ? -1 : (seen[(size_t)v] ? v : -(v + 2));
+            if (v >= 0) seen[(size_t)v] = 1;
+        }
+        return m;
+    };
+    std::vector<unsigned char> wseen((size_t)std::max(n.n_w, 1), 0), nseen((size_t)std::max(n.n_neurons, 1), 0);
+    p.top_ridx = mark(n.hop[K - 1].nid, nseen);
+    for (int k = K - 1; k >= 0; --k) {
+        p.ridx[k] = mark(bwd_w[k], wseen);
+        p.gridx[k] = mark(p.gidx[k], nseen);
+    }
+    return true;
+}
+
 Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) {
     clear_error();
     if (!bytes || len < 36 || std::memcmp(bytes, "FLY1", 4) != 0) {
@@ -265,167 +431,68 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         set_error("unknown state precision");
         return nullptr;
     }
+    NetHost n;
+    if (!read_net(bytes, len, n)) return nullptr;
+    NetPlans P;
+    if (!plan_net(n, P)) {
+        set_error("row plan");
+        return nullptr;
+    }
     std::unique_ptr<Core, void (*)(Core*)> c(new Core, release);
     c->prec = prec;
-    Reader r{bytes, len, 4};
-    auto hd = r.ints(8);
-    if (!r.ok) { set_error("short network file (header)"); return nullptr; }
-    c->obs_dim = hd[0]; c->n_act = hd[1]; c->hops = hd[2]; c->n_neurons = hd[3];
-    c->n_w = hd[4]; c->n_s = hd[5]; c->fan = hd[6]; c->n_dn = hd[7];
-    if (c->obs_dim <= 0 || c->n_act <= 0 || c->hops <= 0 || c->hops > 64 || c->n_neurons <= 0 || c->n_w < 0 ||
-        c->n_s <= 0 || c->fan <= 0 || c->n_dn <= 0) {
-        set_error("bad network header");
-        return nullptr;
-    }
-    const int K = c->hops;
-    c->sizes = r.ints(K + 1);
-    c->E = r.ints(K);
-    if (!r.ok) { set_error("short network file (sizes)"); return nullptr; }
-    if (c->sizes[0] != c->n_s) { set_error("sizes[0] != n_s"); return nullptr; }
-    for (int k = 0; k <= K; ++k)
-        if (c->sizes[k] <= 0) { set_error("empty layer"); return nullptr; }
-    for (int k = 0; k < K; ++k)
-        if (c->E[k] < 0) { set_error("negative edge count"); return nullptr; }
-    c->E_in = c->n_s * c->fan;
-    auto in_crow = r.ints(c->n_s + 1), in_col = r.ints(c->E_in);
-    r.ints(c->obs_dim + 1); r.ints(c->E_in); r.ints(c->E_in);      // the plug's transposed form: not used here
-    auto n0 = r.ints(c->n_s);
-    if (!r.ok) { set_error("short network file (plug)"); return nullptr; }
-    if (!rowptr_ok(in_crow, c->E_in) || !in_range(in_col, 0, c->obs_dim) || !distinct(n0, c->n_neurons, false)) {
-        set_error("bad plug index arrays");
-        return nullptr;
-    }
-    struct HH { std::vector<int> nid, crow, col, widx, tcrow, tcol, twidx, drow; };
-    std::vector<HH> hh(K);
-    std::vector<int> edge_of;                                       // (scratch of transposes())
-    for (int k = 0; k < K; ++k) {
-        HH& h = hh[k];
-        const int rows = c->sizes[k + 1], src = c->sizes[k], E = c->E[k];
-        h.nid = r.ints(rows); h.crow = r.ints(rows + 1); h.col = r.ints(E); h.widx = r.ints(E);
-        h.tcrow = r.ints(src + 1); h.tcol = r.ints(E); h.twidx = r.ints(E); h.drow = r.ints(rows);
-        if (!r.ok) { set_error("short network file (hop " + std::to_string(k + 1) + ")"); return nullptr; }
-        bool ok = distinct(h.nid, c->n_neurons, false) && rowptr_ok(h.crow, E) && in_range(h.col, 0, src) &&
-                  distinct(h.widx, c->n_w, false) && rowptr_ok(h.tcrow, E) && in_range(h.tcol, 0, rows) &&
-                  distinct(h.twidx, c->n_w, false) && in_range(h.drow, -1, c->n_s) && distinct(h.drow, c->n_s, true);
-        if (!ok) { set_error("bad index arrays in hop " + std::to_string(k + 1)); return nullptr; }
-        if (!transposes(h.crow, h.col, h.widx, h.tcrow, h.tcol, h.twidx, c->n_w, edge_of)) {
-            set_error("hop " + std::to_string(k + 1) + ": the by-source form (tcrow, tcol, twidx) is not the transpose "
-                      "of the by-target form (crow, col, widx)");
-            return nullptr;
-        }
-    }
-    auto dn = r.ints(c->n_dn);
-    r.ints(c->n_w);                                                 // wmap: the caller's business
-    if (!r.ok) { set_error("short network file (read-out)"); return nullptr; }
-    if (!distinct(dn, c->sizes[K], false)) { set_error("bad read-out rows"); return nullptr; }
+    c->obs_dim = n.obs_dim; c->n_act = n.n_act; c->hops = n.hops; c->n_neurons = n.n_neurons;
+    c->n_w = n.n_w; c->n_s = n.n_s; c->fan = n.fan; c->n_dn = n.n_dn; c->E_in = n.E_in;
+    c->sizes = n.sizes;
+    c->E = n.E;
+    const int K = n.hops;
 
-    // plans
+    // plans on the device
     const int tq = prec ? TW16 : TW;
     const int bm = (max_batch + tq - 1) / tq * tq;
     c->maxB = bm;
     c->Tm = bm / TW;
-    HostPlan hp;
-    if (!make_plan(in_crow.data(), c->n_s, seg_cap(c->E_in), nullptr, hp) ||
-        !upload_plan(*c, hp, c->n_s, in_col, nullptr, c->pp)) {
+    if (!upload_plan(*c, P.plug, c->n_s, n.in_col, nullptr, c->pp)) {
         if (!*last_error()) set_error("plug plan");
         return nullptr;
     }
     c->in_cw = dalloc<int2>(*c, (size_t)c->pp.npos);
     long long max_slot = c->pp.nslot, max_pos = 1, max_rows = 1;
-    // The re-drive field of the transposed plans' segments, which is read by the backward only.  The backward writes
-    // the drive's gradient layer by layer from the top, so the top layer writes each of its re-drive rows first and
-    // a lower layer's row writes its re-drive row first when no layer above re-drives that row (a sensory row
-    // appears at most once per layer).  A first write starts from zero and reads nothing: its row is encoded as
-    // -(d + 3).  A sensory row that no layer re-drives reads zero: it is encoded -2 (others -1).  The gradient
-    // buffer then needs no clearing before a backward.
-    std::vector<std::vector<int>> bwd_drow(K);
-    std::vector<char> touched(c->n_s, 0);
-    for (int L = K; L >= 1; --L) {
-        const std::vector<int>& dr = hh[L - 1].drow;
-        if (L < K) {
-            bwd_drow[L - 1].resize(dr.size());
-            for (size_t r = 0; r < dr.size(); ++r)
-                bwd_drow[L - 1][r] = dr[r] >= 0 && !touched[dr[r]] ? -(dr[r] + 3) : dr[r];
-        }
-        for (int v : dr)
-            if (v >= 0) touched[v] = 1;
-    }
-    std::vector<int> sensory_drow(c->n_s);
-    for (int j = 0; j < c->n_s; ++j) sensory_drow[j] = touched[j] ? -1 : -2;
     c->hop.resize(K);
-    std::vector<std::vector<int>> bwd_w(K), bwd_n(K);   // per hop: strength per backward position, neuron per column
     for (int k = 0; k < K; ++k) {
         HopD& d = c->hop[k];
-        HH& h = hh[k];
+        HopHost& h = n.hop[k];
         d.rows = c->sizes[k + 1]; d.src = c->sizes[k]; d.E = c->E[k];
-        // the transposed plan's rows are the layer below, with their re-drive fields as above
-        const int* below_drow = k >= 1 ? bwd_drow[k - 1].data() : sensory_drow.data();
-        HostPlan f, b;
-        if (!make_plan(h.crow.data(), d.rows, seg_cap(d.E), h.drow.data(), f) ||
-            !make_plan(h.tcrow.data(), d.src, seg_cap(d.E), below_drow, b)) {
-            set_error("row plan");
+        if (!upload_plan(*c, P.fwd[k], d.rows, h.col, &h.widx, d.fp) ||
+            !upload_plan(*c, P.bwd[k], d.src, h.tcol, &h.twidx, d.bp))
             return nullptr;
-        }
-        if (!upload_plan(*c, f, d.rows, h.col, &h.widx, d.fp) || !upload_plan(*c, b, d.src, h.tcol, &h.twidx, d.bp))
-            return nullptr;
-        {   // the backward stores the layer below's gain and threshold partials in plan columns: a whole row at its
-            // segment, split row i after the segments (coalesced stores); each column's neuron, for the reduction
-            const std::vector<int>& nid_below = k >= 1 ? c->hop[k - 1].h_nid : n0;
-            d.gcols = (int)(b.seg.size() + b.split.size());
-            std::vector<int> gidx((size_t)std::max(d.gcols, 1), -1);
-            for (size_t si = 0; si < b.seg.size(); ++si)
-                if (b.seg[si].y < 0) gidx[si] = nid_below[(size_t)b.seg[si].x];
-            for (size_t i = 0; i < b.split.size(); ++i) gidx[b.seg.size() + i] = nid_below[(size_t)b.split[i].x];
-            d.gidx = upload(*c, gidx);
-            if (!d.gidx) return nullptr;
-            bwd_n[k] = std::move(gidx);
-            bwd_w[k].resize(b.pos.size());
-            for (size_t i = 0; i < b.pos.size(); ++i) bwd_w[k][i] = b.pos[i] >= 0 ? h.twidx[(size_t)b.pos[i]] : -1;
-        }
+        d.gcols = (int)P.gidx[k].size();
+        d.gidx = upload(*c, P.gidx[k]);
+        d.ridx = upload(*c, P.ridx[k]);
+        d.gridx = upload(*c, P.gridx[k]);
         d.has_drive = std::any_of(h.drow.begin(), h.drow.end(), [](int v) { return v >= 0; });
         d.pair_bwd = pair_tiles(h.crow, d.rows);
-        d.bwd_skip = bwd_skip_rows(b);
+        d.bwd_skip = bwd_skip_rows(P.bwd[k]);
         d.nid = upload(*c, h.nid);
         d.drow = upload(*c, h.drow);
         d.cw = dalloc<int2>(*c, (size_t)d.fp.npos);
         d.tcw = dalloc<int2>(*c, (size_t)d.bp.npos);
-        if (!d.nid || !d.drow || !d.cw || !d.tcw) return nullptr;
+        if (!d.gidx || !d.ridx || !d.gridx || !d.nid || !d.drow || !d.cw || !d.tcw) return nullptr;
         d.h_nid = std::move(h.nid); d.h_crow = std::move(h.crow); d.h_col = std::move(h.col); d.h_widx = std::move(h.widx);
         max_slot = std::max<long long>({max_slot, d.fp.nslot, d.bp.nslot});
         max_pos = std::max<long long>(max_pos, d.bp.npos);
         max_rows = std::max<long long>(max_rows, d.rows);
     }
-    {   // the first sum into each gradient entry in a backward's order of reductions: the top layer's neurons, then
-        // hop K's strengths and the layer below's neurons, ..., hop 1's (a teaching step stores those sums)
-        auto mark = [](const std::vector<int>& idx, std::vector<unsigned char>& seen) {
-            std::vector<int> m(idx.size());
-            for (size_t i = 0; i < idx.size(); ++i) {
-                const int v = idx[i];
-                m[i] = v < 0 ? -1 : (seen[(size_t)v] ? v : -(v + 2));
-                if (v >= 0) seen[(size_t)v] = 1;
-            }
-            return m;
-        };
-        std::vector<unsigned char> wseen((size_t)std::max<long long>(c->n_w, 1), 0),
-            nseen((size_t)std::max(c->n_neurons, 1), 0);
-        c->top_ridx = upload(*c, mark(c->hop[K - 1].h_nid, nseen));
-        if (!c->top_ridx) return nullptr;
-        for (int k = K - 1; k >= 0; --k) {
-            c->hop[k].ridx = upload(*c, mark(bwd_w[k], wseen));
-            c->hop[k].gridx = upload(*c, mark(bwd_n[k], nseen));
-            if (!c->hop[k].ridx || !c->hop[k].gridx) return nullptr;
-        }
-    }
+    c->top_ridx = upload(*c, P.top_ridx);
+    if (!c->top_ridx) return nullptr;
     std::vector<int> dn_inv(c->sizes[K], -1);
-    for (int j = 0; j < c->n_dn; ++j) dn_inv[dn[j]] = j;
-    c->in_crow = upload(*c, in_crow); c->in_col = upload(*c, in_col); c->n0 = upload(*c, n0);
-    c->dn = upload(*c, dn); c->dn_inv = upload(*c, dn_inv);
+    for (int j = 0; j < c->n_dn; ++j) dn_inv[n.dn[j]] = j;
+    c->in_crow = upload(*c, n.in_crow); c->in_col = upload(*c, n.in_col); c->n0 = upload(*c, n.n0);
+    c->dn = upload(*c, n.dn); c->dn_inv = upload(*c, dn_inv);
     c->rows_total = c->n_s;
     for (auto& d : c->hop) c->rows_total += d.rows;
-    c->h_n0 = std::move(n0);
-    c->h_dn = std::move(dn);
+    c->h_n0 = std::move(n.n0);
+    c->h_dn = std::move(n.dn);
     if (!c->in_crow || !c->in_col || !c->n0 || !c->dn || !c->dn_inv || !c->in_cw) return nullptr;
-
     // parameters: 5 sets x 7 arrays
     const long long ps[7] = {c->n_w, c->n_neurons, c->n_neurons, c->E_in, c->n_s, (long long)c->n_act * c->n_dn, c->n_act};
     long long o = 0;
@@ -1132,20 +1199,53 @@ int fc_plan_rows(const int* rowptr, int rows, int seg_max, int* wave_out, long l
         set_error("fc_plan_rows: malformed row pointer");
         return -1;
     }
-    if (counts) {
-        counts[0] = (long long)p.wave.size(); counts[1] = (long long)p.seg.size(); counts[2] = (long long)p.split.size();
-        counts[3] = p.nslot; counts[4] = (long long)p.pos.size();
-    }
-    if ((long long)p.wave.size() > wave_cap || (long long)p.seg.size() > seg_cap || (long long)p.split.size() > split_cap ||
-        (long long)p.pos.size() > pos_cap) {
-        set_error("fc_plan_rows: capacity");
+    return plan_out(p, "fc_plan_rows", wave_out, wave_cap, seg_out, seg_cap, split_out, split_cap, pos_out, pos_cap,
+                    counts);
+}
+
+int fc_net_plan(const char* net, long long len, int product, int backward, int* wave_out, long long wave_cap,
+                int* seg_out, long long seg_cap, int* split_out, long long split_cap, int* pos_out, long long pos_cap,
+                long long* counts) {
+    clear_error();
+    NetHost n;
+    NetPlans P;
+    if (!read_net(reinterpret_cast<const unsigned char*>(net), len, n)) return -1;
+    if (product < 0 || product > n.hops || backward < 0 || backward > 1 || (product == 0 && backward)) {
+        set_error("fc_net_plan: product 0 (the plug, forward only) or 1 .. hops, backward 0 or 1");
         return -1;
     }
-    if (wave_out && !p.wave.empty()) std::memcpy(wave_out, p.wave.data(), p.wave.size() * sizeof(int2));
-    if (seg_out && !p.seg.empty()) std::memcpy(seg_out, p.seg.data(), p.seg.size() * sizeof(int4));
-    if (split_out && !p.split.empty()) std::memcpy(split_out, p.split.data(), p.split.size() * sizeof(int4));
-    if (pos_out && !p.pos.empty()) std::memcpy(pos_out, p.pos.data(), p.pos.size() * sizeof(int));
-    return 0;
+    if (!plan_net(n, P)) {
+        set_error("fc_net_plan: row plan");
+        return -1;
+    }
+    const HostPlan& p = product == 0 ? P.plug : (backward ? P.bwd[product - 1] : P.fwd[product - 1]);
+    return plan_out(p, "fc_net_plan", wave_out, wave_cap, seg_out, seg_cap, split_out, split_cap, pos_out, pos_cap,
+                    counts);
+}
+
+long long fc_net_marks(const char* net, long long len, int hop, int which, int* out, long long cap) {
+    clear_error();
+    NetHost n;
+    NetPlans P;
+    if (!read_net(reinterpret_cast<const unsigned char*>(net), len, n)) return -1;
+    if (which < 0 || which > 3 || (which < 3 && (hop < 1 || hop > n.hops))) {
+        set_error("fc_net_marks: which 0 .. 2 with hop 1 .. hops, or which 3");
+        return -1;
+    }
+    if (!plan_net(n, P)) {
+        set_error("fc_net_marks: row plan");
+        return -1;
+    }
+    const std::vector<int>& v = which == 0 ? P.gidx[hop - 1] : which == 1 ? P.ridx[hop - 1]
+                                : which == 2 ? P.gridx[hop - 1] : P.top_ridx;
+    if (out) {
+        if ((long long)v.size() > cap) {
+            set_error("fc_net_marks: capacity");
+            return -1;
+        }
+        if (!v.empty()) std::memcpy(out, v.data(), v.size() * sizeof(int));
+    }
+    return (long long)v.size();
 }
 
 }  // extern "C"

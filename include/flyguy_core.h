@@ -132,6 +132,28 @@ int fc_plan_rows(const int* rowptr, int rows, int seg_max, int* wave_out, long l
                  long long seg_cap, int* split_out, long long split_cap, int* pos_out, long long pos_cap,
                  long long* counts);
 
+/* The plans a handle's kernels run, computed on the host from NET.bin bytes (no device; the network is checked as
+ * fc_create checks it).  product 0: the plug's rows (forward only; its gradient pass walks the same plan); product k
+ * = 1 .. hops: hop k, backward 0 its CSR rows (forward), backward 1 its CSC rows, i.e. the layer below (backward).
+ * Outputs as fc_plan_rows, with these differences: the segment length cap is the library's own (at least 4096
+ * segments, 16 .. 512 edges per segment); among segments of equal length, whole rows that read a line of the drive
+ * (forward: a re-drive row; backward: the drive gradient written so far) come first; the third int of a segment
+ * and the fourth of a split row are that row's re-drive field: the sensory row it re-drives (>= 0), -1 none, and in
+ * the backward -(d + 3) when its hop is the first (from the top) to write sensory row d's gradient, -2 for a sensory
+ * row that no hop re-drives.  Returns 0 or -1 (fc_last_error).  (No counterpart in the reference.) */
+int fc_net_plan(const char* net, long long len, int product, int backward, int* wave_out, long long wave_cap,
+                int* seg_out, long long seg_cap, int* split_out, long long split_cap, int* pos_out, long long pos_cap,
+                long long* counts);
+
+/* The backward's reduction tables of a network, from NET.bin bytes on the host (no device).  which 0: for hop
+ * 1 .. hops, the neuron of each gain / threshold partial column of its backward (the plan's segments, then its split
+ * rows; -1 for a segment of a split row); 1: the strength of each backward plan position, 2: the column neurons,
+ * 3: the top layer's neurons (hop ignored), each with the first write in a backward's order of reductions (top
+ * layer, then hop K's strengths and columns, down to hop 1) marked -(i + 2) for entry i, later writes i, nothing -1.
+ * Copies at most cap ints into out (null: none) and returns the length, or -1 (fc_last_error).  (No counterpart in
+ * the reference.) */
+long long fc_net_marks(const char* net, long long len, int hop, int which, int* out, long long cap);
+
 /* ---- the HopCuda-style hop (flyguy/fly_cuda.py:78-115): states [rows][B] row-major, B % 32 == 0 ---- */
 
 /* out[n_rows][B] = A h for the CSR matrix A (n_rows rows over n_src sources, E weights w in CSR order), through the

@@ -37,7 +37,7 @@ def test_cache_keeps_its_tensors_alive_and_plans_by_content():
     assert [tuple(x) for x in pb["wave"].tolist()] == want_wave            # b's own plan, not a's
     assert [tuple(x) for x in pb["seg"].tolist()] == want_seg
     pos = np.array(want_pos)
-    assert pb["pidx"].tolist() == want_pos                    # weight index = the edge itself
+    assert pb["pidx"].tolist() == want_pos.tolist()           # weight index = the edge itself
     assert pb["pcol"].tolist() == [int(cb[e]) if e >= 0 else NO_ROW for e in pos]
     assert pa["npos"] != pb["npos"] or not torch.equal(pa["pcol"], pb["pcol"])
 
