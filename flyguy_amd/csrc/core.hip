@@ -334,6 +334,26 @@ static bool read_net(const unsigned char* bytes, long long len, NetHost& n) {
             return false;
         }
     }
+    {   // a strength is one connection: in every hop that uses it, the same source and target neuron (the revive
+        // surgery and the first-write marks take a strength's neurons from any of its hops)
+        std::vector<int> src_of((size_t)std::max(n.n_w, 1), -1), dst_of((size_t)std::max(n.n_w, 1), -1);
+        for (int k = 0; k < K; ++k) {
+            const HopHost& h = n.hop[k];
+            const std::vector<int>& below = k ? n.hop[k - 1].nid : n.n0;
+            for (int t = 0; t + 1 < (int)h.crow.size(); ++t)
+                for (int e = h.crow[t]; e < h.crow[t + 1]; ++e) {
+                    const size_t wi = (size_t)h.widx[(size_t)e];
+                    const int pre = below[(size_t)h.col[(size_t)e]], post = h.nid[(size_t)t];
+                    if (dst_of[wi] < 0) {
+                        src_of[wi] = pre;
+                        dst_of[wi] = post;
+                    } else if (src_of[wi] != pre || dst_of[wi] != post) {
+                        set_error("strength " + std::to_string(wi) + " joins different neurons in different hops");
+                        return false;
+                    }
+                }
+        }
+    }
     n.dn = r.ints(n.n_dn);
     r.ints(n.n_w);                                                  // wmap: the caller's business
     if (!r.ok) { set_error("short network file (read-out)"); return false; }

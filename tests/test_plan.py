@@ -235,3 +235,18 @@ def test_net_plan_refuses_bad_arguments():
         net_plan(b"FLY0" + raw[4:], 1)
     with pytest.raises(LibraryError):
         net_marks(raw, 0, 1)
+
+
+def test_a_strength_joins_the_same_neurons_in_every_hop():
+    """A network in which one strength stands for two different connections (other source or target neuron in another
+    hop) is refused: the revive surgery and the first-write marks take a strength's neurons from any of its hops."""
+    from flyguy_amd._lib import LibraryError
+    s, _ = scaled_3hop(16)
+    h1, h2 = s["hop"][0], s["hop"][1]
+    w_new, w_old = int(h1["widx"][0]), int(h2["widx"][0])
+    h2["widx"] = np.asarray(h2["widx"]).copy()
+    h2["twidx"] = np.asarray(h2["twidx"]).copy()
+    h2["widx"][0] = w_new
+    h2["twidx"][h2["twidx"] == w_old] = w_new
+    with pytest.raises(LibraryError, match="joins different neurons"):
+        net_plan(net_bytes(s), 1)
