@@ -79,7 +79,8 @@ class _Session:
             self.handle = None
 
     def arrays(self, actor: FlyActor) -> list[torch.Tensor]:
-        """The seven arrays in the library's order, as PyTorch memory."""
+        """The PyTorch tensors the library exchanges with, in fc_copy's order: the gathered in-play strengths, gain,
+        theta, in_w, in_b, out.weight, out.bias."""
         return [self.w_play, actor.gain.data, actor.theta.data, actor.in_w.data, actor.in_b.data, actor.out.weight.data,
                 actor.out.bias.data]
 
@@ -258,8 +259,8 @@ class NativeFlyActor(FlyActor):
         self._session.transfer(which, [t.contiguous().float() for t in tensors], into_library=True)
 
     def push(self, also_average: bool = False) -> None:
-        """PyTorch's weights -> the library (after a checkpoint was loaded); also_average restarts its running
-        average from them."""
+        """Copy the actor's PyTorch parameters into the library session (needed whenever they were set from outside,
+        e.g. by load_state_dict); with also_average the library's running average is restarted from them too."""
         sess = self._session
         sess.w_play.copy_(self.w.data[sess.wmap])
         arrays = sess.arrays(self)
@@ -269,7 +270,8 @@ class NativeFlyActor(FlyActor):
         self._stale = False
 
     def pull(self) -> None:
-        """The library's weights -> PyTorch's (after every optimiser step)."""
+        """Copy the library's current weights back into the actor's PyTorch parameters (NativeAdam.step does this
+        after every update, so PyTorch-side readers see the trained values)."""
         sess = self._session
         sess.transfer(WEIGHTS, sess.arrays(self), into_library=False)
         self.w.data[sess.wmap] = sess.w_play
@@ -302,5 +304,6 @@ class NativeFlyActor(FlyActor):
 
 
 def grad_arrays(actor: NativeFlyActor) -> list[np.ndarray]:
-    """The seven gradient arrays the library has gathered since zero_grad, as numpy (for checks against PyTorch)."""
+    """Host copies (numpy, fc_copy's order) of the library's seven gradient buffers as accumulated since the last
+    zero_grad."""
     return [t.cpu().numpy() for t in actor._fetch(GRADIENT)]

@@ -167,8 +167,10 @@ def main(argv=None) -> int:
     ap.add_argument("out")
     ap.add_argument("--samples", type=int, default=512)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--passes", type=int, default=3, help="rounds of bringing the revived neurons' inputs to --target")
-    ap.add_argument("--target", type=float, default=0.4, help="input size (rms) given to a revived neuron")
+    ap.add_argument("--passes", type=int, default=3,
+                    help="survey-and-rescale rounds applied to the inputs of the neurons brought back")
+    ap.add_argument("--target", type=float, default=0.4,
+                    help="root-mean-square pre-activation each neuron brought back is scaled towards")
     args = ap.parse_args(argv)
     s = read_net(Path(args.net))
     step, P = read_params(Path(args.params), s)
@@ -179,24 +181,25 @@ def main(argv=None) -> int:
     outside[np.asarray(s["n0"])] = False                          # neurons outside the sensory layer
     dead = seen & (fired == 0) & outside
     n = len(obs)
-    print(f"native step {step:,}, {n} samples: firing share per hop {[round(v, 3) for v in share]}; KL {kl0:.4f}")
-    print(f"silent neurons (never fire in any hop): {int(dead.sum()):,} of {int((seen & outside).sum()):,} in play "
-          f"outside the sensory layer")
+    print(f"weights of step {step:,} surveyed on {n} samples | share of (neuron, sample) firing per layer "
+          f"{[round(v, 3) for v in share]} | KL {kl0:.4f}")
+    print(f"silent neurons: {int(dead.sum()):,} of the {int((seen & outside).sum()):,} hop neurons outside the sensory "
+          f"layer fire for none of the samples")
     rev = Revival(net, P, dead, args.seed)
-    print("re-signed {:,} incoming strengths, zeroed {:,} outgoing ones and the action weights of {} descending "
-          "neurons".format(*rev.counts))
+    print("surgery: {:,} strengths into silent neurons given a new sign, {:,} from them into live neurons set to 0, "
+          "read-out weights of {} silent descending neurons set to 0".format(*rev.counts))
     for k in range(args.passes + 1):
         fired2, _, rms, share2, kl = net.survey(rev.P, obs, teacher)
         still = seen & (fired2 == 0) & outside
         woke = float((fired2[dead] / n).mean()) if dead.any() else 0.0
-        print(f"   pass {k}: firing share per hop {[round(v, 3) for v in share2]}; still silent {int(still.sum()):,}; "
-              f"the revived fire {woke:.3f} of the time; KL {kl:.4f}")
+        print(f"   round {k} | firing shares {[round(v, 3) for v in share2]} | silent {int(still.sum()):,} | "
+              f"those brought back fire on {woke:.3f} of the samples | KL {kl:.4f}")
         if abs(kl - kl0) >= 1e-4 * max(1.0, abs(kl0)):
             raise SystemExit("the surgery changed the network's output")
         if k < args.passes:
             rev.rescale(rms, args.target)
     write_params(rev.P, Path(args.out), step)
-    print("wrote", args.out)
+    print(f"{args.out}: written (step {step:,})")
     return 0
 
 

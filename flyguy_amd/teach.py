@@ -71,7 +71,7 @@ class Moments:
             if ans is not None:
                 learn_t.append(ans[:keep])
                 held_t.append(ans[keep:])
-            print(f"{p.name}: {len(obs):,} moments, the last {len(obs) - keep:,} held out", flush=True)
+            print(f"{p.name}: {len(obs):,} moments read, {len(obs) - keep:,} at its end kept for scoring", flush=True)
         stride = max(1, sum(len(h) for h in held) // 4096)
         self.obs_dim = learn[0].shape[1]
         self.learn = torch.from_numpy(np.concatenate(learn))
@@ -188,9 +188,10 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=3000)
     ap.add_argument("--batch", type=int, default=128)
     ap.add_argument("--lr", type=float, default=4e-4,
-                    help="for the connection strengths and the plugs; the neurons' gains and thresholds get 0.3 of it")
+                    help="Adam rate of the strengths and the plug / read-out weights (gains and thresholds: 0.3 x this)")
     ap.add_argument("--temp", type=float, default=0.5)
-    ap.add_argument("--average", type=float, default=0.999, help="the running average of the weights that is saved and scored")
+    ap.add_argument("--average", type=float, default=0.999,
+                    help="decay of the weights' running average, the network that is scored and written out")
     ap.add_argument("--holdout", type=float, default=0.05)
     ap.add_argument("--eval-every", type=int, default=250)
     ap.add_argument("--out", type=Path, default=Path("runs") / "teach" / "student.pt")
@@ -215,8 +216,9 @@ def main(argv=None) -> int:
 
     first, first_kl = score(shown, teacher, data, args.temp, device)
     agree = first
-    print(f"start | unseen: same first choice {first:.3f}, distance {first_kl:.3f} | {len(data.learn):,} moments to "
-          f"learn from, {args.steps * args.batch / len(data.learn):.1f} passes over them", flush=True)
+    print(f"before learning | held-out moments: argmax agreement {first:.3f}, KL {first_kl:.3f} | "
+          f"{len(data.learn):,} moments to learn from over {args.steps * args.batch / len(data.learn):.1f} passes",
+          flush=True)
     began, smooth = time.time(), 0.0
     for step in range(1, args.steps + 1):
         rows = torch.as_tensor(np.sort(draw.integers(0, len(data.learn), args.batch)))
@@ -229,14 +231,14 @@ def main(argv=None) -> int:
             continue
         agree, dist = score(shown, teacher, data, args.temp, device)
         rate = step * args.batch / (time.time() - began)
-        print(f"step {step:,} | distance {smooth:.3f} | unseen: same first choice {agree:.3f}, distance {dist:.3f} | "
-              f"{rate:,.0f} moments a second", flush=True)
+        print(f"step {step:,} | KL (running) {smooth:.3f} | held-out moments: argmax agreement {agree:.3f}, KL "
+              f"{dist:.3f} | {rate:,.0f} moments/s", flush=True)
         args.out.parent.mkdir(parents=True, exist_ok=True)
         torch.save({"model": {"actor." + k: v.detach().cpu() for k, v in shown.state_dict().items()},
                     "steps": step0 + step, "taught_steps": step0 + step, "config": {"model": saved_cfg},
                     "taught_by": teacher.name, "unseen_same_first_choice": agree}, args.out)
-    print(f"saved {args.out} (the running average; the teacher's first choice on {agree:.3f} of unseen moments, "
-          f"{first:.3f} at the start)")
+    print(f"{args.out}: running average written; argmax agreement with the teacher on held-out moments "
+          f"{first:.3f} -> {agree:.3f}")
     return 0
 
 

@@ -31,7 +31,7 @@ def test_revive_tool(tmp_path, capsys):
     assert main([str(tmp_path / "net.bin"), str(tmp_path / "p.bin"), str(tmp_path / "chunk.bin"), str(tmp_path / "out.bin"),
                  "--samples", "192"]) == 0
     out = capsys.readouterr().out
-    assert "silent neurons" in out and "wrote" in out
+    assert "silent neurons" in out and ": written" in out
     s2 = read_net(tmp_path / "net.bin")
     step, Q = read_params(tmp_path / "out.bin", s2)
     assert step == 17

@@ -40,8 +40,8 @@ def _teacher(tmp_path):
 
 
 def _distances(out):
-    start = float(re.search(r"start \| unseen: same first choice [0-9.]+, distance ([0-9.]+)", out).group(1))
-    last = [float(v) for v in re.findall(r"\| unseen: same first choice [0-9.]+, distance ([0-9.]+) \|", out)][-1]
+    start = float(re.search(r"before learning \| held-out moments: argmax agreement [0-9.]+, KL ([0-9.]+)", out).group(1))
+    last = [float(v) for v in re.findall(r"\| held-out moments: argmax agreement [0-9.]+, KL ([0-9.]+) \|", out)][-1]
     return start, last
 
 
