@@ -561,6 +561,7 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     if (!c->info0 || !c->sinfo0) return nullptr;
     if (const char* f = std::getenv("FLYGUY_SKIP_SILENT")) c->skip_silent = f[0] != '0';
     if (const char* f = std::getenv("FLYGUY_PLUG_LDS")) c->plug_lds = std::min(std::max(std::atoi(f), 0), 64);
+    if (!(prec ? lds_plug_fits16() : lds_plug_fits())) c->plug_lds = 0;     // (a device with less LDS per workgroup)
     for (int l = 0; l < K; ++l) {                   // (the top layer's would have no reader)
         c->fire_bytes.push_back(dalloc<unsigned char>(*c, Tp * (size_t)fires_bytes_ld(c->sizes[l])));
         c->fire_bits.push_back(dalloc<unsigned>(*c, Tp * (size_t)fires_ld(c->sizes[l])));
@@ -685,7 +686,7 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
     const int T = B / TW;
     hipStream_t st = c.st;
     { Timed t(c, ST_OBS); FG_CHECK(launch_obs_in(obs, c.x, c.obs_dim, B, st), false); }
-    const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
+    const float *gain = c.arr(set, 1), *theta = c.arr(set, 2);
     // tables made in an earlier pass: the caches have moved on since (see the plug below)
     const bool old_tables = c.made_fpairs.same(set, c.wver[set]) && c.made_info.same(set, c.wver[set]);
     {
@@ -757,7 +758,7 @@ bool backward(Core& c, const float* dlogits, int B, bool fresh) {
     if (c.prec) return backward16(c, dlogits, B, fresh);
     const int T = B / TW, K = c.hops;
     hipStream_t st = c.st;
-    const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
+    const float *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
     float* G[7];
     for (int i = 0; i < 7; ++i) G[i] = c.arr(SET_G, i);
     {
@@ -805,14 +806,13 @@ bool backward(Core& c, const float* dlogits, int B, bool fresh) {
         const float* hbelow;
         int rows_below;
         float *ggp, *gsp;
-        const int* nid_below;
         if (k >= 2) {
             HopD& b = c.hop[k - 2];
             e.mode = 1;
             e.h = b.h; e.lh = tiled(b.rows);
             e.info = b.info;
             e.gz_out = c.gz[cur ^ 1]; e.lgz = tiled(b.rows);
-            hbelow = b.h; rows_below = b.rows; ggp = b.ggp; gsp = b.gsp; nid_below = b.nid;
+            hbelow = b.h; rows_below = b.rows; ggp = b.ggp; gsp = b.gsp;
         } else {
             e.mode = 2;
             e.h = c.h0; e.lh = tiled(c.n_s);
@@ -821,7 +821,7 @@ bool backward(Core& c, const float* dlogits, int B, bool fresh) {
             e.in_crow = c.in_crow; e.in_col = c.in_col; e.x = c.x; e.lx = tiled(c.obs_dim); e.x_rows = c.obs_dim;
             e.ginb_part = c.ginb; e.gb_ld = c.n_s;
             e.ginw_part = c.ginw; e.gw_ld = c.E_in;
-            hbelow = c.h0; rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
+            hbelow = c.h0; rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0;
         }
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = d.gcols;
         e.sinfo = d.bsinfo;
@@ -859,7 +859,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
     const int T = B / TW16;
     hipStream_t st = c.st;
     { Timed t(c, ST_OBS); FG_CHECK(launch_obs_in16(obs, s16(c.x), c.obs_dim, B, st), false); }
-    const float *W = c.arr(set, 0), *gain = c.arr(set, 1), *theta = c.arr(set, 2);
+    const float *gain = c.arr(set, 1), *theta = c.arr(set, 2);
     {
         Timed t(c, ST_PACK);
         FG_CHECK(derive_forward(c, set, true, gain, theta), false);
@@ -915,7 +915,7 @@ static bool forward16(Core& c, const float* obs, int B, float* logits, int set) 
 static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
     const int T = B / TW16, K = c.hops;
     hipStream_t st = c.st;
-    const float *W = c.arr(SET_P, 0), *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
+    const float *gain = c.arr(SET_P, 1), *theta = c.arr(SET_P, 2);
     float* G[7];
     for (int i = 0; i < 7; ++i) G[i] = c.arr(SET_G, i);
     {
@@ -962,9 +962,7 @@ static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
         e.gdrive = c.gdrive;
         e.n_s = c.n_s;
         e.skip_silent = c.skip_silent && d.bwd_skip;
-        int rows_below;
         float *ggp, *gsp;
-        const int* nid_below;
         if (k >= 2) {
             HopD& b = c.hop[k - 2];
             e.mode = 1;
@@ -972,7 +970,7 @@ static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
             e.rows = b.rows;
             e.info = b.info;
             e.gz_out = s16(c.gz[cur ^ 1]);
-            rows_below = b.rows; ggp = b.ggp; gsp = b.gsp; nid_below = b.nid;
+            ggp = b.ggp; gsp = b.gsp;
         } else {
             e.mode = 2;
             e.h = s16(c.h0);
@@ -982,7 +980,7 @@ static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
             e.in_crow = c.in_crow; e.in_col = c.in_col; e.x = s16(c.x); e.x_rows = c.obs_dim;
             e.ginb_part = c.ginb; e.gb_ld = c.n_s;
             e.ginw_part = c.ginw; e.gw_ld = c.E_in;
-            rows_below = c.n_s; ggp = c.ggp0; gsp = c.gsp0; nid_below = c.n0;
+            ggp = c.ggp0; gsp = c.gsp0;
         }
         e.ggain_part = ggp; e.gsum_part = gsp; e.gp_ld = d.gcols;
         e.sinfo = d.bsinfo;

@@ -10,6 +10,8 @@
 // uses z = (h + softplus(theta)) / gain of the stored h, the sensory layer's the stored drive, and the drive's
 // gradient collects the hops' gz before their rounding.  Float32 tensors beside them (partials, the drive's gradient)
 // use the same tiling, [T][rows][64] floats.
+#include <initializer_list>
+
 #include "half.h"
 #include "readout.h"
 
@@ -403,7 +405,6 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(gz + (size_t)tile * gz_rows * TW16), (short)0, gz_rows * 128, 0x00020000);
     float* gwp = gwpart ? gwpart + (size_t)tile * gw_ld + wv.x + lane : nullptr;
-    const bool whole = live && sg.y < 0;
     // the row's h, as stored (the weight gradient's operand), first: where the row fires on no sample of the tile its
     // g is zero, and its gathers are skipped (as in k_bwd)
     u32x4 hj = {0u, 0u, 0u, 0u};
@@ -471,7 +472,6 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
     const __amdgpu_buffer_rsrc_t rbs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(gz + (size_t)(hasb ? tb : ta) * gz_rows * TW16), (short)0, hasb ? gz_rows * 128 : 0, 0x00020000);
     float* gwp = gwpart ? gwpart + (size_t)pr * gw_ld + wv.x + lane : nullptr;
-    const bool whole = live && sg.y < 0;
     // the row's h lines first, and on a tile where the row fires on no sample its gathers are skipped (k_cbwd16)
     u32x4 hja = {0u, 0u, 0u, 0u}, hjb = {0u, 0u, 0u, 0u};
     if (live) {
@@ -627,6 +627,9 @@ hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* sr
     }
     return hipSuccess;
 }
+
+bool lds_fits(std::initializer_list<const void*> kernels);
+bool lds_plug_fits16() { return lds_fits({reinterpret_cast<const void*>(&k_cfwd16_lds)}); }
 
 hipError_t launch_fwd16c_lds(const Plan& p, const int2* cw, const unsigned short* src, int src_rows,
                              const FwdEpi16& epi, float* part, int T, int S, hipStream_t st) {

@@ -3,7 +3,7 @@
 //
 // fh_spmm_static is fh_spmm for callers that cannot allocate device memory (code under HIP graph capture, serving
 // loops that forbid allocation): its two workspaces, the packed (source, weight) pairs and the split rows' partial
-// sums, live in `scratch`, a file-scope device array of FH_STATIC_BYTES.  Every GPU the library runs on holds its
+// sums, live in `g_fh_static_ws`, a file-scope device array of FH_STATIC_BYTES.  Every GPU the library runs on holds its
 // own copy until the process ends.  Calls on one GPU share that copy, so calls that overlap on one GPU (two streams,
 // two threads) race; calls in one stream are ordered.  Nothing in it needs clearing: a call packs every pair it
 // reads and writes every partial sum before it reads it.
@@ -14,16 +14,17 @@
 
 using namespace fg;
 
-static __device__ __align__(256) unsigned char scratch[FH_STATIC_BYTES];
+static __device__ __align__(256) unsigned char g_fh_static_ws[FH_STATIC_BYTES];
 
 namespace {
 
 constexpr int MAX_DEVICES = 64;
 std::mutex g_static_mu;
-void* g_static_ptr[MAX_DEVICES] = {};      // per device: the device address of its copy of `scratch`
+void* g_static_ptr[MAX_DEVICES] = {};      // per device: the device address of its copy of g_fh_static_ws
 
-// The device address of the current device's `scratch` (looked up once per device, with that device current).  In
-// host code the array's name is only a stand-in for the symbol: kernels and copies get this address instead.
+// The device address of the current device's g_fh_static_ws (looked up once per device, with that device current:
+// a runtime lookup, no allocation; a caller that captures its calls in a graph makes one call first).  In host code
+// the array's name is only a stand-in for the symbol: kernels and copies get this address instead.
 unsigned char* static_scratch() {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
@@ -33,7 +34,7 @@ unsigned char* static_scratch() {
     std::lock_guard<std::mutex> lock(g_static_mu);
     if (!g_static_ptr[dev]) {
         void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_fh_static_ws));
         if (e != hipSuccess || !p) {
             set_error(std::string("fh_spmm_static: hipGetSymbolAddress: ") + hipGetErrorString(e));
             return nullptr;

@@ -133,6 +133,11 @@ hipError_t launch_fwd_lds(const Plan& p, const int2* cw, const float* src, int s
 // The plug's bias and per-connection gradient partials (ginb [T][gb_ld], ginw [T][gw_ld]) from the drive's complete
 // gradient gd ([T][n_s][32], left by a sensory-layer backward whose BwdEpi has no in_crow), with each tile's
 // observation slab (x_rows x 128 bytes) staged in LDS by each of its S workgroups
+// Whether the current device gives a workgroup the LDS the staged plug kernels ask for (FWD_LDS_BYTES of dynamic LDS
+// plus their own static LDS): float32 (k_fwd_lds, k_plug_bwd_lds) or bfloat16 (k_cfwd16_lds) states.  Where it does
+// not, the plug runs through launch_fwd and its gradients in the sensory finish.
+bool lds_plug_fits();
+bool lds_plug_fits16();
 hipError_t launch_plug_bwd_lds(const float* gd, const float* x, int x_rows, const int* in_crow, const int* in_col,
                                int n_s, float* ginb, long long gb_ld, float* ginw, long long gw_ld, int T, int S,
                                hipStream_t st);

@@ -9,6 +9,8 @@
 // next step are one contiguous 512-byte block in plan order (one 8-byte load per lane, issued a step ahead) and
 // reach the 8 lanes of each group through LDS; the 8 source rows are then gathered as independent 128-byte lines
 // of the tile's slab, with no branch per edge (unused positions gather NO_ROW, which reads zeros).
+#include <initializer_list>
+
 #include "device.h"
 #include "readout.h"
 
@@ -957,6 +959,23 @@ hipError_t launch_fwd_lds(const Plan& p, const int2* cw, const float* src, int s
         return hipGetLastError();
     }
     return hipSuccess;
+}
+
+// the LDS a workgroup may use on the current device against FWD_LDS_BYTES + each kernel's static LDS
+bool lds_fits(std::initializer_list<const void*> kernels) {
+    int dev = 0, cap = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cap, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return false;
+    for (const void* k : kernels) {
+        hipFuncAttributes a{};
+        if (hipFuncGetAttributes(&a, k) != hipSuccess || FWD_LDS_BYTES + a.sharedSizeBytes > (size_t)cap) return false;
+    }
+    return true;
+}
+
+bool lds_plug_fits() {
+    return lds_fits({reinterpret_cast<const void*>(&k_fwd_lds), reinterpret_cast<const void*>(&k_plug_bwd_lds)});
 }
 
 hipError_t launch_plug_bwd_lds(const float* gd, const float* x, int x_rows, const int* in_crow, const int* in_col,

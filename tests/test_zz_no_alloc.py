@@ -1,6 +1,8 @@
 """fh_spmm_static, the allocation-free variant of fh_spmm (its workspace is a static device array): bit-identical
-to fh_spmm on two calls in a row, the second smaller than the first, and a product too large for the workspace is
-refused before any device work."""
+to fh_spmm on two calls in a row, the second smaller than the first; a product too large for the workspace is
+refused before any device work; after one warm-up call (which looks up the workspace's address) a call leaves the
+device's free memory unchanged, and the call captured in a HIP graph (PyTorch's CUDAGraph) replays bit-identically
+to eager fh_spmm, with new inputs, eager work and synchronisations between the replays."""
 from __future__ import annotations
 
 import numpy as np
@@ -63,3 +65,48 @@ def test_static_workspace_refuses_a_larger_product(gpu_lib):
     with pytest.raises(LibraryError, match="static workspace"):
         call("fh_spmm_static", *_args(d), w.data_ptr(), dummy.data_ptr(), dummy.data_ptr(), n_rows, n_src, B,
              torch.cuda.current_stream().cuda_stream)
+
+
+def test_static_workspace_allocates_nothing_and_replays_in_a_graph(gpu_lib):
+    crow, col, w, n_src, n_rows = _hop(16, 1)
+    B = 128
+    d = _plan(crow, col, None, int(col.numel()))
+    assert d["nsplit"] > 0                                         # (split rows: partial sums in the workspace)
+    h = torch.empty(n_src, B, device="cuda")
+    out = torch.empty(n_rows, B, device="cuda")
+
+    def static_call():
+        call("fh_spmm_static", *_args(d), w.data_ptr(), h.data_ptr(), out.data_ptr(), n_rows, n_src, B,
+             torch.cuda.current_stream().cuda_stream)
+
+    def eager_reference():
+        want = torch.empty(n_rows, B, device="cuda")
+        cw = torch.empty(max(d["npos"], 1), 2, dtype=torch.int32, device="cuda")
+        part = torch.empty(max(d["nslot"] * B, 1), device="cuda")
+        call("fh_spmm", *_args(d), w.data_ptr(), h.data_ptr(), want.data_ptr(), n_rows, n_src, B, cw.data_ptr(),
+             part.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        return want
+
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    h.copy_(torch.randn(n_src, B, device="cuda", generator=gen))
+    say("fh_spmm_static: warm-up call, then free device memory across a call")
+    static_call()                                                  # (looks up the workspace's address)
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info()[0]
+    static_call()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free_before
+    assert torch.equal(out, eager_reference())
+    say("fh_spmm_static: captured in a graph, three replays")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_call()
+    for i in range(3):
+        h.copy_(torch.randn(n_src, B, device="cuda", generator=gen))
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = eager_reference()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
