@@ -17,7 +17,8 @@ struct DevPlan {
     int *pcol = nullptr, *pidx = nullptr;      // per position: source row and weight index (-1: no edge)
     int nwave = 0, nseg = 0, nsplit = 0, nslot = 0, rows = 0;
     long long npos = 0;
-    Plan view() const { return Plan{wave, nwave, seg, nseg, split, nsplit, rows, nslot, npos}; }
+    int pb = 8;                                 // pair storage (Plan::pb)
+    Plan view() const { return Plan{wave, nwave, seg, nseg, split, nsplit, rows, nslot, npos, pb}; }
 };
 
 struct HopD {

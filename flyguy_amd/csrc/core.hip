@@ -124,11 +124,25 @@ static T* upload(Core& c, const std::vector<T>& v) {
     }
     return p;
 }
+// How a plan's pairs are stored (Plan::pb): in 6 bytes when the state its product gathers has at most PAIR6_MAX_ROWS
+// rows and its waves walk 3 steps or more on average, else in 8.  Every tile reads the pairs again, and 6-byte
+// pairs cut that stream by a quarter: float32 forward 3.062 -> 3.013 ms, teaching step 6.975 -> 6.914 ms at B=4096.
+// A wave of one or two steps waits for its first pairs before any gather, and the 6-byte form's unpacking lies on
+// that path: the plug (2 steps a wave) took 0.160 -> 0.163 ms and hop 3's backward (1.4) 0.513 -> 0.519 ms with them,
+// so those keep 8 bytes.  FLYGUY_PAIR_BYTES=8 keeps every plan at 8 bytes (the results are the same bit for bit).
+static int pair_storage(int gathered_rows, const HostPlan& h) {
+    if (const char* f = std::getenv("FLYGUY_PAIR_BYTES"))
+        if (std::atoi(f) == 8) return 8;
+    const long long steps = (long long)h.pos.size() / 64, waves = (long long)h.wave.size();
+    return gathered_rows <= PAIR6_MAX_ROWS && steps >= 3 * waves ? 6 : 8;
+}
+
 // the plan on the device, with its positions resolved through col (source rows) and idx (weight index of a CSR edge;
-// nullptr: the edge itself)
+// nullptr: the edge itself); gathered: the rows of the state its product gathers
 static bool upload_plan(Core& c, const HostPlan& h, int rows, const std::vector<int>& col, const std::vector<int>* idx,
-                        DevPlan& d) {
+                        int gathered, DevPlan& d) {
     d.rows = rows;
+    d.pb = pair_storage(gathered, h);
     d.nwave = (int)h.wave.size();
     d.nseg = (int)h.seg.size();
     d.nsplit = (int)h.split.size();
@@ -471,19 +485,19 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     const int bm = (max_batch + tq - 1) / tq * tq;
     c->maxB = bm;
     c->Tm = bm / TW;
-    if (!upload_plan(*c, P.plug, c->n_s, n.in_col, nullptr, c->pp)) {
+    if (!upload_plan(*c, P.plug, c->n_s, n.in_col, nullptr, c->obs_dim, c->pp)) {
         if (!*last_error()) set_error("plug plan");
         return nullptr;
     }
-    c->in_cw = dalloc<int2>(*c, (size_t)c->pp.npos);
+    c->in_cw = dalloc<int2>(*c, (size_t)(pair_bytes(c->pp.npos, c->pp.pb) / 8));
     long long max_slot = c->pp.nslot, max_pos = 1, max_rows = 1;
     c->hop.resize(K);
     for (int k = 0; k < K; ++k) {
         HopD& d = c->hop[k];
         HopHost& h = n.hop[k];
         d.rows = c->sizes[k + 1]; d.src = c->sizes[k]; d.E = c->E[k];
-        if (!upload_plan(*c, P.fwd[k], d.rows, h.col, &h.widx, d.fp) ||
-            !upload_plan(*c, P.bwd[k], d.src, h.tcol, &h.twidx, d.bp))
+        if (!upload_plan(*c, P.fwd[k], d.rows, h.col, &h.widx, d.src, d.fp) ||
+            !upload_plan(*c, P.bwd[k], d.src, h.tcol, &h.twidx, d.rows, d.bp))
             return nullptr;
         d.gcols = (int)P.gidx[k].size();
         d.gidx = upload(*c, P.gidx[k]);
@@ -494,8 +508,8 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         d.bwd_skip = bwd_skip_rows(P.bwd[k]);
         d.nid = upload(*c, h.nid);
         d.drow = upload(*c, h.drow);
-        d.cw = dalloc<int2>(*c, (size_t)d.fp.npos);
-        d.tcw = dalloc<int2>(*c, (size_t)d.bp.npos);
+        d.cw = dalloc<int2>(*c, (size_t)(pair_bytes(d.fp.npos, d.fp.pb) / 8));
+        d.tcw = dalloc<int2>(*c, (size_t)(pair_bytes(d.bp.npos, d.bp.pb) / 8));
         if (!d.gidx || !d.ridx || !d.gridx || !d.nid || !d.drow || !d.cw || !d.tcw) return nullptr;
         d.h_nid = std::move(h.nid); d.h_crow = std::move(h.crow); d.h_col = std::move(h.col); d.h_widx = std::move(h.widx);
         max_slot = std::max<long long>({max_slot, d.fp.nslot, d.bp.nslot});
@@ -626,10 +640,10 @@ static hipError_t rowinfo(Core& c, const float* gain, const float* theta, const 
 static hipError_t pack(Core& c, int set, bool transposed, bool bf16w) {
     std::vector<PackJob> j;
     const float* W = c.arr(set, 0);
-    if (!transposed) j.push_back({c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos});
+    if (!transposed) j.push_back({c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos, c.pp.pb});
     for (auto& d : c.hop)
-        j.push_back(transposed ? PackJob{d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos}
-                               : PackJob{d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos});
+        j.push_back(transposed ? PackJob{d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos, d.bp.pb}
+                               : PackJob{d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos, d.fp.pb});
     hipError_t e = hipSuccess;
     for (size_t k = 0; k < j.size() && e == hipSuccess; k += PACK_JOBS)
         e = launch_pack_n(j.data() + k, (int)std::min<size_t>(PACK_JOBS, j.size() - k), c.st, bf16w);
@@ -712,7 +726,7 @@ bool forward(Core& c, const float* obs, int B, float* logits, int set) {
             // XCD's L2 first took repeated forwards at B=4096 from 3.085 to 3.071 ms (the plug with the read from
             // 0.183 to 0.167 ms); in a teaching step it would only cost its launch.
             TouchJob tj;
-            tj.p[0] = reinterpret_cast<const uint4*>(c.in_cw); tj.n[0] = c.pp.npos / 2;
+            tj.p[0] = reinterpret_cast<const uint4*>(c.in_cw); tj.n[0] = pair_bytes(c.pp.npos, c.pp.pb) / 16;
             tj.p[1] = reinterpret_cast<const uint4*>(c.sinfo0); tj.n[1] = c.pp.nseg;
             tj.p[2] = reinterpret_cast<const uint4*>(c.pp.seg); tj.n[2] = c.pp.nseg;
             tj.p[3] = reinterpret_cast<const uint4*>(c.pp.wave); tj.n[3] = c.pp.nwave / 2;

@@ -99,6 +99,7 @@ __device__ __forceinline__ void fwd_finish16(const FwdEpi16& e, int t, int tile,
 
 // the plug or one hop over its row plan (as k_fwd); split rows leave float32 partials [T][nslot][64]
 // src_fires: the source layer's firing bitmaps (k_fires_pack, fw_ld words per tile; fw_ld 0: none)
+template <int PB>
 __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ cw, const bf16_t* __restrict__ src,
                                                int src_rows, FwdEpi16 epi, float* __restrict__ part, int T, int RB,
                                                const unsigned* __restrict__ src_fires, int fw_ld) {
@@ -111,8 +112,8 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
     const bool wok = load_wave(p, w, wv);
-    const int2* q = cw + wv.x + lane;
-    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    const PairLoad<PB> q(cw, wv.x, lane);
+    int2 nxt = (wok && wv.y > 0) ? q.step(0) : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -121,15 +122,17 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     FwdIn16 in{};
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
-        if (bits) drop_silent(nxt, fires, src_rows);   // a silent source row adds zeros: its gather reads NO_ROW
         int c[8];
         float wt[8];
-        stage8(slots[grp], sub, nxt, c, wt);
+        // (a silent source row adds zeros: its gather reads NO_ROW)
+        if constexpr (PB == 8)                 // (6-byte pairs: stage_pairs drops them)
+            if (bits) drop_silent(nxt, fires, src_rows);
+        stage_pairs<PB>(slots, grp, sub, nxt, bits, fires, src_rows, c, wt);
         u32x4 raw[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) raw[s] = s < left ? gather16(rs, c[s], sub) : u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
-        if (left > 8) nxt = q[64 * (j + 1)];
+        if (left > 8) nxt = q.step(j + 1);
         if (j == 0 && whole) {                 // the row's own inputs after the first gathers; the bias starts the sum
             fwd_inputs16(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub, in);
             if (epi.bias) {
@@ -162,6 +165,7 @@ __global__ __launch_bounds__(WG) void k_cfwd16(Plan p, const int2* __restrict__ 
 // The plug with the tile's observation slab (src_rows lines of 64 bfloat16 samples) staged in LDS, as k_fwd_lds:
 // the same sums as k_cfwd16, plan waves walked by each wave with the next one's loads requested before the
 // previous one's stores.  No re-drive rows.
+template <int PB>
 __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_cfwd16_lds(Plan p, const int2* __restrict__ cw,
                                                                const bf16_t* __restrict__ src, int src_rows,
                                                                FwdEpi16 epi, float* __restrict__ part, int T, int S) {
@@ -188,7 +192,7 @@ __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_cfwd16_lds(Plan p, const in
         const int2 v = make_int2(__builtin_amdgcn_readlane(wrec.x, k), __builtin_amdgcn_readlane(wrec.y, k));
         it.wok = v.x >= 0 && v.y >= 0 && (long long)v.x + 64 * (((long long)v.y + 7) / 8) <= p.npos;
         it.wv = it.wok ? v : make_int2(0, 0);
-        it.pr = (it.wok && it.wv.y > 0) ? cw[it.wv.x + lane] : make_int2(NO_ROW, 0);
+        it.pr = (it.wok && it.wv.y > 0) ? PairLoad<PB>(cw, it.wv.x, lane).step(0) : make_int2(NO_ROW, 0);
         it.live = load_segment(p, it.w * 8 + gi, it.sg) && it.wok;
         it.rec = epi.sinfo && it.w * 8 + gi < p.nseg ? epi.sinfo[it.w * 8 + gi] : make_float4(0.f, 0.f, 0.f, 0.f);
     };
@@ -198,13 +202,13 @@ __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_cfwd16_lds(Plan p, const in
         const bool whole = cur.live && cur.sg.y < 0;
         const float b = whole && epi.bias ? (epi.sinfo ? cur.rec.w : epi.bias[cur.sg.x]) : 0.f;
         float acc[8] = {b, b, b, b, b, b, b, b};            // (the bias starts the sum)
-        const int2* q = cw + cur.wv.x + lane;
+        const PairLoad<PB> q(cw, cur.wv.x, lane);
         int2 nxt = cur.pr;
         for (int j = 0, left = cur.wok ? cur.wv.y : 0; left > 0; ++j, left -= 8) {
             int c[8];
             float wt[8];
-            stage8(slots[grp], sub, nxt, c, wt);
-            if (left > 8) nxt = q[64 * (j + 1)];
+            stage_pairs<PB>(slots, grp, sub, nxt, false, nullptr, src_rows, c, wt);
+            if (left > 8) nxt = q.step(j + 1);
             u32x4 raw[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u)
@@ -387,7 +391,7 @@ __device__ __forceinline__ void bwd_finish16(const BwdEpi16& e, int j, int tile,
 
 // over the transposed plan (rows = the layer below, j): gh_j = sum W gz (gathered), the per-edge weight gradient
 // partial sum over the tile of gz * h_j, then the layer's neuron backward
-template <int MODE>
+template <int MODE, int PB>
 __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ cw, const bf16_t* __restrict__ gz,
                                                int gz_rows, float* __restrict__ gwpart, long long gw_ld, BwdEpi16 epi,
                                                float* __restrict__ part, int T, int RB) {
@@ -398,8 +402,8 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
     const bool wok = load_wave(p, w, wv);
-    const int2* q = cw + wv.x + lane;
-    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    const PairLoad<PB> q(cw, wv.x, lane);
+    int2 nxt = (wok && wv.y > 0) ? q.step(0) : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -417,13 +421,13 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
         constexpr bool FULL = decltype(full)::value;
         int c[8];
         float wt[8];
-        stage8(slots[grp], sub, nxt, c, wt);
+        stage_pairs<PB>(slots, grp, sub, nxt, false, nullptr, gz_rows, c, wt);
         u32x4 raw[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s)
             raw[s] = (FULL || s < left) ? gather16(rs, quiet ? NO_ROW : c[s], sub) : u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (FULL) nxt = q[64 * (j + 1)];
+        if constexpr (FULL) nxt = q.step(j + 1);
         if (gwp && j > 0) gwp[64 * (j - 1)] = pend;
         __builtin_amdgcn_sched_barrier(0);
         float d[8];
@@ -450,7 +454,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16(Plan p, const int2* __restrict__ 
 // The same over two tiles at once, tiles 2 pr and 2 pr + 1 of a pair pr (the second may not exist): a step gathers
 // the source lines of both tiles for the same (source, weight) pairs, and the weight-gradient partial of a position is
 // summed over both tiles (tile 2 pr first) and stored once per pair: gwpart [ceil(T / 2)][gw_ld]
-template <int MODE>
+template <int MODE, int PB>
 __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict__ cw, const bf16_t* __restrict__ gz,
                                                  int gz_rows, float* __restrict__ gwpart, long long gw_ld, BwdEpi16 epi,
                                                  float* __restrict__ part, int T, int RB) {
@@ -463,8 +467,8 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
     const bool wok = load_wave(p, w, wv);
-    const int2* q = cw + wv.x + lane;
-    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    const PairLoad<PB> q(cw, wv.x, lane);
+    int2 nxt = (wok && wv.y > 0) ? q.step(0) : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
@@ -487,7 +491,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
         constexpr bool FULL = decltype(full)::value;
         int c[8];
         float wt[8];
-        stage8(slots[grp], sub, nxt, c, wt);
+        stage_pairs<PB>(slots, grp, sub, nxt, false, nullptr, gz_rows, c, wt);
         u32x4 va[8], vb[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s)
@@ -496,7 +500,7 @@ __global__ __launch_bounds__(WG) void k_cbwd16x2(Plan p, const int2* __restrict_
         for (int s = 0; s < 8; ++s)
             vb[s] = (FULL || s < left) ? gather16(rbs, quiet_b ? NO_ROW : c[s], sub) : u32x4{0u, 0u, 0u, 0u};
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (FULL) nxt = q[64 * (j + 1)];
+        if constexpr (FULL) nxt = q.step(j + 1);
         if (gwp && j > 0) gwp[64 * (j - 1)] = pend;
         __builtin_amdgcn_sched_barrier(0);
         float d[8];
@@ -613,11 +617,17 @@ hipError_t launch_obs_in16(const float* obs, unsigned short* x, int obs_dim, int
 
 hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* src, int src_rows, const FwdEpi16& epi,
                          float* part, int T, hipStream_t st, const unsigned* src_fires) {
+    // (6-byte pairs: a slab of at most PAIR6_MAX_ROWS rows, as launch_fwd)
+    if ((p.pb != 8 && p.pb != 6) || (p.pb == 6 && src_rows > PAIR6_MAX_ROWS)) return hipErrorInvalidValue;
     if (p.nwave > 0) {
         const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
         const int fw = src_fires && fires_ld(src_rows) <= FIRES_LDS_WORDS ? fires_ld(src_rows) : 0;
-        k_cfwd16<<<(unsigned)((long long)T * RB), WG, (size_t)(fw > 0 ? fw - 4 : 0) * 4, st>>>(
-            p, cw, src, src_rows, epi, part, T, RB, src_fires, fw);
+        const dim3 grid((unsigned)((long long)T * RB));
+        const size_t lds = (size_t)(fw > 0 ? fw - 4 : 0) * 4;
+        if (p.pb == 6)
+            k_cfwd16<6><<<grid, WG, lds, st>>>(p, cw, src, src_rows, epi, part, T, RB, src_fires, fw);
+        else
+            k_cfwd16<8><<<grid, WG, lds, st>>>(p, cw, src, src_rows, epi, part, T, RB, src_fires, fw);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -629,19 +639,27 @@ hipError_t launch_fwd16c(const Plan& p, const int2* cw, const unsigned short* sr
 }
 
 bool lds_fits(std::initializer_list<const void*> kernels);
-bool lds_plug_fits16() { return lds_fits({reinterpret_cast<const void*>(&k_cfwd16_lds)}); }
+bool lds_plug_fits16() {
+    return lds_fits({reinterpret_cast<const void*>(&k_cfwd16_lds<8>), reinterpret_cast<const void*>(&k_cfwd16_lds<6>)});
+}
 
 hipError_t launch_fwd16c_lds(const Plan& p, const int2* cw, const unsigned short* src, int src_rows,
                              const FwdEpi16& epi, float* part, int T, int S, hipStream_t st) {
     const size_t lds = (size_t)src_rows * 128;
-    if (S < 1 || src_rows < 1 || lds > FWD_LDS_BYTES || epi.drive || !epi.info) return hipErrorInvalidValue;
+    if (S < 1 || src_rows < 1 || lds > FWD_LDS_BYTES || epi.drive || !epi.info || (p.pb != 8 && p.pb != 6) ||
+        (p.pb == 6 && src_rows > PAIR6_MAX_ROWS))
+        return hipErrorInvalidValue;
     S = std::max(S, (p.nwave + 64 * FWD_LDS_NW - 1) / (64 * FWD_LDS_NW));     // (at most 64 plan waves per wave)
     if (p.nwave > 0) {
-        const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_cfwd16_lds),   // (k_fwd_lds)
-                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
-        if (attr != hipSuccess) return attr;
-        k_cfwd16_lds<<<(unsigned)((long long)T * S), FWD_LDS_NW * 64, lds, st>>>(p, cw, (const bf16_t*)src, src_rows,
-                                                                                   epi, part, T, S);
+        const void* k =
+            p.pb == 6 ? reinterpret_cast<const void*>(&k_cfwd16_lds<6>) : reinterpret_cast<const void*>(&k_cfwd16_lds<8>);
+        const hipError_t attr = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
+        if (attr != hipSuccess) return attr;       // (k_fwd_lds)
+        const dim3 grid((unsigned)((long long)T * S));
+        if (p.pb == 6)
+            k_cfwd16_lds<6><<<grid, FWD_LDS_NW * 64, lds, st>>>(p, cw, (const bf16_t*)src, src_rows, epi, part, T, S);
+        else
+            k_cfwd16_lds<8><<<grid, FWD_LDS_NW * 64, lds, st>>>(p, cw, (const bf16_t*)src, src_rows, epi, part, T, S);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -652,18 +670,28 @@ hipError_t launch_fwd16c_lds(const Plan& p, const int2* cw, const unsigned short
     return hipSuccess;
 }
 
+template <int MODE, int PB>
+static void launch_bwd16c_kernel(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
+                                 long long gw_ld, const BwdEpi16& epi, float* part, int T, bool pair, hipStream_t st) {
+    const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
+    // a hop layer may take two tiles per workgroup; the sensory layer's epilogue leaves no VGPRs for a second
+    if (MODE == 1 && pair)
+        k_cbwd16x2<1, PB><<<(unsigned)((long long)((T + 1) / 2) * RB), WG, 0, st>>>(p, cw, gz, gz_rows, gwpart, gw_ld,
+                                                                                   epi, part, T, RB);
+    else
+        k_cbwd16<MODE, PB><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T,
+                                                                        RB);
+}
+
 template <int MODE>
 static hipError_t launch_bwd16c_as(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
                                    long long gw_ld, const BwdEpi16& epi, float* part, int T, bool pair, hipStream_t st) {
+    if ((p.pb != 8 && p.pb != 6) || (p.pb == 6 && gz_rows > PAIR6_MAX_ROWS)) return hipErrorInvalidValue;
     if (p.nwave > 0) {
-        const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
-        // a hop layer may take two tiles per workgroup; the sensory layer's epilogue leaves no VGPRs for a second
-        if (MODE == 1 && pair)
-            k_cbwd16x2<1><<<(unsigned)((long long)((T + 1) / 2) * RB), WG, 0, st>>>(p, cw, gz, gz_rows, gwpart, gw_ld,
-                                                                                    epi, part, T, RB);
+        if (p.pb == 6)
+            launch_bwd16c_kernel<MODE, 6>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, pair, st);
         else
-            k_cbwd16<MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T,
-                                                                         RB);
+            launch_bwd16c_kernel<MODE, 8>(p, cw, gz, gz_rows, gwpart, gw_ld, epi, part, T, pair, st);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -143,6 +143,66 @@ __device__ __forceinline__ void drop_silent(int2& pair, const unsigned* lds, int
     if (r >= (unsigned)src_rows || !((lds[r >> 5] >> (r & 31)) & 1u)) pair.x = NO_ROW;
 }
 
+// The 8 bytes a lane loads of each step's pairs (Plan::pb).  PB 8: the pair of its own slot (position woff + 64 j +
+// lane).  PB 6: bytes 8 lane .. 8 lane + 7 of the step's 384-byte block (lanes 0-31 two weights each, lanes 32-47
+// four sources each; lanes 48-63 load nothing).  woff is a multiple of 64, so a block starts on a 128-byte boundary.
+template <int PB>
+struct PairLoad {
+    const int2* q;
+    bool on;
+    __device__ __forceinline__ PairLoad(const int2* cw, int woff, int lane) {
+        if constexpr (PB == 8) {
+            q = cw + woff + lane;
+            on = true;
+        } else {
+            q = cw + (size_t)woff / 64 * 48 + lane;
+            on = lane < 48;
+        }
+    }
+    __device__ __forceinline__ int2 step(int j) const {
+        if constexpr (PB == 8) return q[64 * j];
+        return on ? q[48 * j] : make_int2(0, 0);
+    }
+};
+
+// A step's pairs from the lanes' loads to each 8-lane group: c[s], w[s] = source and weight of the group's slot s.
+// slots: the workgroup's staging, 64 int2 per wave (slots[grp] is group grp's 8).  bits: fires holds the source
+// layer's firing bits of the tile (in LDS); then a silent source (or one outside src_rows) becomes NO_ROW (PB 6; with
+// 8-byte pairs the caller drops it from the lane's own pair before, drop_silent).
+// PB 8 hands the pairs round within each group (stage8).  PB 6 writes the lanes' 8-byte pieces of the block to the
+// wave's 512 bytes of staging, and each group reads its 8 weights (two 16-byte reads) and 8 sources (one); an unused
+// slot's source reads 0xFFFF, which lies past every slab of at most PAIR6_MAX_ROWS rows.  Silent sources are found
+// after the staging there: lane s of a group tests the group's slot s and a ballot shares the 8 answers.
+template <int PB>
+__device__ __forceinline__ void stage_pairs(int2 (*slots)[LPR], int grp, int sub, int2 my, bool bits,
+                                            const unsigned* fires, int src_rows, int (&c)[8], float (&w)[8]) {
+    if constexpr (PB == 8) {
+        stage8(slots[grp], sub, my, c, w);
+    } else {
+        int2* wb = slots[grp & ~7];
+        const int g = grp & 7, lane = (g << 3) | sub;
+        wb[lane] = my;
+        __builtin_amdgcn_wave_barrier();
+        const int4* q = reinterpret_cast<const int4*>(wb);
+        const int4 a = q[2 * g], b = q[2 * g + 1], s = q[16 + g];
+        w[0] = __int_as_float(a.x); w[1] = __int_as_float(a.y); w[2] = __int_as_float(a.z); w[3] = __int_as_float(a.w);
+        w[4] = __int_as_float(b.x); w[5] = __int_as_float(b.y); w[6] = __int_as_float(b.z); w[7] = __int_as_float(b.w);
+        c[0] = s.x & 0xFFFF; c[1] = (int)((unsigned)s.x >> 16);
+        c[2] = s.y & 0xFFFF; c[3] = (int)((unsigned)s.y >> 16);
+        c[4] = s.z & 0xFFFF; c[5] = (int)((unsigned)s.z >> 16);
+        c[6] = s.w & 0xFFFF; c[7] = (int)((unsigned)s.w >> 16);
+        if (bits) {
+            const unsigned r = reinterpret_cast<const unsigned short*>(wb)[128 + lane];     // the lane's own slot
+            const bool alive = r < (unsigned)src_rows && ((fires[r >> 5] >> (r & 31)) & 1u);
+            const unsigned gm = (unsigned)(__ballot(alive) >> (lane & 56)) & 0xFFu;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (!((gm >> k) & 1u)) c[k] = NO_ROW;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 // Reduce-scatter over the 8 lanes of a group: lane s ends with the sum over the group's lanes of d[s].  Three
 // butterfly steps, each pairing lanes that hold the same set of slots and keeping the half named by a lane bit:
 // lanes i and 7-i (row_half_mirror) split the slots by bit 2, then i and i^2, then i and i^1 (quad perms).

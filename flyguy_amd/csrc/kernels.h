@@ -26,6 +26,10 @@ inline Lay plain(int B) { return Lay{TW, B}; }                          // [rows
 //   split[k] = {row, first slot, number of segments, 0} of a split row; its partial sums are added in segment order
 // rows / nslot / npos bound what the plan may name: a wave or segment outside them is skipped (the library's own
 // plans never are; the bounds guard plans handed in through the fh_* entry points).
+// pb: how the pairs are stored.  8: an int2 (source, float bits) per position, as above.  6 (a tiled product whose
+// gathered state has at most 65,535 rows): per block of 64 positions (one wave's step) the 64 float weights (256 bytes)
+// and then the 64 sources as 16-bit indices (128 bytes), 0xFFFF where no edge is; 384 bytes a step instead of 512.
+// Every tile of a pass reads a product's pairs again, so they are a large share of what its gathers fetch past the L2.
 struct Plan {
     const int2* wave = nullptr;
     int nwave = 0;
@@ -36,7 +40,12 @@ struct Plan {
     int rows = 0;
     int nslot = 0;
     long long npos = 0;
+    int pb = 8;
 };
+// the bytes the pairs of npos positions take
+inline long long pair_bytes(long long npos, int pb) { return npos * (pb == 6 ? 6 : 8); }
+// the largest gathered state (rows) whose products may store their pairs in 6 bytes (0xFFFF names no row)
+constexpr int PAIR6_MAX_ROWS = 65535;
 
 // A source index that no slab reaches: as a buffer offset (index * 128 B) it lies past every slab, so a buffer load
 // of it returns zeros without touching memory; a masked global load of it is skipped.
@@ -110,6 +119,7 @@ struct PackJob {
     const float* w = nullptr;
     int2* cw = nullptr;
     long long n = 0;
+    int pb = 8;                       // the plan's pair storage (Plan::pb); 6 takes n a multiple of 64
 };
 constexpr int PACK_JOBS = 4;
 hipError_t launch_pack_n(const PackJob* jobs, int n, hipStream_t st, bool bf16w = false);

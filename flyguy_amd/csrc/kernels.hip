@@ -62,6 +62,12 @@ __global__ __launch_bounds__(WG) void k_pack(JobTable<PackJob, PACK_JOBS> t) {
     const int i = J.pidx[p];
     float v = i >= 0 ? J.w[i] : 0.f;
     if (BF16W) v = (float)(__bf16)v;
+    if (J.pb == 6) {                            // (Plan::pb) the weight plane, then the source plane of the step
+        unsigned char* blk = reinterpret_cast<unsigned char*>(J.cw) + (size_t)(p >> 6) * 384;
+        reinterpret_cast<float*>(blk)[p & 63] = v;
+        reinterpret_cast<unsigned short*>(blk + 256)[p & 63] = i >= 0 ? (unsigned short)J.pcol[p] : (unsigned short)0xFFFF;
+        return;
+    }
     J.cw[p] = i >= 0 ? make_int2(J.pcol[p], __float_as_int(v)) : make_int2(NO_ROW, 0);
 }
 
@@ -109,7 +115,7 @@ __device__ __forceinline__ void fwd_finish(const FwdEpi& e, int t, int tile, int
     }
 }
 
-template <bool TILED>
+template <bool TILED, int PB>
 __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw, const float* __restrict__ src, Lay ls,
                                             int src_rows, FwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB,
                                             const unsigned* __restrict__ src_fires, int fw_ld) {
@@ -122,8 +128,8 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
     const bool wok = load_wave(p, w, wv);
-    const int2* q = cw + wv.x + lane;
-    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    const PairLoad<PB> q(cw, wv.x, lane);
+    int2 nxt = (wok && wv.y > 0) ? q.step(0) : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     const Slab<TILED> slab(src + (size_t)tile * ls.tile, ls.row, src_rows, sub);
@@ -135,16 +141,18 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
     // complete in order, so requested earlier they would hold up the first gathers.  The bias still starts the sum
     // (flyguy_train.cu:75).
     for (int j = 0, left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
-        if (bits) drop_silent(nxt, fires, src_rows);   // a silent source row adds zeros: its gather reads NO_ROW
         int c[8];
         float wt[8];
-        stage8(slots[grp], sub, nxt, c, wt);
+        // (a silent source row adds zeros: its gather reads NO_ROW)
+        if constexpr (PB == 8)                 // (6-byte pairs: stage_pairs drops them)
+            if (bits) drop_silent(nxt, fires, src_rows);
+        stage_pairs<PB>(slots, grp, sub, nxt, bits, fires, src_rows, c, wt);
         float4 v[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(c[s], sub) : splat(0.f);
         // the next step's pairs are requested after this step's gathers, so the gathers do not wait for them
         __builtin_amdgcn_sched_barrier(0);
-        if (left > 8) nxt = q[64 * (j + 1)];
+        if (left > 8) nxt = q.step(j + 1);
         if (j == 0 && whole) {
             in = fwd_inputs(epi, epi.sinfo ? epi.sinfo + 8 * w : nullptr, grp & 7, sg.z, tile, sub);
             if (epi.bias) acc = splat(epi.sinfo ? in.b : epi.bias[sg.x]);
@@ -173,6 +181,7 @@ __global__ __launch_bounds__(WG) void k_fwd(Plan p, const int2* __restrict__ cw,
 // Stores count in the same vector-memory counter as loads, so a load issued after a store is waited for only
 // once the store is done: each plan wave's records and first pairs are therefore requested before the previous
 // plan wave's stores.  No re-drive rows (the plug has none).
+template <int PB>
 __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_fwd_lds(Plan p, const int2* __restrict__ cw,
                                                             const float* __restrict__ src, int src_rows, FwdEpi epi,
                                                             float* __restrict__ part, Lay lp, int T, int S) {
@@ -201,7 +210,7 @@ __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_fwd_lds(Plan p, const int2*
         const int2 v = make_int2(__builtin_amdgcn_readlane(wrec.x, k), __builtin_amdgcn_readlane(wrec.y, k));
         it.wok = v.x >= 0 && v.y >= 0 && (long long)v.x + 64 * (((long long)v.y + 7) / 8) <= p.npos;
         it.wv = it.wok ? v : make_int2(0, 0);
-        it.pr = (it.wok && it.wv.y > 0) ? cw[it.wv.x + lane] : make_int2(NO_ROW, 0);
+        it.pr = (it.wok && it.wv.y > 0) ? PairLoad<PB>(cw, it.wv.x, lane).step(0) : make_int2(NO_ROW, 0);
         it.live = load_segment(p, it.w * 8 + gi, it.sg) && it.wok;
         it.rec = epi.sinfo && it.w * 8 + gi < p.nseg ? epi.sinfo[it.w * 8 + gi] : splat(0.f);
     };
@@ -211,13 +220,13 @@ __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_fwd_lds(Plan p, const int2*
         const bool whole = cur.live && cur.sg.y < 0;
         float4 acc = splat(0.f);
         if (whole && epi.bias) acc = splat(epi.sinfo ? cur.rec.w : epi.bias[cur.sg.x]);   // (the bias starts the sum)
-        const int2* q = cw + cur.wv.x + lane;
+        const PairLoad<PB> q(cw, cur.wv.x, lane);
         int2 nxt = cur.pr;
         for (int j = 0, left = cur.wok ? cur.wv.y : 0; left > 0; ++j, left -= 8) {
             int c[8];
             float wt[8];
-            stage8(slots[grp], sub, nxt, c, wt);
-            if (left > 8) nxt = q[64 * (j + 1)];
+            stage_pairs<PB>(slots, grp, sub, nxt, false, nullptr, src_rows, c, wt);
+            if (left > 8) nxt = q.step(j + 1);
             float4 v[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u)
@@ -504,7 +513,7 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
     }
 }
 
-template <bool TILED, int MODE>
+template <bool TILED, int MODE, int PB>
 __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw, const float* __restrict__ gz, Lay lg,
                                             int gz_rows, const float* __restrict__ hs, Lay lhs, float* __restrict__ gwpart,
                                             long long gw_ld, BwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB) {
@@ -515,8 +524,8 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
     const bool wok = load_wave(p, w, wv);
-    const int2* q = cw + wv.x + lane;
-    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    const PairLoad<PB> q(cw, wv.x, lane);
+    int2 nxt = (wok && wv.y > 0) ? q.step(0) : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     // The source row's own line (the per-edge gradient's operand) comes first, with the wave's first pairs: with a
@@ -537,12 +546,12 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     for (int left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
         float wt[8];
-        stage8(slots[grp], sub, nxt, c, wt);
+        stage_pairs<PB>(slots, grp, sub, nxt, false, nullptr, gz_rows, c, wt);
         float4 v[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) v[s] = s < left ? slab.get(quiet ? NO_ROW : c[s], sub) : splat(0.f);
         __builtin_amdgcn_sched_barrier(0);
-        if (left > 8) nxt = q[64 * (j + 1)];
+        if (left > 8) nxt = q.step(j + 1);
         if (gwp && j > 0) __builtin_nontemporal_store(pend, gwp + 64 * (j - 1));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -570,7 +579,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
 // The same over two tiles at once, tiles 2 pr and 2 pr + 1 of a pair pr (the second may not exist): a step gathers
 // the source lines of both tiles for the same (source, weight) pairs, and the weight-gradient partial of a position is
 // summed over both tiles (tile 2 pr first) and stored once per pair: gwpart [ceil(T / 2)][gw_ld]
-template <int MODE>
+template <int MODE, int PB>
 __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw, const float* __restrict__ gz, Lay lg,
                                              int gz_rows, const float* __restrict__ hs, Lay lhs, float* __restrict__ gwpart,
                                              long long gw_ld, BwdEpi epi, float* __restrict__ part, Lay lp, int T, int RB) {
@@ -583,8 +592,8 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
     const int w = __builtin_amdgcn_readfirstlane(rb * (WG / 64) + (int)(threadIdx.x >> 6));
     int2 wv;
     const bool wok = load_wave(p, w, wv);
-    const int2* q = cw + wv.x + lane;
-    int2 nxt = (wok && wv.y > 0) ? q[0] : make_int2(NO_ROW, 0);
+    const PairLoad<PB> q(cw, wv.x, lane);
+    int2 nxt = (wok && wv.y > 0) ? q.step(0) : make_int2(NO_ROW, 0);
     int4 sg;
     const bool live = load_segment(p, w * 8 + (grp & 7), sg) && wok;
     // the source row's own lines first, and on a tile where the row fires on no sample its gathers are skipped (k_bwd)
@@ -604,14 +613,14 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
     for (int left = wok ? wv.y : 0; left > 0; ++j, left -= 8) {
         int c[8];
         float wt[8];
-        stage8(slots[grp], sub, nxt, c, wt);
+        stage_pairs<PB>(slots, grp, sub, nxt, false, nullptr, gz_rows, c, wt);
         float4 va[8], vb[8];
 #pragma unroll
         for (int s = 0; s < 8; ++s) va[s] = s < left ? sa.get(quiet_a ? NO_ROW : c[s], sub) : splat(0.f);
 #pragma unroll
         for (int s = 0; s < 8; ++s) vb[s] = (hasb && s < left) ? sb.get(quiet_b ? NO_ROW : c[s], sub) : splat(0.f);
         __builtin_amdgcn_sched_barrier(0);
-        if (left > 8) nxt = q[64 * (j + 1)];
+        if (left > 8) nxt = q.step(j + 1);
         if (gwp && j > 0) __builtin_nontemporal_store(pend, gwp + 64 * (j - 1));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -903,7 +912,9 @@ hipError_t launch_pack_n(const PackJob* jobs, int n, hipStream_t st, bool bf16w)
     long long nb;
     if (!fill_table(t, jobs, n, [](const PackJob& j) { return j.n; }, nb)) return hipErrorInvalidValue;
     for (int k = 0; k < t.n; ++k)
-        if (!t.j[k].pcol || !t.j[k].pidx || !t.j[k].w || !t.j[k].cw) return hipErrorInvalidValue;
+        if (!t.j[k].pcol || !t.j[k].pidx || !t.j[k].w || !t.j[k].cw || (t.j[k].pb != 8 && t.j[k].pb != 6) ||
+            (t.j[k].pb == 6 && t.j[k].n % 64))
+            return hipErrorInvalidValue;
     if (nb == 0) return hipSuccess;
     if (bf16w)
         k_pack<true><<<(unsigned)nb, WG, 0, st>>>(t);
@@ -920,15 +931,20 @@ hipError_t launch_pack(const int* pcol, const int* pidx, const float* w, int2* c
 
 hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, int src_rows, const FwdEpi& epi,
                       float* part, Lay lp, int T, hipStream_t st, const unsigned* src_fires) {
+    // 6-byte pairs name rows by 16 bits: only a tiled slab of at most PAIR6_MAX_ROWS rows reads 0xFFFF as past its end
+    if ((p.pb != 8 && p.pb != 6) || (p.pb == 6 && (ls.row != TW || src_rows > PAIR6_MAX_ROWS)))
+        return hipErrorInvalidValue;
     if (p.nwave > 0) {
         const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
         const int fw = src_fires && ls.row == TW && fires_ld(src_rows) <= FIRES_LDS_WORDS ? fires_ld(src_rows) : 0;
-        if (ls.row == TW)
-            k_fwd<true><<<(unsigned)((long long)T * RB), WG, (size_t)(fw > 0 ? fw - 4 : 0) * 4, st>>>(
-                p, cw, src, ls, src_rows, epi, part, lp, T, RB, src_fires, fw);
+        const dim3 grid((unsigned)((long long)T * RB));
+        const size_t lds = (size_t)(fw > 0 ? fw - 4 : 0) * 4;
+        if (ls.row != TW)
+            k_fwd<false, 8><<<grid, WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB, nullptr, 0);
+        else if (p.pb == 6)
+            k_fwd<true, 6><<<grid, WG, lds, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB, src_fires, fw);
         else
-            k_fwd<false><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB,
-                                                                       nullptr, 0);
+            k_fwd<true, 8><<<grid, WG, lds, st>>>(p, cw, src, ls, src_rows, epi, part, lp, T, RB, src_fires, fw);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -942,15 +958,21 @@ hipError_t launch_fwd(const Plan& p, const int2* cw, const float* src, Lay ls, i
 hipError_t launch_fwd_lds(const Plan& p, const int2* cw, const float* src, int src_rows, const FwdEpi& epi, float* part,
                           Lay lp, int T, int S, hipStream_t st) {
     const size_t lds = (size_t)src_rows * TW * 4;
-    if (S < 1 || src_rows < 1 || lds > FWD_LDS_BYTES || epi.drive || !epi.info) return hipErrorInvalidValue;
+    if (S < 1 || src_rows < 1 || lds > FWD_LDS_BYTES || epi.drive || !epi.info || (p.pb != 8 && p.pb != 6) ||
+        (p.pb == 6 && src_rows > PAIR6_MAX_ROWS))
+        return hipErrorInvalidValue;
     S = std::max(S, (p.nwave + 64 * FWD_LDS_NW - 1) / (64 * FWD_LDS_NW));     // (at most 64 plan waves per wave)
     if (p.nwave > 0) {
         // (above 64 kB of dynamic LDS the kernel must be told its size; set on every launch, so that it holds on
         // whichever device is current)
-        const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_lds),
-                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
+        const void* k = p.pb == 6 ? reinterpret_cast<const void*>(&k_fwd_lds<6>) : reinterpret_cast<const void*>(&k_fwd_lds<8>);
+        const hipError_t attr = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)FWD_LDS_BYTES);
         if (attr != hipSuccess) return attr;
-        k_fwd_lds<<<(unsigned)((long long)T * S), FWD_LDS_NW * 64, lds, st>>>(p, cw, src, src_rows, epi, part, lp, T, S);
+        const dim3 grid((unsigned)((long long)T * S));
+        if (p.pb == 6)
+            k_fwd_lds<6><<<grid, FWD_LDS_NW * 64, lds, st>>>(p, cw, src, src_rows, epi, part, lp, T, S);
+        else
+            k_fwd_lds<8><<<grid, FWD_LDS_NW * 64, lds, st>>>(p, cw, src, src_rows, epi, part, lp, T, S);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -975,7 +997,8 @@ bool lds_fits(std::initializer_list<const void*> kernels) {
 }
 
 bool lds_plug_fits() {
-    return lds_fits({reinterpret_cast<const void*>(&k_fwd_lds), reinterpret_cast<const void*>(&k_plug_bwd_lds)});
+    return lds_fits({reinterpret_cast<const void*>(&k_fwd_lds<8>), reinterpret_cast<const void*>(&k_fwd_lds<6>),
+                     reinterpret_cast<const void*>(&k_plug_bwd_lds)});
 }
 
 hipError_t launch_plug_bwd_lds(const float* gd, const float* x, int x_rows, const int* in_crow, const int* in_col,
@@ -1005,22 +1028,36 @@ hipError_t launch_touch(const TouchJob& j, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <bool TILED, int MODE, int PB>
+static void launch_bwd_kernel(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc,
+                              Lay lhs, float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T,
+                              bool pair, hipStream_t st) {
+    const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
+    if constexpr (TILED && MODE != 0) {
+        if (pair) {                             // two tiles per workgroup
+            k_bwd2<MODE, PB><<<(unsigned)((long long)((T + 1) / 2) * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs,
+                                                                                     gwpart, gw_ld, epi, part, lp, T, RB);
+            return;
+        }
+    }
+    k_bwd<TILED, MODE, PB><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld,
+                                                                         epi, part, lp, T, RB);
+}
+
 template <bool TILED, int MODE>
 static hipError_t launch_bwd_as(const Plan& p, const int2* cw, const float* gz, Lay lg, int gz_rows, const float* hsrc,
                                 Lay lhs, float* gwpart, long long gw_ld, const BwdEpi& epi, float* part, Lay lp, int T,
                                 bool pair, hipStream_t st) {
+    // (6-byte pairs: a tiled slab of at most PAIR6_MAX_ROWS rows, as launch_fwd)
+    if ((p.pb != 8 && p.pb != 6) || (p.pb == 6 && (!TILED || gz_rows > PAIR6_MAX_ROWS))) return hipErrorInvalidValue;
     if (p.nwave > 0) {
-        const int RB = (p.nwave + WG / 64 - 1) / (WG / 64);
-        if constexpr (TILED && MODE != 0) {
-            if (pair)                           // two tiles per workgroup
-                k_bwd2<MODE><<<(unsigned)((long long)((T + 1) / 2) * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs,
-                                                                                      gwpart, gw_ld, epi, part, lp, T, RB);
+        if constexpr (TILED) {
+            if (p.pb == 6)
+                launch_bwd_kernel<true, MODE, 6>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, pair, st);
             else
-                k_bwd<TILED, MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs,
-                                                                                 gwpart, gw_ld, epi, part, lp, T, RB);
+                launch_bwd_kernel<true, MODE, 8>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, pair, st);
         } else {
-            k_bwd<TILED, MODE><<<(unsigned)((long long)T * RB), WG, 0, st>>>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart,
-                                                                             gw_ld, epi, part, lp, T, RB);
+            launch_bwd_kernel<false, MODE, 8>(p, cw, gz, lg, gz_rows, hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, pair, st);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

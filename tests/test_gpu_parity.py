@@ -226,3 +226,45 @@ def test_skipping_silent_rows_changes_nothing(gpu_lib, monkeypatch, full, B, fla
         assert np.array_equal(a, b)
     for name, a, b in zip(NAMES, g1, g0):
         assert np.array_equal(a, b), name
+
+
+@pytest.mark.parametrize("B,flags,tiles,plug", [(96, 0, "2", ""), (4096, 0, "1", ""), (4096, 0, "2", ""),
+                                                 (192, 1, "2", ""), (4096, 1, "1", ""), (96, 0, "2", "fan32"),
+                                                 (192, 1, "1", "fan32")])
+def test_pair_storage_changes_nothing(gpu_lib, monkeypatch, full, B, flags, tiles, plug):
+    """A plan's (source, weight) pairs are stored in 6 bytes (weights, then 16-bit sources, per wave step) when the
+    state its product gathers has at most 65,535 rows and its waves walk 3 steps or more on average (on the benchmark
+    network every product but the plug and hop 3's backward); FLYGUY_PAIR_BYTES=8 keeps the 8-byte pairs.  Logits,
+    every layer's state and all seven gradients are bit-identical either way: float32 states at B = 96 and 4096, one
+    and two tiles per backward workgroup, bfloat16 states (flags 1) at B = 192 and 4096, with a third of the neurons
+    silenced so that the forward's silent-source drops (made after the staging with 6-byte pairs) are taken; and a
+    network of the benchmark shape whose plug reads 32 inputs per sensory neuron (4 steps a wave, so its pairs take 6
+    bytes too) through the plug kernels that stage the observations in LDS (FLYGUY_PLUG_LDS=4)."""
+    if plug == "fan32":
+        s, params = synth_3hop(fan=32)
+        monkeypatch.setenv("FLYGUY_PLUG_LDS", "4")
+    else:
+        s, params = full
+    P = [p.copy() for p in params]
+    rng = np.random.default_rng(32)
+    P[2][rng.random(P[2].size) < 1 / 3] = 6.0                  # softplus(6) ~ 6: these neurons almost never fire
+    obs = rng.standard_normal((B, 517)).astype(np.float32)
+    dl = (rng.standard_normal((B, 90)) / B).astype(np.float32)
+    monkeypatch.setenv("FLYGUY_BWD_TILES", tiles)
+    out = {}
+    for pb in ("8", "6"):
+        monkeypatch.setenv("FLYGUY_PAIR_BYTES", pb)
+        core = Core(s, P, max_batch=B, flags=flags)
+        lg = core.forward(obs)
+        states = [core.state(layer, 0, s["sizes"][layer], B) for layer in range(s["hops"] + 1)]
+        core.zero_grad()
+        core.backward(dl)
+        out[pb] = (lg, states, core.get(4))
+        del core
+    (l8, s8, g8), (l6, s6, g6) = out["8"], out["6"]
+    assert np.isfinite(l6).all()
+    assert np.array_equal(l8, l6)
+    for a, b in zip(s8, s6):
+        assert np.array_equal(a, b)
+    for name, a, b in zip(NAMES, g8, g6):
+        assert np.array_equal(a, b), name
