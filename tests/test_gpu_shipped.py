@@ -15,8 +15,9 @@ checkpoint, and the network handed to the library as NET.bin bytes.
     and 2e-3, a gain between 1e-4 and 6e-4 (rate 0.3x), strengths not in play not at all;
   * B = 4096 (the benchmark batch): logits <= 1e-5 against float64 and <= 4e-6 against the float32 oracle, argmax
     identical off near-ties; 64-sample slices give the same logits bit for bit;
-  * a teaching step (KL loss against teacher logits 2 N(0,1)) at B = 512: the gradients held as at the synthetic
-    network's benchmark batch (tests/test_gpu_configs.py).
+  * a teaching step (KL loss against teacher logits 2 N(0,1)) at B = 512 and 4096: the gradients held as at the
+    synthetic network's benchmark batch (tests/test_gpu_configs.py);
+  * B = 4096: gradients of four 1024-sample pieces add up to the whole batch's (<= 1e-5), pieces' logits bit for bit.
 """
 from __future__ import annotations
 
@@ -188,14 +189,15 @@ def test_shipped_b4096_forward_against_oracle(gpu_lib, shipped):
         assert np.array_equal(core.forward(obs[start:start + 64]), got[start:start + 64]), start
 
 
-def test_shipped_teaching_step_against_oracle(gpu_lib, shipped):
-    """Forward, KL loss and backward on the shipped network at B = 512.  Gradients: on the samples whose firing
+@pytest.mark.parametrize("B", [512, 4096])
+def test_shipped_teaching_step_against_oracle(gpu_lib, shipped, B):
+    """Forward, KL loss and backward on the shipped network at B = 512 and at the benchmark batch, 4096.  Gradients:
+    on the samples whose firing
     pattern the library, the float32 oracle and the float64 oracle share, within 1e-4 of float64 and of the float32
     oracle; over the whole batch within 1e-4 of float64 or no further from it than 1.1 x the float32 oracle's own
     distance + 1e-6 (a pre-activation within rounding of its threshold fires in one float32 sum order and not in
     another, and then the two gradients differ by that neuron's whole term)."""
     f, s, params = shipped
-    B = 512
     rng = np.random.default_rng(51)
     obs = (0.5 * rng.standard_normal((B, 517))).astype(np.float32)
     teacher = (rng.standard_normal((B, 90)) * 2).astype(np.float32)
@@ -223,3 +225,27 @@ def test_shipped_teaching_step_against_oracle(gpu_lib, shipped):
         r, r_ref = rel(g, w), rel(a, w)
         say(f"   whole batch: grad {name:6s} rel {r:.2e} (float32 oracle {r_ref:.2e})")
         assert r <= 1e-4 or r <= 1.1 * r_ref + 1e-6, (name, r, r_ref)
+
+
+def test_shipped_b4096_gradients_add_up_over_pieces(gpu_lib, shipped):
+    """The benchmark batch's gradients on the shipped network equal the sum of those of its four 1024-sample
+    pieces (each sum in its own tile order) to 1e-5, and a piece's logits are those of the whole batch bit for bit:
+    no sample's result depends on the batch it is in."""
+    f, s, params = shipped
+    B = 4096
+    rng = np.random.default_rng(52)
+    obs = (0.5 * rng.standard_normal((B, 517))).astype(np.float32)
+    dl = (rng.standard_normal((B, 90)) / B).astype(np.float32)
+    core = Core(s, params, max_batch=B)
+    whole_lg = core.forward(obs)
+    core.zero_grad()
+    core.backward(dl)
+    whole = core.get(4)
+    core.zero_grad()
+    for i in range(0, B, 1024):
+        assert np.array_equal(core.forward(obs[i:i + 1024]), whole_lg[i:i + 1024]), i
+        core.backward(dl[i:i + 1024])
+    for name, a, b in zip(NAMES, core.get(4), whole):
+        r = rel(a, b)
+        say(f"   grad {name:6s} 4 x 1024 vs 4096 rel {r:.2e}")
+        assert r <= 1e-5, (name, r)
