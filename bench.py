@@ -20,6 +20,9 @@ fp32, B = 4096, observations ~N(0,1) and teacher logits ~N(0,2) already in devic
            train: one teaching step of that PyTorch path on the CPU at B = 4096.
   silent_floor (in each roofline): the dominant hop launch re-timed with its source layer silenced, so that every
            gather is skipped: the kernel's floor without memory traffic, measured in the same run.
+  gather_ceiling (in each roofline): the time the dominant hop's line gathers take at the device's gather rate
+           (fc_gather_ceiling: random 128-byte lines from a slab of the same size, 8 lines per wave instruction,
+           every CU issuing nothing else), measured in the same run, and the share of it the kernel reaches.
   decision_latency_gpu: one fc_forward of a 32-sample tile (a batch-1 decision padded), synchronised per call;
   bf16_b16384: the bfloat16-state core at B = 16384 (forward and teaching step) on the same network and on its
            Erdos-Renyi control;
@@ -71,6 +74,29 @@ def algorithmic_bytes(s: dict, B: int, sz: int = 4) -> dict:
         train += b
     train += 3 * N[0] * B * sz + 2 * N[0] * B * 4 + OD * B * 4 + 36 * n_params
     return {"hop_fwd": hop_fwd, "hop_bwd": hop_bwd, "infer": infer, "train": train, "n_params": n_params}
+
+
+def gather_ceiling(ms: float, row_of, B: int, rows: int, tiles: int) -> dict:
+    """A hop launch against the device's gather ceiling, measured in this run (fc_gather_ceiling): the time the same
+    number of 128-byte line gathers takes when every CU does nothing but gather, 8 lines per wave instruction and 8
+    row indices loaded per step as the hop kernels do, from a slab of `rows` lines (per tile; `tiles` of them for a
+    backward that takes two tiles per workgroup), each row drawn as a random connection's (row_of: the gathered row
+    of every connection, so that rows come as often as the kernel gathers them).  The kernel gathers one line per
+    connection and tile; frac is the ceiling's time over the kernel's, the share of the gather rate it reaches."""
+    import numpy as np
+    import torch
+    from flyguy_amd._lib import call
+    idx = torch.as_tensor(np.ascontiguousarray(row_of, dtype=np.int32)).cuda()
+    ns = ctypes.c_double(0.0)
+    call("fc_gather_ceiling", rows, tiles, idx.data_ptr(), idx.numel(), 5,
+         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream), ctypes.byref(ns))
+    lines = idx.numel() * (B // 32)
+    at = lines * ns.value * 1e-6
+    return {"slab_rows": rows, "tiles": tiles, "ns_per_line": round(ns.value, 6), "lines_per_launch": lines,
+            "ms_at_ceiling": round(at, 4), "frac": round(at / ms, 4),
+            "note": "fc_gather_ceiling: 128-byte lines of a tile's slab, rows drawn as the kernel's connections draw "
+                    "them, 16 bytes a lane, 8 lines per wave instruction, every CU gathering and nothing else; the "
+                    "bound the hop kernels meet before HBM bandwidth"}
 
 
 def silent_floor(ms: float, floor_ms: float, E: int, B: int) -> dict:
@@ -771,7 +797,7 @@ def main() -> int:
     # skipped), forward and teaching step (rate 0: the weights stay as they are), then the weights restored
     def layer_neurons(layer):
         return np.asarray(s["n0"] if layer == 0 else s["hop"][layer - 1]["nid"], np.int64)
-    floor_f = floor_b = None
+    floor_f = floor_b = ceil_f = ceil_b = None
     if not args.no_floor:
         quiet = params[1].copy()
         for layer in {kf, kb}:
@@ -791,6 +817,12 @@ def main() -> int:
         call("fc_copy", core, 0, 1, ptrs)
         floor_f = silent_floor(dom_f_ms, quiet_f_ms, len(s["hop"][kf]["col"]), B)
         floor_b = silent_floor(dom_b_ms, quiet_b_ms, len(s["hop"][kb]["col"]), B)
+        # the gather ceilings: the forward gathers the source layer's slab, the backward the hop's own layer (gz), two
+        # tiles' slabs at once when it takes two tiles per workgroup
+        ceil_f = gather_ceiling(dom_f_ms, s["hop"][kf]["col"], B, s["sizes"][kf], 1)
+        crow_b = np.asarray(s["hop"][kb]["crow"])
+        ceil_b = gather_ceiling(dom_b_ms, np.repeat(np.arange(len(crow_b) - 1), np.diff(crow_b)), B,
+                                s["sizes"][kb + 1], 2 if bwd_pairs(s["hop"][kb]["crow"]) else 1)
         print(f"# floors: {dom_f} {floor_f['ms']:.3f} of {dom_f_ms:.3f} ms, {dom_b} {floor_b['ms']:.3f} of "
               f"{dom_b_ms:.3f} ms", file=sys.stderr, flush=True)
 
@@ -835,7 +867,7 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": ab["hop_fwd"][kf], "mean_launch_ms": round(dom_f_ms, 4),
                      "whole_batch_frac": round(ab["infer"] / (t_fwd / K) / PEAK_HBM, 4),
                      "whole_batch_algorithmic_bytes": ab["infer"],
-                     "silent_floor": floor_f},
+                     "silent_floor": floor_f, "gather_ceiling": ceil_f},
         "decision_latency_gpu": lat_b32,
         "cpu_baseline": cpu_f,
         "train": {"value": round(sps, 1), "unit": "samples/s", "ms_per_step": round(ms_train, 4),
@@ -850,7 +882,7 @@ def main() -> int:
                                "mean_launch_ms": round(dom_b_ms, 4),
                                "whole_step_frac": round(ab["train"] / (t_train / K) / PEAK_HBM, 4),
                                "whole_step_algorithmic_bytes": ab["train"],
-                               "silent_floor": floor_b},
+                               "silent_floor": floor_b, "gather_ceiling": ceil_b},
                   "cpu_baseline": cpu_t},
         "trainer": trainer,
         "bf16_b16384": bf16,

@@ -34,6 +34,7 @@ _SIGS = {
     "fc_export_state": (None, [vp, ci, ci, vp, ci]),
     "fc_profile": (None, [vp, ci]),
     "fc_profile_read": (ci, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(cll), ci, ci]),
+    "fc_gather_ceiling": (ci, [ci, ci, vp, cll, ci, vp, ctypes.POINTER(ctypes.c_double)]),
     "fc_plan_rows": (ci, [vp, ci, ci, vp, cll, vp, cll, vp, cll, vp, cll, ctypes.POINTER(cll)]),
     "fc_net_plan": (ci, [ctypes.c_char_p, cll, ci, ci, vp, cll, vp, cll, vp, cll, vp, cll, ctypes.POINTER(cll)]),
     "fc_net_marks": (cll, [ctypes.c_char_p, cll, ci, ci, vp, cll]),

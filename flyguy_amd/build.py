@@ -19,7 +19,7 @@ ROOT = PKG.parent
 LIB = PKG / "libflyguy_core.so"
 EXE = PKG / "flyguy_train"
 CPU_LIB = PKG / "libfly_infer.so"          # decisions on the host CPU (include/fly_infer.h): no HIP
-SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "core16.hip", "readout.hip", "hop_api.hip", "half.hip", "train.hip")]
+SOURCES = [PKG / "csrc" / n for n in ("kernels.hip", "core.hip", "core16.hip", "readout.hip", "hop_api.hip", "half.hip", "train.hip", "probe.hip")]
 HEADERS = [PKG / "csrc" / n for n in ("common.h", "kernels.h", "device.h", "core.h", "half.h")] + \
     [ROOT / "include" / "flyguy_core.h", ROOT / "include" / "flyguy_train.h", ROOT / "include" / "fly_infer.h"]
 ARCH = os.environ.get("FLYGUY_OFFLOAD_ARCH", "gfx950")

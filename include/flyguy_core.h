@@ -117,6 +117,16 @@ void fc_export_state(void* core, int layer, int what, float* dst, int B);
 void fc_profile(void* core, int on);
 int fc_profile_read(void* core, double* ms, long long* counts, int n, int reset);
 
+/* The gather ceiling (measurement): the time per gathered 128-byte line, for the whole device, when every CU's 8-lane
+ * groups do nothing but gather, as the hop kernels gather: per step each lane of a group draws one connection at
+ * random and takes its row, row_of[e] (device, n_edges entries, each in 0 .. rows - 1; NULL: rows drawn uniformly),
+ * the group shares the 8 rows and loads each row's line, 16 bytes a lane (8 lines per wave instruction), from each
+ * of `tiles` slabs of rows x 128 bytes (1, or 2 for a backward that takes two tiles per workgroup).  reps timed
+ * launches after an untimed one, on `stream` (a hipStream_t, or NULL); writes nanoseconds per line to ns_per_line.
+ * Allocates and frees its own scratch.  Returns 0, or -1 (fc_last_error).  (No counterpart in the reference.) */
+int fc_gather_ceiling(int rows, int tiles, const int* row_of, long long n_edges, int reps, void* stream,
+                      double* ns_per_line);
+
 /* The row plan of one sparse product, computed on the host (no device needed).  Every row is cut into segments of
  * at most seg_max edges; the segments are sorted longest first (ties: row, then segment order) and dealt 8 to a
  * wave; the edges are laid out in plan order, edge k of the segment of group g of wave w at position

@@ -46,3 +46,30 @@ def test_profile_every_stage_or_one(gpu_lib):
     assert profile_read(core.h, reset=True) == {}
     with pytest.raises(LibraryError):
         call("fc_profile", core.h, 2 + 25)       # past the last stage
+
+
+def test_gather_ceiling(gpu_lib):
+    """fc_gather_ceiling (bench.py's gather ceiling): a positive time per line; no smaller for a slab larger than an
+    XCD's L2 than for one that fits it (misses cost), nor for two tiles' slabs than for one; rows drawn from a
+    connection table (here every connection on row 0: one line, always in the cache) no slower than uniform ones over
+    a large slab; bad arguments refused before any device work."""
+    import ctypes
+    from flyguy_amd._lib import lib
+
+    def ns(rows, tiles=1, row_of=None):
+        v = ctypes.c_double(-1.0)
+        ptr, n = (row_of.data_ptr(), row_of.numel()) if row_of is not None else (None, 0)
+        call("fc_gather_ceiling", rows, tiles, ptr, n, 3, None, ctypes.byref(v))
+        return v.value
+
+    small, large, two = ns(1024), ns(200000), ns(100000, 2)
+    hot = ns(200000, 1, torch.zeros(4096, dtype=torch.int32, device="cuda"))
+    say(f"   gather ceiling: {small:.5f} ns per line (1,024 rows), {large:.5f} (200,000 rows: 25.6 MB), "
+        f"{two:.5f} (2 x 100,000), {hot:.5f} (200,000 rows, every draw row 0)")
+    assert 0 < small < 1 and np.isfinite(large) and large >= small and two >= small and hot <= large
+    v = ctypes.c_double(0.0)
+    assert lib().fc_gather_ceiling(0, 1, None, 0, 3, None, ctypes.byref(v)) == -1
+    with pytest.raises(LibraryError):
+        call("fc_gather_ceiling", 1024, 3, None, 0, 3, None, ctypes.byref(v))
+    with pytest.raises(LibraryError):
+        call("fc_gather_ceiling", 1024, 1, None, 0, 0, None, ctypes.byref(v))
