@@ -35,6 +35,12 @@ struct HopD {
     int* ridx = nullptr;
     int* gridx = nullptr;
     int2 *cw = nullptr, *tcw = nullptr;
+    // The backward through k_bwd_lds (launch_bwd_lds), for a hop whose gathered rows mostly fit the LDS (bwd_lds_choice
+    // in core.hip): lds_hot rows staged (0: the hop never takes it), hot_rows (most gathered first), and the transposed
+    // plan's pairs with LDS codes (tcw_lds, packed from pcol_lds like tcw from bp.pcol)
+    int lds_hot = 0;
+    int *hot_rows = nullptr, *pcol_lds = nullptr;
+    int2 *tcw_lds = nullptr, *wave_lds = nullptr;   // (wave_lds: bp's wave records with WLDS_COLD marks)
     DevPlan fp, bp;
     float *h = nullptr, *ggp = nullptr, *gsp = nullptr;
     float4* info = nullptr;          // per row {gain, softplus(theta), re-drive row}, from the current weights
@@ -101,6 +107,9 @@ struct Core {
     // results are the same).
     bool skip_silent = true;
     int plug_lds = -1;               // the plug staged in LDS: -1 by batch size, 0 never, S > 0 with S workgroups per tile
+    int bwd_lds = -1;                // k_bwd_lds for the hops that have it: -1 from BWD_LDS_MIN_TILES tiles up, 0 never,
+                                     //   1 at every batch (FLYGUY_BWD_LDS)
+    int cus = 0;                     // the device's CUs (k_bwd_lds takes one workgroup per CU)
     // What the derived tables were made from.  wver[set] counts the writes to the weights (set 0) and to the running
     // average (set 1): fc_copy into the handle, an Adam step, the trainer's host-side edits.  A table made from a
     // set at its current version is not made again: the forward's packed pairs and per-row records (from one set),

@@ -129,10 +129,13 @@ static T* upload(Core& c, const std::vector<T>& v) {
 // pairs cut that stream by a quarter: float32 forward 3.062 -> 3.013 ms, teaching step 6.975 -> 6.914 ms at B=4096.
 // A wave of one or two steps waits for its first pairs before any gather, and the 6-byte form's unpacking lies on
 // that path: the plug (2 steps a wave) took 0.160 -> 0.163 ms and hop 3's backward (1.4) 0.513 -> 0.519 ms with them,
-// so those keep 8 bytes.  FLYGUY_PAIR_BYTES=8 keeps every plan at 8 bytes (the results are the same bit for bit).
+// so those keep 8 bytes.  FLYGUY_PAIR_BYTES=8 keeps every plan at 8 bytes, =6 stores every plan whose gathered state
+// allows it in 6 (the results are the same bit for bit).
 static int pair_storage(int gathered_rows, const HostPlan& h) {
-    if (const char* f = std::getenv("FLYGUY_PAIR_BYTES"))
+    if (const char* f = std::getenv("FLYGUY_PAIR_BYTES")) {
         if (std::atoi(f) == 8) return 8;
+        if (std::atoi(f) == 6 && gathered_rows <= PAIR6_MAX_ROWS) return 6;
+    }
     const long long steps = (long long)h.pos.size() / 64, waves = (long long)h.wave.size();
     return gathered_rows <= PAIR6_MAX_ROWS && steps >= 3 * waves ? 6 : 8;
 }
@@ -252,6 +255,31 @@ static bool bwd_skip_rows(const HostPlan& b) {
     }
     return (long long)b.pos.size() > 2LL * 64 * (long long)b.wave.size();
 }
+
+// Which rows a hop's backward stages in LDS (k_bwd_lds): its backward gathers the hop's own rows, each as often as its
+// in-degree; the `cap` most gathered (ties by row) go into `hot`, most gathered first.  The hop takes the kernel when
+// the rows left out take at most 1/64 of the gathers, so that few steps gather anything through the vector-memory
+// path: the hop into the descending layer (1,332 rows) of the benchmark networks and of the shipped graph (1,216 rows
+// staged, the other 116 about 0.2% of the gathers).  Returns the number staged, 0 when the hop does not take it.
+static int bwd_lds_choice(const std::vector<int>& crow, int rows, int cap, std::vector<int>& hot) {
+    hot.clear();
+    const long long E = crow[rows];
+    if (cap <= 0 || rows <= 0 || E <= 0 || (long long)std::min(rows, cap) + rows > PAIR6_MAX_ROWS) return 0;
+    std::vector<int> order(rows);
+    for (int i = 0; i < rows; ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int a, int b) { return crow[a + 1] - crow[a] > crow[b + 1] - crow[b]; });
+    const int n = std::min(rows, cap);
+    long long out = 0;
+    for (int r = n; r < rows; ++r) out += crow[order[r] + 1] - crow[order[r]];
+    if (64 * out > E) return 0;
+    hot.assign(order.begin(), order.begin() + n);
+    return n;
+}
+
+// k_bwd_lds from this many tiles up (one workgroup per CU: at fewer tiles each workgroup stages its 152 kB for fewer
+// rows).  FLYGUY_BWD_LDS=0 turns it off, =1 takes it at every batch.
+constexpr int BWD_LDS_MIN_TILES = 16;
 
 static bool distinct(const std::vector<int>& v, long long n, bool skip_negative) {
     std::vector<unsigned char> seen((size_t)std::max<long long>(n, 1), 0);
@@ -492,6 +520,14 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     c->in_cw = dalloc<int2>(*c, (size_t)(pair_bytes(c->pp.npos, c->pp.pb) / 8));
     long long max_slot = c->pp.nslot, max_pos = 1, max_rows = 1;
     c->hop.resize(K);
+    if (const char* f = std::getenv("FLYGUY_BWD_LDS")) c->bwd_lds = f[0] == '0' ? 0 : (f[0] == '1' ? 1 : -1);
+    const int lds_cap = c->bwd_lds == 0 ? 0 : bwd_lds_rows();
+    {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            c->cus = 0;
+    }
     for (int k = 0; k < K; ++k) {
         HopD& d = c->hop[k];
         HopHost& h = n.hop[k];
@@ -511,6 +547,35 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         d.cw = dalloc<int2>(*c, (size_t)(pair_bytes(d.fp.npos, d.fp.pb) / 8));
         d.tcw = dalloc<int2>(*c, (size_t)(pair_bytes(d.bp.npos, d.bp.pb) / 8));
         if (!d.gidx || !d.ridx || !d.gridx || !d.nid || !d.drow || !d.cw || !d.tcw) return nullptr;
+        // the last hop's backward (a hop layer below it) through k_bwd_lds, float32 states
+        std::vector<int> hot;
+        if (prec == 0 && k == K - 1 && K >= 2 && lds_cap > 0 && bwd_lds_choice(h.crow, d.rows, lds_cap, hot) > 0) {
+            std::vector<int> rank(d.rows, -1);
+            for (size_t r = 0; r < hot.size(); ++r) rank[hot[r]] = (int)r;
+            const int nh = (int)hot.size();
+            const HostPlan& b = P.bwd[k];
+            std::vector<int> code(b.pos.size());
+            for (size_t i = 0; i < b.pos.size(); ++i) {
+                const int e = b.pos[i];
+                const int row = e >= 0 ? h.tcol[(size_t)e] : -1;
+                code[i] = row < 0 ? NO_ROW : (rank[row] >= 0 ? rank[row] : nh + row);
+            }
+            std::vector<int2> wl(b.wave);           // (plan waves with a pair outside the LDS marked)
+            for (auto& v : wl) {
+                const long long end = v.x + 64LL * ((v.y + 7) / 8);
+                for (long long i = v.x; i < end; ++i)
+                    if (code[(size_t)i] >= nh && code[(size_t)i] < nh + d.rows) {
+                        v.y |= WLDS_COLD;
+                        break;
+                    }
+            }
+            d.lds_hot = nh;
+            d.hot_rows = upload(*c, hot);
+            d.pcol_lds = upload(*c, code);
+            d.wave_lds = upload(*c, wl);
+            d.tcw_lds = dalloc<int2>(*c, (size_t)(pair_bytes(d.bp.npos, d.bp.pb) / 8));
+            if (!d.hot_rows || !d.pcol_lds || !d.wave_lds || !d.tcw_lds) return nullptr;
+        }
         d.h_nid = std::move(h.nid); d.h_crow = std::move(h.crow); d.h_col = std::move(h.col); d.h_widx = std::move(h.widx);
         max_slot = std::max<long long>({max_slot, d.fp.nslot, d.bp.nslot});
         max_pos = std::max<long long>(max_pos, d.bp.npos);
@@ -545,8 +610,8 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     // per tile, or per pair of tiles when every hop's backward takes two (the bfloat16 sensory layer takes one).
     const size_t Tm = c->Tm, S = TW, Tp = (size_t)bm / tq;
     size_t gw_rows = 0;
-    for (int k = 1; k <= K; ++k) {
-        const bool pair = c->hop[k - 1].pair_bwd && (prec == 0 || k >= 2);
+    for (int k = 1; k <= K; ++k) {       // (k_bwd_lds takes one tile per workgroup)
+        const bool pair = c->hop[k - 1].pair_bwd && (prec == 0 || k >= 2) && !c->hop[k - 1].lds_hot;
         gw_rows = std::max(gw_rows, pair ? (Tp + 1) / 2 : Tp);
     }
     auto state = [&](long long rows) -> float* {
@@ -641,9 +706,12 @@ static hipError_t pack(Core& c, int set, bool transposed, bool bf16w) {
     std::vector<PackJob> j;
     const float* W = c.arr(set, 0);
     if (!transposed) j.push_back({c.pp.pcol, c.pp.pidx, c.arr(set, 3), c.in_cw, c.pp.npos, c.pp.pb});
-    for (auto& d : c.hop)
+    for (auto& d : c.hop) {
         j.push_back(transposed ? PackJob{d.bp.pcol, d.bp.pidx, W, d.tcw, d.bp.npos, d.bp.pb}
                                : PackJob{d.fp.pcol, d.fp.pidx, W, d.cw, d.fp.npos, d.fp.pb});
+        if (transposed && d.lds_hot)    // (the same pairs with LDS codes, for k_bwd_lds)
+            j.push_back(PackJob{d.pcol_lds, d.bp.pidx, W, d.tcw_lds, d.bp.npos, d.bp.pb});
+    }
     hipError_t e = hipSuccess;
     for (size_t k = 0; k < j.size() && e == hipSuccess; k += PACK_JOBS)
         e = launch_pack_n(j.data() + k, (int)std::min<size_t>(PACK_JOBS, j.size() - k), c.st, bf16w);
@@ -843,17 +911,24 @@ bool backward(Core& c, const float* dlogits, int B, bool fresh) {
         // (plug_split): the sensory finish then leaves the drive's complete gradient in gdrive for it
         const int ps = k == 1 ? plug_split(c, T, 1024) : 0;
         if (ps) e.in_crow = nullptr;
+        // the gathered rows staged in LDS (bwd_lds_choice), one workgroup per CU
+        const bool lds = d.lds_hot > 0 && e.mode == 1 && (c.bwd_lds == 1 || (c.bwd_lds < 0 && T >= BWD_LDS_MIN_TILES));
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
-            FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below), c.gwpart,
-                                d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st, d.pair_bwd), false);
+            if (lds)
+                FG_CHECK(launch_bwd_lds(d.bp.view(), d.wave_lds, d.tcw_lds, c.gz[cur], d.rows, d.hot_rows, d.lds_hot, hbelow,
+                                        tiled(rows_below), c.gwpart, d.bp.npos, e, c.part, tiled(d.bp.nslot), T,
+                                        std::max(1, (c.cus > 0 ? c.cus : 256) / T), st), false);
+            else
+                FG_CHECK(launch_bwd(d.bp.view(), d.tcw, c.gz[cur], tiled(d.rows), d.rows, hbelow, tiled(rows_below),
+                                    c.gwpart, d.bp.npos, e, c.part, tiled(d.bp.nslot), T, st, d.pair_bwd), false);
             if (ps)
                 FG_CHECK(launch_plug_bwd_lds(c.gdrive, c.x, c.obs_dim, c.in_crow, c.in_col, c.n_s, c.ginb, c.n_s, c.ginw,
                                              c.E_in, T, ps, st), false);
         }
         Timed t(c, ST_REDUCE);
         // the layer's sums in one launch: each writes its own gradient array
-        const int np = d.pair_bwd ? (T + 1) / 2 : T;   // (a two-tile backward stores its partials per pair of tiles)
+        const int np = d.pair_bwd && !lds ? (T + 1) / 2 : T;   // (a two-tile backward: partials per pair of tiles)
         const RedJob jobs[5] = {{c.gwpart, d.bp.npos, d.bp.npos, np, d.ridx, nullptr, G[0], fresh},
                                 {ggp, d.gcols, d.gcols, np, d.gridx, nullptr, G[1], fresh},
                                 {gsp, d.gcols, d.gcols, np, d.gridx, theta, G[2], fresh},

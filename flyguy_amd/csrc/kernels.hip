@@ -441,6 +441,25 @@ __device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int t
     return bwd_inputs_h<MODE>(e, j, d, tile, sub, *at4u(e.h, e.lh, tile, j, sub));
 }
 
+// A hop layer's neuron backward for (row, tile) from gh, the gradient of its output: gz = g gain with g = gh where the
+// row fired (h > 0) and 0 elsewhere, and the tile's gain and threshold partials pg = sum g z, ps = sum g (every lane of
+// the 8-lane group calls this; each gets the group's sums).  The sum of g z needs no z: where h > 0, z = (h +
+// softplus(theta)) / gain, and elsewhere g = 0, so it is (sum g h + softplus(theta) sum g) / gain.  A neuron of gain 0
+// never fires (h = relu(-sp)): its g and so its sum are 0.
+struct HopBack {
+    float4 gz;
+    float pg, ps;
+};
+__device__ __forceinline__ HopBack hop_back(const float4& gh, const float4& hv, float gn, float sp) {
+    const float4 g = make_float4(hv.x > 0.f ? gh.x : 0.f, hv.y > 0.f ? gh.y : 0.f, hv.z > 0.f ? gh.z : 0.f,
+                                 hv.w > 0.f ? gh.w : 0.f);
+    HopBack b;
+    b.gz = make_float4(g.x * gn, g.y * gn, g.z * gn, g.w * gn);
+    b.ps = gsum8(hsum4(g));
+    b.pg = gn != 0.f ? (gsum8(dot4(g, hv)) + sp * b.ps) / gn : 0.f;
+    return b;
+}
+
 // gh: the gradient of this layer's output h for (row j, tile); every lane of the 8-lane group calls this
 template <int MODE>
 // keep (optional): the row's gain and threshold partials of the tile are returned there instead of stored (a kernel
@@ -452,19 +471,20 @@ __device__ __forceinline__ void bwd_finish(const BwdEpi& e, int j, int tile, int
         *at4w(e.gh_out, e.lgh, tile, j, sub) = gh;
         return;
     }
-    const float4 hv = in.h;
-    const float4 g = make_float4(hv.x > 0.f ? gh.x : 0.f, hv.y > 0.f ? gh.y : 0.f, hv.z > 0.f ? gh.z : 0.f,
-                                 hv.w > 0.f ? gh.w : 0.f);
-    const float gn = in.gn;
-    const float4 gzv = make_float4(g.x * gn, g.y * gn, g.z * gn, g.w * gn);
-    const float ps = gsum8(hsum4(g));
-    float pg;
+    float4 gzv;
+    float ps, pg;
     if constexpr (MODE == 1) {
-        // sum over the tile of g * z without z: where h > 0, z = (h + softplus(theta)) / gain, and elsewhere g = 0,
-        // so the sum is (sum g h + softplus(theta) sum g) / gain.  A neuron of gain 0 never fires (h = relu(-sp)):
-        // its g and so its sum are 0
-        pg = gn != 0.f ? (gsum8(dot4(g, hv)) + in.sp * ps) / gn : 0.f;
+        const HopBack b = hop_back(gh, in.h, in.gn, in.sp);
+        gzv = b.gz;
+        ps = b.ps;
+        pg = b.pg;
     } else {
+        const float4 hv = in.h;
+        const float4 g = make_float4(hv.x > 0.f ? gh.x : 0.f, hv.y > 0.f ? gh.y : 0.f, hv.z > 0.f ? gh.z : 0.f,
+                                     hv.w > 0.f ? gh.w : 0.f);
+        const float gn = in.gn;
+        gzv = make_float4(g.x * gn, g.y * gn, g.z * gn, g.w * gn);
+        ps = gsum8(hsum4(g));
         pg = gsum8(dot4(g, in.z));              // the sensory layer keeps its pre-activation (the drive)
     }
     if (keep) {
@@ -689,6 +709,263 @@ __global__ __launch_bounds__(WG) void k_bwd_combine(Plan p, const float* __restr
             epi.gsum_part[(size_t)u * epi.gp_ld + p.nseg + i] = k2[0].y + k2[1].y;
         }
     }
+}
+
+// ------------------------------------------------------------------------------------------------ backward, LDS
+// The backward of a hop layer (mode 1) for a gathered slab that mostly fits the LDS: the hop into the descending
+// layer gathers 1,332 rows of gradient, 170 kB a tile, against the 160 kB of LDS a workgroup may hold.  Each workgroup
+// stages the `hot` most gathered rows of its tile's slab in LDS once and walks its share of the transposed plan,
+// gathering from the LDS.  A pair's code names an LDS row (code < hot) or a slab row (hot + row); a step issues
+// vector-memory gathers only for slots that some group needs from the slab.  With the gathers off the vector-memory
+// path, that path carries only the loads that come from HBM (each row's own h line, the plan's records and pairs),
+// and those no longer hold up the return of gathered lines behind them.  The sums are k_bwd's (one tile per
+// workgroup), term for term in the same order.
+// S workgroups per tile, one per CU; a wave walks plan waves w0 + k dw, k < n <= 64 BWD_LDS_WREC, with lane l of
+// wrec[r] holding plan wave 64 r + l's record.  A plan wave's segment, records and first pairs are requested two plan
+// waves ahead and its rows' h lines one plan wave ahead (they need the segment's row), so that waiting for them does
+// not wait for the stores issued in between.
+// a ? x : y, element by element (a select of whole vector structs can turn into a select of their addresses,
+// which puts arrays of them in scratch memory)
+__device__ __forceinline__ float4 sel4(bool a, const float4& x, const float4& y) {
+    return make_float4(a ? x.x : y.x, a ? x.y : y.y, a ? x.z : y.z, a ? x.w : y.w);
+}
+constexpr int BWD_LDS_STAGE = (BWD_LDS_MAXROWS * LPR + BWD_LDS_NW * 64 - 1) / (BWD_LDS_NW * 64);
+template <int PB, bool SKIP>
+__global__ __launch_bounds__(BWD_LDS_NW * 64) void k_bwd_lds(Plan p, const int2* __restrict__ wlds,
+                                                            const int2* __restrict__ cw,
+                                                            const float* __restrict__ gz, int gz_rows,
+                                                            const int* __restrict__ hot_rows, int hot,
+                                                            const float* __restrict__ hs, Lay lhs,
+                                                            float* __restrict__ gwpart, long long gw_ld, BwdEpi epi,
+                                                            float* __restrict__ part, Lay lp, int T, int S) {
+    constexpr int NT = BWD_LDS_NW * 64;
+    __shared__ __align__(16) int2 slots[NT / LPR][LPR];
+    extern __shared__ __align__(16) float4 gs[];          // LDS row r: slab row hot_rows[r], LPR float4
+    int s;
+    const int tile = tile_of(blockIdx.x, S, T, s);
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63, gi = grp & 7;
+    const int w0 = __builtin_amdgcn_readfirstlane(s * BWD_LDS_NW + (int)(threadIdx.x >> 6)), dw = S * BWD_LDS_NW;
+    const int n = w0 < p.nwave ? min((p.nwave - 1 - w0) / dw + 1, 64 * BWD_LDS_WREC) : 0;
+    int2 wrec[BWD_LDS_WREC];
+#pragma unroll
+    for (int r = 0; r < BWD_LDS_WREC; ++r)
+        wrec[r] = 64 * r + lane < n ? wlds[w0 + (64 * r + lane) * dw] : make_int2(0, 0);
+    // the hot rows: every row index first, then every line, then the LDS stores (so the loads overlap)
+    const float4* gt = reinterpret_cast<const float4*>(gz + (size_t)tile * gz_rows * TW);
+    {
+        int ri[BWD_LDS_STAGE];
+        float4 lv[BWD_LDS_STAGE];
+#pragma unroll
+        for (int u = 0; u < BWD_LDS_STAGE; ++u) {
+            const int i = (int)threadIdx.x + u * NT;
+            ri[u] = i < hot * LPR ? hot_rows[i / LPR] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < BWD_LDS_STAGE; ++u) {
+            const int i = (int)threadIdx.x + u * NT;
+            lv[u] = (unsigned)ri[u] < (unsigned)gz_rows ? gt[(size_t)ri[u] * LPR + (i % LPR)] : splat(0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < BWD_LDS_STAGE; ++u) {
+            const int i = (int)threadIdx.x + u * NT;
+            if (i < hot * LPR) gs[i] = lv[u];
+        }
+    }
+    __syncthreads();
+    const Slab<true> slab(gz + (size_t)tile * gz_rows * TW, TW, gz_rows, sub);
+    // The loads of plan waves still to come are issued on every path, at addresses clamped into their arrays, and
+    // the rare loads of a step (a slab row outside the LDS, a third step's pairs, a drive gradient to add to) are
+    // waited for inside their own branches.  The compiler then knows how many loads follow each prefetched one, and
+    // waiting for it does not wait for those issued after it.
+    // A plan wave's loads as they arrive: nothing derived from a loaded value is computed before it is needed
+    struct Pre {
+        int w;
+        int2 wv;                                // its record {woff, longest segment} (wave-uniform)
+        bool cold;                              // some pair of it names a slab row outside the LDS (wave-uniform)
+        bool wok;                               // the record is real and inside the plan (wave-uniform)
+        bool sok;                               // the group has a segment (w * 8 + gi < nseg)
+        int2 pr0, pr1;                          // the pairs of its first two steps as loaded
+        int4 sg;                                // the group's segment as loaded
+        float2 rec;                             // the row's gain and softplus(theta) as loaded
+    };
+    // the loads of plan wave k that need only its number (k >= n: the last plan wave's again, marked empty)
+    auto issue = [&](int k, Pre& it) __attribute__((always_inline)) {
+        const bool real = k < n;
+        k = min(k, n - 1);
+        it.w = w0 + k * dw;
+        const int r = k >> 6, kk = k & 63;
+        int vx = 0, vy = 0;
+#pragma unroll
+        for (int q = 0; q < BWD_LDS_WREC; ++q)
+            if (q == r) {
+                vx = __builtin_amdgcn_readlane(wrec[q].x, kk);
+                vy = __builtin_amdgcn_readlane(wrec[q].y, kk);
+            }
+        it.cold = (vy & WLDS_COLD) != 0;
+        vy &= ~WLDS_COLD;
+        it.wok = real && vx >= 0 && vy >= 0 && (long long)vx + 64 * (((long long)vy + 7) / 8) <= p.npos;
+        it.wv = it.wok ? make_int2(vx, vy) : make_int2(0, 0);
+        // (a step past the wave's last reads the first step's block again; with 6-byte pairs lanes 48-63 load a
+        // lane's below, which the staging never reads)
+        const int2* pq;
+        int ps;
+        if constexpr (PB == 8) {
+            pq = cw + it.wv.x + lane;
+            ps = 64;
+        } else {
+            pq = cw + (size_t)it.wv.x / 64 * 48 + min(lane, 47);
+            ps = 48;
+        }
+        it.pr0 = pq[0];
+        it.pr1 = pq[it.wv.y > 8 ? ps : 0];
+        it.sok = it.w * 8 + gi < p.nseg;
+        const int si = min(it.w * 8 + gi, p.nseg - 1);
+        it.sg = p.seg[si];
+        it.rec = *reinterpret_cast<const float2*>(epi.sinfo + si);
+    };
+    // whether the group's segment is real (load_segment's test)
+    auto live = [&](const Pre& it) { return it.wok && it.sok && it.sg.x >= 0 && it.sg.x < p.rows && it.sg.y < p.nslot; };
+    // the h lines of a plan wave's rows (row 0's where a group has none: the reader masks them)
+    auto hline = [&](const Pre& it) { return *at4u(hs, lhs, tile, live(it) ? it.sg.x : 0, sub); };
+    // one step of plan wave `cur`: the gathers of its pairs `pr` (8 slots of each group) and the sums; returns the step's
+    // weight-gradient partial of the lane's position
+    // (slots past a segment's end hold the pair (no row, 0), which gathers zeros; a silent row's slots gather nothing)
+    auto step = [&](bool cold, int2 pr, bool quiet, const float4& hc, float4& acc) __attribute__((always_inline)) {
+        int c[8];
+        float wt[8];
+        stage_pairs<PB>(slots, grp, sub, pr, false, nullptr, 0, c, wt);
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const unsigned cu = (SKIP && quiet) ? 0xFFFFFFFFu : (unsigned)c[u];
+            v[u] = cu < (unsigned)hot ? gs[cu * LPR + sub] : splat(0.f);
+        }
+        bool any = false;
+        if (cold) {                                   // (the plan waves with a pair outside the LDS: 1 in 8)
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                any |= ((SKIP && quiet) ? 0xFFFFFFFFu : (unsigned)c[u]) - (unsigned)hot < (unsigned)gz_rows;
+        }
+        if (__ballot(any)) {                          // (the loads go out together)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const unsigned cold_row = ((SKIP && quiet) ? 0xFFFFFFFFu : (unsigned)c[u]) - (unsigned)hot;
+                if (cold_row < (unsigned)gz_rows) v[u] = slab.get((int)cold_row, sub);
+            }
+            asm volatile("" ::"v"(v[0].x), "v"(v[1].x), "v"(v[2].x), "v"(v[3].x), "v"(v[4].x), "v"(v[5].x),
+                         "v"(v[6].x), "v"(v[7].x));   // (waited for here)
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) fma4(wt[u], v[u], acc);
+        float d[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) d[u] = dot4(hc, v[u]);
+        return rs8(d, sub);
+    };
+    // Every plan wave issues the same vector-memory operations whatever its rows: 5 loads (plan wave k + 2's four,
+    // plan wave k + 1's h lines) and 7 stores (two steps' weight-gradient partials, the row's gz, drive gradient,
+    // split-row sum, gain and threshold partials).  A store that does not apply gets an offset past its buffer, which
+    // the hardware drops.  Stores count in the same counter as loads: with their number fixed, waiting for a
+    // prefetched load does not wait for the stores issued after it.
+    constexpr unsigned OFF = 0x80000000u;
+    auto rsrc = [](const void* b, long long bytes) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(b), (short)0,
+                                                 b ? (int)min(bytes, 0x7FFFFFFFLL) : 0, 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t r_gw = rsrc(gwpart ? gwpart + (size_t)tile * gw_ld : nullptr, gw_ld * 4);
+    const __amdgpu_buffer_rsrc_t r_gz = rsrc(epi.gz_out + (size_t)tile * epi.lgz.tile, epi.lgz.tile * 4);
+    const __amdgpu_buffer_rsrc_t r_gd = rsrc(epi.gdrive + (size_t)tile * epi.lgd.tile, epi.lgd.tile * 4);
+    const __amdgpu_buffer_rsrc_t r_pt = rsrc(part ? part + (size_t)tile * lp.tile : nullptr, lp.tile * 4);
+    const __amdgpu_buffer_rsrc_t r_gg = rsrc(epi.ggain_part + (size_t)tile * epi.gp_ld, epi.gp_ld * 4);
+    const __amdgpu_buffer_rsrc_t r_gs = rsrc(epi.gsum_part + (size_t)tile * epi.gp_ld, epi.gp_ld * 4);
+    // (the buffer stores take the values' bits: a float handed over as it is would be converted to an integer)
+    auto st4 = [](const float4& v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+        const u32x4 t = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+        __builtin_amdgcn_raw_buffer_store_b128(t, r, off, 0, 2);        // (nontemporal)
+    };
+    auto st1 = [](float v, __amdgpu_buffer_rsrc_t r, unsigned off, int nt) {
+        if (nt)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 2);
+        else
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+    };
+    // Plan wave k with its loads in flight: cur (its own, issued two plan waves ago) and hr (its rows' h lines, one
+    // plan wave ago); it issues nx's h lines (plan wave k + 1) into hn and plan wave k + 2's loads into n2.  The caller
+    // rotates three Pre and two h slots by unrolling (below) instead of copying them: a copy of a register whose load
+    // is still in flight would wait for it.
+    auto plan_wave = [&](int k, const Pre& cur, const float4& hr, const Pre& nx, float4& hn, Pre& n2)
+        __attribute__((always_inline)) {
+        issue(k + 2, n2);
+        hn = hline(nx);
+        const bool lv = live(cur);
+        const float4 hc = sel4(lv, hr, splat(0.f));
+        // a row that fires on none of the tile's samples gathers nothing (k_bwd)
+        const bool quiet = SKIP && group_silent(hc);
+        float4 acc = splat(0.f);
+        const int L = cur.wv.y;                       // (0 unless the record is real)
+        float pend0 = 0.f, pend1 = 0.f;
+        if (L > 0) pend0 = step(cur.cold, cur.pr0, quiet, hc, acc);
+        if (L > 8) pend1 = step(cur.cold, cur.pr1, quiet, hc, acc);
+        if (L > 16) {                                 // (rare: a third step and more, their pairs loaded here)
+            const PairLoad<PB> q(cw, cur.wv.x, lane);
+            for (int j = 2; 8 * j < L; ++j) {
+                int2 pr = q.step(j);
+                asm volatile("" : "+v"(pr.x), "+v"(pr.y));
+                const float pe = step(cur.cold, pr, quiet, hc, acc);
+                st1(pe, r_gw, (unsigned)(cur.wv.x + 64 * j + lane) * 4u, 1);
+            }
+        }
+        st1(pend0, r_gw, L > 0 ? (unsigned)(cur.wv.x + lane) * 4u : OFF, 1);
+        st1(pend1, r_gw, L > 8 ? (unsigned)(cur.wv.x + 64 + lane) * 4u : OFF, 1);
+        // the row's neuron backward (bwd_finish, MODE 1), or a split row's partial sum
+        const bool whole = lv && cur.sg.y < 0;
+        const HopBack b = hop_back(acc, hc, cur.rec.x, cur.rec.y);
+        const int d = cur.sg.z, dr = d <= -3 ? -d - 3 : d;
+        float4 gdv = splat(0.f);
+        const bool add = whole && d >= 0 && !epi.first;
+        if (__ballot(add)) {                          // (rare: a drive gradient written by a layer above)
+            const float4 g = *at4u(epi.gdrive, epi.lgd, tile, add ? dr : 0, sub);
+            gdv = sel4(add, g, gdv);
+            asm volatile("" : "+v"(gdv.x), "+v"(gdv.y), "+v"(gdv.z), "+v"(gdv.w));
+        }
+        add4(b.gz, gdv);
+        const unsigned line = (unsigned)sub * 16u;
+        st4(b.gz, r_gz, whole ? (unsigned)cur.sg.x * (TW * 4u) + line : OFF);
+        st4(gdv, r_gd, whole && dr >= 0 ? (unsigned)dr * (TW * 4u) + line : OFF);
+        st4(acc, r_pt, lv && cur.sg.y >= 0 ? (unsigned)cur.sg.y * (TW * 4u) + line : OFF);
+        const unsigned col = whole && sub == 0 ? (unsigned)(cur.w * 8 + gi) * 4u : OFF;
+        st1(b.pg, r_gg, col, 0);
+        st1(b.ps, r_gs, col, 0);
+    };
+    if (n <= 0) return;
+    Pre p0, p1, p2;                             // plan wave k's loads in slot k % 3
+    float4 h0, h1;                              // its rows' h lines in slot k % 2
+    issue(0, p0);
+    issue(1, p1);
+    h0 = hline(p0);
+    // the 7 stores a plan wave ends with, all dropped: the first plan wave then finds the operations in flight in the
+    // same order as every later one, and its waits are counted as theirs
+    st1(0.f, r_gw, OFF, 1);
+    st1(0.f, r_gw, OFF, 1);
+    st4(splat(0.f), r_gz, OFF);
+    st4(splat(0.f), r_gd, OFF);
+    st4(splat(0.f), r_pt, OFF);
+    st1(0.f, r_gg, OFF, 0);
+    st1(0.f, r_gs, OFF, 0);
+    int k = 0;
+    for (; k + 6 <= n; k += 6) {
+        plan_wave(k, p0, h0, p1, h1, p2);
+        plan_wave(k + 1, p1, h1, p2, h0, p0);
+        plan_wave(k + 2, p2, h0, p0, h1, p1);
+        plan_wave(k + 3, p0, h1, p1, h0, p2);
+        plan_wave(k + 4, p1, h0, p2, h1, p0);
+        plan_wave(k + 5, p2, h1, p0, h0, p1);
+    }
+    if (k < n) plan_wave(k, p0, h0, p1, h1, p2);
+    if (k + 1 < n) plan_wave(k + 1, p1, h1, p2, h0, p0);
+    if (k + 2 < n) plan_wave(k + 2, p2, h0, p0, h1, p1);
+    if (k + 3 < n) plan_wave(k + 3, p0, h1, p1, h0, p2);
+    if (k + 4 < n) plan_wave(k + 4, p1, h0, p2, h1, p0);
 }
 
 // ------------------------------------------------------------------------------------------------ obs / logits
@@ -1095,6 +1372,59 @@ hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, in
         default:
             return hipErrorInvalidValue;
     }
+}
+
+int bwd_lds_rows() {
+    int dev = 0, cap = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cap, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return 0;
+    size_t stat = 0;
+    for (const void* k : {reinterpret_cast<const void*>(&k_bwd_lds<8, false>), reinterpret_cast<const void*>(&k_bwd_lds<6, false>),
+                          reinterpret_cast<const void*>(&k_bwd_lds<8, true>), reinterpret_cast<const void*>(&k_bwd_lds<6, true>)}) {
+        hipFuncAttributes a{};
+        if (hipFuncGetAttributes(&a, k) != hipSuccess) return 0;
+        stat = std::max(stat, a.sharedSizeBytes);
+    }
+    if ((size_t)cap <= stat) return 0;
+    return (int)std::min<size_t>(((size_t)cap - stat) / (TW * 4), BWD_LDS_MAXROWS);
+}
+
+hipError_t launch_bwd_lds(const Plan& p, const int2* wlds, const int2* cw, const float* gz, int gz_rows,
+                          const int* hot_rows, int hot, const float* hsrc, Lay lhs, float* gwpart, long long gw_ld,
+                          const BwdEpi& epi, float* part, Lay lp, int T, int S, hipStream_t st) {
+    // (codes name rows below hot + gz_rows: with 6-byte pairs that must stay below 0xFFFF, which names no row)
+    if (epi.mode != 1 || !epi.sinfo || !epi.h || !epi.gz_out || !epi.gdrive || !epi.ggain_part || !epi.gsum_part ||
+        !wlds || !hot_rows || hot < 1 || hot > BWD_LDS_MAXROWS || hot > gz_rows || S < 1 || lhs.row != TW ||
+        lp.row != TW || epi.lgz.row != TW || epi.lgd.row != TW || (p.pb != 8 && p.pb != 6) ||
+        (p.pb == 6 && (long long)hot + gz_rows > PAIR6_MAX_ROWS))
+        return hipErrorInvalidValue;
+    if (p.nwave > 0) {
+        S = std::max(S, (p.nwave + 64 * BWD_LDS_WREC * BWD_LDS_NW - 1) / (64 * BWD_LDS_WREC * BWD_LDS_NW));
+        const void* k = p.pb == 6 ? (epi.skip_silent ? reinterpret_cast<const void*>(&k_bwd_lds<6, true>)
+                                                     : reinterpret_cast<const void*>(&k_bwd_lds<6, false>))
+                                  : (epi.skip_silent ? reinterpret_cast<const void*>(&k_bwd_lds<8, true>)
+                                                     : reinterpret_cast<const void*>(&k_bwd_lds<8, false>));
+        const size_t lds = (size_t)hot * TW * 4;
+        const hipError_t attr = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (attr != hipSuccess) return attr;
+        const dim3 grid((unsigned)((long long)T * S));
+#define FG_BWD_LDS(P, K) k_bwd_lds<P, K><<<grid, BWD_LDS_NW * 64, lds, st>>>(p, wlds, cw, gz, gz_rows, hot_rows, hot, \
+                                                                               hsrc, lhs, gwpart, gw_ld, epi, part, lp, T, S)
+        if (p.pb == 6) {
+            if (epi.skip_silent) FG_BWD_LDS(6, true); else FG_BWD_LDS(6, false);
+        } else {
+            if (epi.skip_silent) FG_BWD_LDS(8, true); else FG_BWD_LDS(8, false);
+        }
+#undef FG_BWD_LDS
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (p.nsplit > 0) {
+        k_bwd_combine<1, false><<<blocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, lp, epi, T);
+        return hipGetLastError();
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_fires_pack(const unsigned char* bytes, int rows, unsigned* bits, int T, hipStream_t st) {

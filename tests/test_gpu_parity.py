@@ -234,8 +234,9 @@ def test_skipping_silent_rows_changes_nothing(gpu_lib, monkeypatch, full, B, fla
 def test_pair_storage_changes_nothing(gpu_lib, monkeypatch, full, B, flags, tiles, plug):
     """A plan's (source, weight) pairs are stored in 6 bytes (weights, then 16-bit sources, per wave step) when the
     state its product gathers has at most 65,535 rows and its waves walk 3 steps or more on average (on the benchmark
-    network every product but the plug and hop 3's backward); FLYGUY_PAIR_BYTES=8 keeps the 8-byte pairs.  Logits,
-    every layer's state and all seven gradients are bit-identical either way: float32 states at B = 96 and 4096, one
+    network every product but the plug and hop 3's backward); FLYGUY_PAIR_BYTES=8 keeps the 8-byte pairs, =6 stores
+    every plan whose gathered state allows it in 6 bytes (the plug and hop 3's backward too).  Logits, every layer's
+    state and all seven gradients are bit-identical either way: float32 states at B = 96 and 4096, one
     and two tiles per backward workgroup, bfloat16 states (flags 1) at B = 192 and 4096, with a third of the neurons
     silenced so that the forward's silent-source drops (made after the staging with 6-byte pairs) are taken; and a
     network of the benchmark shape whose plug reads 32 inputs per sensory neuron (4 steps a wave, so its pairs take 6
@@ -268,3 +269,44 @@ def test_pair_storage_changes_nothing(gpu_lib, monkeypatch, full, B, flags, tile
         assert np.array_equal(a, b)
     for name, a, b in zip(NAMES, g8, g6):
         assert np.array_equal(a, b), name
+
+
+@pytest.mark.parametrize("net,B,mode,pb,skip", [("full", 4096, "auto", "", ""), ("full", 4096, "1", "6", "1"),
+                                                 ("full", 512, "auto", "", ""), ("full", 96, "1", "", "1"),
+                                                 ("scaled", 160, "1", "6", "")])
+def test_backward_staged_in_lds_changes_nothing(gpu_lib, monkeypatch, full, net, B, mode, pb, skip):
+    """The last hop's backward gathers the descending layer's gradient (1,332 rows, 170 kB a tile).  From 16 tiles up
+    (FLYGUY_BWD_LDS=1: at every batch) it runs k_bwd_lds: each workgroup stages the 1,216 most gathered of those rows
+    in LDS and gathers the other 116 (about 0.2% of the gathers) through the vector-memory path in the steps that
+    need one.  Its sums are those of the one-tile kernel it replaces (FLYGUY_BWD_TILES=1, FLYGUY_BWD_LDS=0), term for
+    term: all seven gradients are bit-identical on the benchmark network at B = 4096, 512 and 96 (three tiles: many
+    workgroups per tile), with 8- and 6-byte pairs, with the backward's silent-row skip forced on (FLYGUY_BWD_SKIP=1)
+    and a third of the neurons silenced so that it is taken; and on the 1/16 network, whose 83 descending rows all fit
+    the LDS."""
+    s, params = full if net == "full" else scaled_3hop(16)
+    P = [p.copy() for p in params]
+    rng = np.random.default_rng(B + 7)
+    P[2][rng.random(P[2].size) < 1 / 3] = 6.0                  # softplus(6) ~ 6: these neurons almost never fire
+    obs = rng.standard_normal((B, 517)).astype(np.float32)
+    dl = (rng.standard_normal((B, 90)) / B).astype(np.float32)
+    monkeypatch.setenv("FLYGUY_BWD_TILES", "1")
+    if pb:
+        monkeypatch.setenv("FLYGUY_PAIR_BYTES", pb)
+    if skip:
+        monkeypatch.setenv("FLYGUY_BWD_SKIP", skip)
+    out = {}
+    for lds in ("0", mode):
+        say(f"{net} B {B}: FLYGUY_BWD_LDS={lds} pairs {pb or 'by plan'} skip {skip or 'by plan'}")
+        monkeypatch.setenv("FLYGUY_BWD_LDS", lds)
+        core = Core(s, P, max_batch=B)
+        lg = core.forward(obs)
+        core.zero_grad()
+        core.backward(dl)
+        out[lds] = (lg, core.get(4))
+        del core
+    (l0, g0), (l1, g1) = out["0"], out[mode]
+    assert np.array_equal(l0, l1)
+    for name, a, b in zip(NAMES, g0, g1):
+        assert np.isfinite(b).all(), name
+        assert np.array_equal(a, b), name
+
