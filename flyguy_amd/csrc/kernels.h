@@ -168,13 +168,14 @@ hipError_t launch_bwd(const Plan& p, const int2* cw, const float* gz, Lay lg, in
                       bool pair = false);
 // The backward of a hop layer (epi.mode 1) whose gathered gradient rows (gz_rows, the hop's own rows) mostly fit the
 // LDS: each of the S workgroups per tile stages rows hot_rows[0 .. hot) of its tile's gz slab in LDS (LDS row r holds
-// slab row hot_rows[r]) and gathers from there.  The pairs cw carry codes instead of rows: code < hot names LDS row
+// slab row hot_rows[r]; row `hot` holds zeros) and gathers from there.  The pairs cw carry codes instead of rows: code < hot names LDS row
 // code, hot <= code < hot + gz_rows names slab row code - hot (gathered through the vector-memory path, only in steps
 // that need one), anything else no row.  One tile per workgroup: gwpart and the gain / threshold partials take one
 // row per tile, as launch_bwd without pair.  epi.sinfo is required (the rows' records in plan order).
 constexpr int BWD_LDS_NW = 12;                    // waves per workgroup (the slab takes a CU's LDS: one workgroup)
 constexpr int BWD_LDS_WREC = 4;                   // a wave walks at most 64 * BWD_LDS_WREC plan waves
-constexpr int BWD_LDS_MAXROWS = 1232;             // most rows staged: 154 kB, with 6 kB of pair staging beside them
+constexpr int BWD_LDS_MAXROWS = 1231;             // most rows staged: 154 kB with a row of zeros, and 6 kB of pair
+                                                  // staging beside them
 // the rows k_bwd_lds can stage on the current device (its LDS per workgroup less the kernel's static LDS, at most
 // BWD_LDS_MAXROWS), 0 if none
 int bwd_lds_rows();

@@ -770,6 +770,7 @@ __global__ __launch_bounds__(BWD_LDS_NW * 64) void k_bwd_lds(Plan p, const int2*
             const int i = (int)threadIdx.x + u * NT;
             if (i < hot * LPR) gs[i] = lv[u];
         }
+        if (threadIdx.x < LPR) gs[hot * LPR + threadIdx.x] = splat(0.f);     // row `hot`: zeros
     }
     __syncthreads();
     const Slab<true> slab(gz + (size_t)tile * gz_rows * TW, TW, gz_rows, sub);
@@ -829,31 +830,34 @@ __global__ __launch_bounds__(BWD_LDS_NW * 64) void k_bwd_lds(Plan p, const int2*
     auto hline = [&](const Pre& it) { return *at4u(hs, lhs, tile, live(it) ? it.sg.x : 0, sub); };
     // one step of plan wave `cur`: the gathers of its pairs `pr` (8 slots of each group) and the sums; returns the step's
     // weight-gradient partial of the lane's position
-    // (slots past a segment's end hold the pair (no row, 0), which gathers zeros; a silent row's slots gather nothing)
+    // (slots past a segment's end hold the pair (no row, 0), which gathers zeros, as does a silent row's: every code
+    // from hot up reads LDS row `hot`, which holds zeros, so that no slot's read is conditional)
     auto step = [&](bool cold, int2 pr, bool quiet, const float4& hc, float4& acc) __attribute__((always_inline)) {
         int c[8];
         float wt[8];
         stage_pairs<PB>(slots, grp, sub, pr, false, nullptr, 0, c, wt);
+        if (SKIP && quiet) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] = NO_ROW;
+        }
         float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const unsigned cu = (SKIP && quiet) ? 0xFFFFFFFFu : (unsigned)c[u];
-            v[u] = cu < (unsigned)hot ? gs[cu * LPR + sub] : splat(0.f);
-        }
-        bool any = false;
+        for (int u = 0; u < 8; ++u) v[u] = gs[min((unsigned)c[u], (unsigned)hot) * LPR + sub];
         if (cold) {                                   // (the plan waves with a pair outside the LDS: 1 in 8)
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                any |= ((SKIP && quiet) ? 0xFFFFFFFFu : (unsigned)c[u]) - (unsigned)hot < (unsigned)gz_rows;
-        }
-        if (__ballot(any)) {                          // (the loads go out together)
+            unsigned cr[8];
+            bool any = false;
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const unsigned cold_row = ((SKIP && quiet) ? 0xFFFFFFFFu : (unsigned)c[u]) - (unsigned)hot;
-                if (cold_row < (unsigned)gz_rows) v[u] = slab.get((int)cold_row, sub);
+                cr[u] = (unsigned)c[u] - (unsigned)hot;
+                any |= cr[u] < (unsigned)gz_rows;
             }
-            asm volatile("" ::"v"(v[0].x), "v"(v[1].x), "v"(v[2].x), "v"(v[3].x), "v"(v[4].x), "v"(v[5].x),
-                         "v"(v[6].x), "v"(v[7].x));   // (waited for here)
+            if (__ballot(any)) {                      // (the loads go out together)
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (cr[u] < (unsigned)gz_rows) v[u] = slab.get((int)cr[u], sub);
+                asm volatile("" ::"v"(v[0].x), "v"(v[1].x), "v"(v[2].x), "v"(v[3].x), "v"(v[4].x), "v"(v[5].x),
+                             "v"(v[6].x), "v"(v[7].x));   // (waited for here)
+            }
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) fma4(wt[u], v[u], acc);
@@ -1387,7 +1391,8 @@ int bwd_lds_rows() {
         stat = std::max(stat, a.sharedSizeBytes);
     }
     if ((size_t)cap <= stat) return 0;
-    return (int)std::min<size_t>(((size_t)cap - stat) / (TW * 4), BWD_LDS_MAXROWS);
+    const size_t rows = ((size_t)cap - stat) / (TW * 4);
+    return rows < 2 ? 0 : (int)std::min<size_t>(rows - 1, BWD_LDS_MAXROWS);      // (less the row of zeros)
 }
 
 hipError_t launch_bwd_lds(const Plan& p, const int2* wlds, const int2* cw, const float* gz, int gz_rows,
@@ -1405,7 +1410,7 @@ hipError_t launch_bwd_lds(const Plan& p, const int2* wlds, const int2* cw, const
                                                      : reinterpret_cast<const void*>(&k_bwd_lds<6, false>))
                                   : (epi.skip_silent ? reinterpret_cast<const void*>(&k_bwd_lds<8, true>)
                                                      : reinterpret_cast<const void*>(&k_bwd_lds<8, false>));
-        const size_t lds = (size_t)hot * TW * 4;
+        const size_t lds = (size_t)(hot + 1) * TW * 4;        // (and a row of zeros)
         const hipError_t attr = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (attr != hipSuccess) return attr;
         const dim3 grid((unsigned)((long long)T * S));
