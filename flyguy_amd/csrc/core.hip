@@ -521,7 +521,7 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
     long long max_slot = c->pp.nslot, max_pos = 1, max_rows = 1;
     c->hop.resize(K);
     if (const char* f = std::getenv("FLYGUY_BWD_LDS")) c->bwd_lds = f[0] == '0' ? 0 : (f[0] == '1' ? 1 : -1);
-    const int lds_cap = c->bwd_lds == 0 ? 0 : bwd_lds_rows();
+    const int lds_cap = c->bwd_lds == 0 ? 0 : (prec ? bwd_lds_rows16() : bwd_lds_rows());
     {
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -547,9 +547,9 @@ Core* build(const unsigned char* bytes, long long len, int max_batch, int prec) 
         d.cw = dalloc<int2>(*c, (size_t)(pair_bytes(d.fp.npos, d.fp.pb) / 8));
         d.tcw = dalloc<int2>(*c, (size_t)(pair_bytes(d.bp.npos, d.bp.pb) / 8));
         if (!d.gidx || !d.ridx || !d.gridx || !d.nid || !d.drow || !d.cw || !d.tcw) return nullptr;
-        // the last hop's backward (a hop layer below it) through k_bwd_lds, float32 states
+        // the last hop's backward (a hop layer below it) through k_bwd_lds / k_cbwd16_lds
         std::vector<int> hot;
-        if (prec == 0 && k == K - 1 && K >= 2 && lds_cap > 0 && bwd_lds_choice(h.crow, d.rows, lds_cap, hot) > 0) {
+        if (k == K - 1 && K >= 2 && lds_cap > 0 && bwd_lds_choice(h.crow, d.rows, lds_cap, hot) > 0) {
             std::vector<int> rank(d.rows, -1);
             for (size_t r = 0; r < hot.size(); ++r) rank[hot[r]] = (int)r;
             const int nh = (int)hot.size();
@@ -1046,7 +1046,9 @@ static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
     int cur = 0;
     for (int k = K; k >= 1; --k) {
         HopD& d = c.hop[k - 1];
-        const bool pair = k >= 2 && d.pair_bwd;     // (the sensory layer's backward always takes one tile)
+        // (the sensory layer's backward always takes one tile; the gathered rows staged in LDS as in backward())
+        const bool lds = d.lds_hot > 0 && k >= 2 && (c.bwd_lds == 1 || (c.bwd_lds < 0 && T >= BWD_LDS_MIN_TILES));
+        const bool pair = k >= 2 && d.pair_bwd && !lds;
         BwdEpi16 e;
         e.gdrive = c.gdrive;
         e.n_s = c.n_s;
@@ -1075,8 +1077,13 @@ static bool backward16(Core& c, const float* dlogits, int B, bool fresh) {
         e.sinfo = d.bsinfo;
         {
             Timed t(c, ST_BHOP + std::min(k - 1, 7));
-            FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, c.gwpart, d.bp.npos, e, c.part, T, st,
-                                   pair), false);
+            if (lds)
+                FG_CHECK(launch_bwd16c_lds(d.bp.view(), d.wave_lds, d.tcw_lds, s16(c.gz[cur]), d.rows, d.hot_rows,
+                                           d.lds_hot, c.gwpart, d.bp.npos, e, c.part, T,
+                                           std::max(1, (c.cus > 0 ? c.cus : 256) / T), st), false);
+            else
+                FG_CHECK(launch_bwd16c(d.bp.view(), d.tcw, s16(c.gz[cur]), d.rows, c.gwpart, d.bp.npos, e, c.part, T, st,
+                                       pair), false);
         }
         Timed t(c, ST_REDUCE);
         // the layer's sums in one launch: each writes its own gradient array

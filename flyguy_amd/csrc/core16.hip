@@ -320,25 +320,55 @@ __device__ __forceinline__ void bwd_inputs16(const BwdEpi16& e, int j, int d, in
     in.sp = r.y;
 }
 
+// A hop layer's neuron backward for (row, tile) over the lane's 8 samples (hop_back in kernels.hip): gz = g gain with
+// g = gh where the stored h > 0, the tile's sums pg = sum g z (from the stored h, see k_bwd) and ps = sum g
+struct HopBack16 {
+    float gz[8];
+    float pg, ps;
+};
+__device__ __forceinline__ HopBack16 hop_back16(const float (&gh)[8], const u32x4& hr, float gn, float sp) {
+    float g[8], h[8];
+    float sg = 0.f, sgh = 0.f;
+    unpack8<BF16>(hr, h);
+    HopBack16 b;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        g[k] = h[k] > 0.f ? gh[k] : 0.f;
+        b.gz[k] = g[k] * gn;
+        sg += g[k];
+        sgh = fmaf(g[k], h[k], sgh);
+    }
+    b.ps = gsum8(sg);
+    b.pg = gn != 0.f ? (gsum8(sgh) + sp * b.ps) / gn : 0.f;
+    return b;
+}
+
 template <int MODE>
 // keep (optional): the row's gain and threshold partials of the tile are returned there instead of stored
 // gcol: as in bwd_finish
 __device__ __forceinline__ void bwd_finish16(const BwdEpi16& e, int j, int tile, int sub, const float (&gh)[8],
                                              const BwdIn16& in, float2* keep = nullptr, int gcol = -1) {
-    float g[8], gzv[8], h[8];
-    float sg = 0.f, sgh = 0.f;
-    unpack8<BF16>(in.hr, h);
+    float gzv[8], ps, pg;
+    if constexpr (MODE == 1) {
+        const HopBack16 hb = hop_back16(gh, in.hr, in.gn, in.sp);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        g[k] = h[k] > 0.f ? gh[k] : 0.f;
-        gzv[k] = g[k] * in.gn;
-        sg += g[k];
-        sgh = fmaf(g[k], MODE == 1 ? h[k] : in.z[k], sgh);
+        for (int k = 0; k < 8; ++k) gzv[k] = hb.gz[k];
+        ps = hb.ps;
+        pg = hb.pg;
+    } else {
+        float g[8], h[8];
+        float sg = 0.f, sgh = 0.f;
+        unpack8<BF16>(in.hr, h);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            g[k] = h[k] > 0.f ? gh[k] : 0.f;
+            gzv[k] = g[k] * in.gn;
+            sg += g[k];
+            sgh = fmaf(g[k], in.z[k], sgh);
+        }
+        ps = gsum8(sg);
+        pg = gsum8(sgh);
     }
-    const float ps = gsum8(sg);
-    float pg;
-    if constexpr (MODE == 1) pg = in.gn != 0.f ? (gsum8(sgh) + in.sp * ps) / in.gn : 0.f;   // (see k_bwd)
-    else pg = gsum8(sgh);
     if (keep) {
         *keep = make_float2(pg, ps);
     } else if (sub == 0) {
@@ -665,6 +695,286 @@ hipError_t launch_fwd16c_lds(const Plan& p, const int2* cw, const unsigned short
     }
     if (p.nsplit > 0) {
         k_cfwd16_combine<<<nblocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, epi, T);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+// The last hop's backward with the descending layer's gradient staged in LDS: k_bwd_lds (kernels.hip) over
+// bfloat16 states.  The `hot` most gathered rows of the tile's gz slab (64 samples, 128 bytes a row) sit in LDS, with a
+// row of zeros after them; a pair's code names an LDS row (code < hot) or a slab row (hot + row), and plan waves marked
+// WLDS_COLD gather their slab rows through the vector-memory path.  The sums are k_cbwd16's (one tile per workgroup),
+// term for term in the same order; every plan wave issues the same loads and stores, as in k_bwd_lds.
+template <int PB, bool SKIP>
+__global__ __launch_bounds__(BWD_LDS_NW * 64) void k_cbwd16_lds(Plan p, const int2* __restrict__ wlds,
+                                                               const int2* __restrict__ cw, const bf16_t* __restrict__ gz,
+                                                               int gz_rows, const int* __restrict__ hot_rows, int hot,
+                                                               float* __restrict__ gwpart, long long gw_ld, BwdEpi16 epi,
+                                                               float* __restrict__ part, int T, int S) {
+    constexpr int NT = BWD_LDS_NW * 64;
+    constexpr int STAGE = (BWD_LDS_MAXROWS * LPR + NT - 1) / NT;
+    __shared__ __align__(16) int2 slots[NT / LPR][LPR];
+    extern __shared__ __align__(16) u32x4 gs16[];          // LDS row r: slab row hot_rows[r]; row `hot`: zeros
+    int s;
+    const int tile = tile_of(blockIdx.x, S, T, s);
+    const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7, lane = threadIdx.x & 63, gi = grp & 7;
+    const int w0 = __builtin_amdgcn_readfirstlane(s * BWD_LDS_NW + (int)(threadIdx.x >> 6)), dw = S * BWD_LDS_NW;
+    const int n = w0 < p.nwave ? min((p.nwave - 1 - w0) / dw + 1, 64 * BWD_LDS_WREC) : 0;
+    int2 wrec[BWD_LDS_WREC];
+#pragma unroll
+    for (int r = 0; r < BWD_LDS_WREC; ++r)
+        wrec[r] = 64 * r + lane < n ? wlds[w0 + (64 * r + lane) * dw] : make_int2(0, 0);
+    const u32x4* gt = reinterpret_cast<const u32x4*>(gz + (size_t)tile * gz_rows * TW16);
+    {
+        int ri[STAGE];
+        u32x4 lv[STAGE];
+#pragma unroll
+        for (int u = 0; u < STAGE; ++u) {
+            const int i = (int)threadIdx.x + u * NT;
+            ri[u] = i < hot * LPR ? hot_rows[i / LPR] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < STAGE; ++u) {
+            const int i = (int)threadIdx.x + u * NT;
+            lv[u] = (unsigned)ri[u] < (unsigned)gz_rows ? gt[(size_t)ri[u] * LPR + (i % LPR)] : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < STAGE; ++u) {
+            const int i = (int)threadIdx.x + u * NT;
+            if (i < hot * LPR) gs16[i] = lv[u];
+        }
+        if (threadIdx.x < LPR) gs16[hot * LPR + threadIdx.x] = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(gz + (size_t)tile * gz_rows * TW16), (short)0, gz_rows * 128, 0x00020000);
+    struct Pre {
+        int w;
+        int2 wv;
+        bool wok, cold, sok;
+        int2 pr0, pr1;
+        int4 sg;
+        float2 rec;
+    };
+    auto issue = [&](int k, Pre& it) __attribute__((always_inline)) {
+        const bool real = k < n;
+        k = min(k, n - 1);
+        it.w = w0 + k * dw;
+        const int r = k >> 6, kk = k & 63;
+        int vx = 0, vy = 0;
+#pragma unroll
+        for (int q = 0; q < BWD_LDS_WREC; ++q)
+            if (q == r) {
+                vx = __builtin_amdgcn_readlane(wrec[q].x, kk);
+                vy = __builtin_amdgcn_readlane(wrec[q].y, kk);
+            }
+        it.cold = (vy & WLDS_COLD) != 0;
+        vy &= ~WLDS_COLD;
+        it.wok = real && vx >= 0 && vy >= 0 && (long long)vx + 64 * (((long long)vy + 7) / 8) <= p.npos;
+        it.wv = it.wok ? make_int2(vx, vy) : make_int2(0, 0);
+        const int2* pq;
+        int ps;
+        if constexpr (PB == 8) {
+            pq = cw + it.wv.x + lane;
+            ps = 64;
+        } else {
+            pq = cw + (size_t)it.wv.x / 64 * 48 + min(lane, 47);
+            ps = 48;
+        }
+        it.pr0 = pq[0];
+        it.pr1 = pq[it.wv.y > 8 ? ps : 0];
+        it.sok = it.w * 8 + gi < p.nseg;
+        const int si = min(it.w * 8 + gi, p.nseg - 1);
+        it.sg = p.seg[si];
+        it.rec = *reinterpret_cast<const float2*>(epi.sinfo + si);
+    };
+    auto live = [&](const Pre& it) { return it.wok && it.sok && it.sg.x >= 0 && it.sg.x < p.rows && it.sg.y < p.nslot; };
+    auto hline = [&](const Pre& it) { return ldr8(epi.h, epi.rows, tile, live(it) ? it.sg.x : 0, sub); };
+    // one step: gathers from LDS (every code from hot up reads the row of zeros), the sums, the step's partial
+    auto step = [&](bool cold, int2 pr, bool quiet, const u32x4& hc, float (&acc)[8]) __attribute__((always_inline)) {
+        int c[8];
+        float wt[8];
+        stage_pairs<PB>(slots, grp, sub, pr, false, nullptr, 0, c, wt);
+        if (SKIP && quiet) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] = NO_ROW;
+        }
+        u32x4 raw[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) raw[u] = gs16[min((unsigned)c[u], (unsigned)hot) * LPR + sub];
+        if (cold) {
+            unsigned cr[8];
+            bool any = false;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                cr[u] = (unsigned)c[u] - (unsigned)hot;
+                any |= cr[u] < (unsigned)gz_rows;
+            }
+            if (__ballot(any)) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (cr[u] < (unsigned)gz_rows) raw[u] = gather16(rs, (int)cr[u], sub);
+                asm volatile("" ::"v"(raw[0][0]), "v"(raw[1][0]), "v"(raw[2][0]), "v"(raw[3][0]), "v"(raw[4][0]),
+                             "v"(raw[5][0]), "v"(raw[6][0]), "v"(raw[7][0]));   // (waited for here)
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u += 2) fma_pair(wt[u], wt[u + 1], raw[u], raw[u + 1], acc);
+        float d[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) d[u] = dot8(hc, raw[u]);
+        return rs8(d, sub);
+    };
+    constexpr unsigned OFF = 0x80000000u;
+    auto rsrc = [](const void* b, long long bytes) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(b), (short)0,
+                                                 b ? (int)min(bytes, 0x7FFFFFFFLL) : 0, 0x00020000);
+    };
+    const __amdgpu_buffer_rsrc_t r_gw = rsrc(gwpart ? gwpart + (size_t)tile * gw_ld : nullptr, gw_ld * 4);
+    const __amdgpu_buffer_rsrc_t r_gz = rsrc(epi.gz_out + (size_t)tile * epi.rows * TW16, (long long)epi.rows * 128);
+    const __amdgpu_buffer_rsrc_t r_gd = rsrc(epi.gdrive + (size_t)tile * epi.n_s * TW16, (long long)epi.n_s * 256);
+    const __amdgpu_buffer_rsrc_t r_pt = rsrc(part ? part + (size_t)tile * p.nslot * TW16 : nullptr, (long long)p.nslot * 256);
+    const __amdgpu_buffer_rsrc_t r_gg = rsrc(epi.ggain_part + (size_t)tile * epi.gp_ld, epi.gp_ld * 4);
+    const __amdgpu_buffer_rsrc_t r_gs = rsrc(epi.gsum_part + (size_t)tile * epi.gp_ld, epi.gp_ld * 4);
+    // (the buffer stores take the values' bits; aux 2: nontemporal, as st8 and the float32 kernels' stores)
+    auto st1 = [](float v, __amdgpu_buffer_rsrc_t r, unsigned off) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+    };
+    auto st8f = [](const float (&v)[8], __amdgpu_buffer_rsrc_t r, unsigned off) {     // 8 floats, off 32-byte aligned
+        const u32x4 a = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+        const u32x4 b = {__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])};
+        __builtin_amdgcn_raw_buffer_store_b128(a, r, off, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(b, r, off == OFF ? OFF : off + 16u, 0, 0);
+    };
+    // Plan wave k (k_bwd_lds's plan_wave): 5 loads and 10 stores whatever its rows
+    auto plan_wave = [&](int k, const Pre& cur, const u32x4& hr, const Pre& nx, u32x4& hn, Pre& n2)
+        __attribute__((always_inline)) {
+        issue(k + 2, n2);
+        hn = hline(nx);
+        const bool lv = live(cur);
+        const u32x4 hc = lv ? hr : u32x4{0u, 0u, 0u, 0u};
+        const bool quiet = SKIP && group_silent(bf16_lane_fires(hc));
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        const int L = cur.wv.y;
+        float pend0 = 0.f, pend1 = 0.f;
+        if (L > 0) pend0 = step(cur.cold, cur.pr0, quiet, hc, acc);
+        if (L > 8) pend1 = step(cur.cold, cur.pr1, quiet, hc, acc);
+        if (L > 16) {                                 // (rare: a third step and more, their pairs loaded here)
+            const PairLoad<PB> q(cw, cur.wv.x, lane);
+            for (int j = 2; 8 * j < L; ++j) {
+                int2 pr = q.step(j);
+                asm volatile("" : "+v"(pr.x), "+v"(pr.y));
+                const float pe = step(cur.cold, pr, quiet, hc, acc);
+                st1(pe, r_gw, (unsigned)(cur.wv.x + 64 * j + lane) * 4u);
+            }
+        }
+        st1(pend0, r_gw, L > 0 ? (unsigned)(cur.wv.x + lane) * 4u : OFF);
+        st1(pend1, r_gw, L > 8 ? (unsigned)(cur.wv.x + 64 + lane) * 4u : OFF);
+        const bool whole = lv && cur.sg.y < 0;
+        const HopBack16 b = hop_back16(acc, hc, cur.rec.x, cur.rec.y);
+        const int d = cur.sg.z, dr = d <= -3 ? -d - 3 : d;
+        float gd[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        const bool add = whole && d >= 0 && !epi.first;
+        if (__ballot(add)) {                          // (rare: a drive gradient written by a layer above)
+            float g[8];
+            ldf8(f8p(epi.gdrive, epi.n_s, tile, add ? dr : 0, sub), g);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) gd[m] = add ? g[m] : 0.f;
+            asm volatile("" : "+v"(gd[0]), "+v"(gd[1]), "+v"(gd[2]), "+v"(gd[3]), "+v"(gd[4]), "+v"(gd[5]), "+v"(gd[6]),
+                         "+v"(gd[7]));
+        }
+        float v[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) v[m] = gd[m] + b.gz[m];
+        u32x4 o;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) o[m] = pack2(b.gz[2 * m], b.gz[2 * m + 1]);
+        __builtin_amdgcn_raw_buffer_store_b128(o, r_gz, whole ? (unsigned)cur.sg.x * 128u + (unsigned)sub * 16u : OFF, 0, 2);
+        st8f(v, r_gd, whole && dr >= 0 ? (unsigned)dr * 256u + (unsigned)sub * 32u : OFF);
+        st8f(acc, r_pt, lv && cur.sg.y >= 0 ? (unsigned)cur.sg.y * 256u + (unsigned)sub * 32u : OFF);
+        const unsigned col = whole && sub == 0 ? (unsigned)(cur.w * 8 + gi) * 4u : OFF;
+        st1(b.pg, r_gg, col);
+        st1(b.ps, r_gs, col);
+    };
+    if (n <= 0) return;
+    Pre p0, p1, p2;
+    u32x4 h0, h1;
+    issue(0, p0);
+    issue(1, p1);
+    h0 = hline(p0);
+    {                                           // (the 10 stores a plan wave ends with, all dropped: k_bwd_lds)
+        const float z8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        st1(0.f, r_gw, OFF);
+        st1(0.f, r_gw, OFF);
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, r_gz, OFF, 0, 2);
+        st8f(z8, r_gd, OFF);
+        st8f(z8, r_pt, OFF);
+        st1(0.f, r_gg, OFF);
+        st1(0.f, r_gs, OFF);
+    }
+    int k = 0;
+    for (; k + 6 <= n; k += 6) {
+        plan_wave(k, p0, h0, p1, h1, p2);
+        plan_wave(k + 1, p1, h1, p2, h0, p0);
+        plan_wave(k + 2, p2, h0, p0, h1, p1);
+        plan_wave(k + 3, p0, h1, p1, h0, p2);
+        plan_wave(k + 4, p1, h0, p2, h1, p0);
+        plan_wave(k + 5, p2, h1, p0, h0, p1);
+    }
+    if (k < n) plan_wave(k, p0, h0, p1, h1, p2);
+    if (k + 1 < n) plan_wave(k + 1, p1, h1, p2, h0, p0);
+    if (k + 2 < n) plan_wave(k + 2, p2, h0, p0, h1, p1);
+    if (k + 3 < n) plan_wave(k + 3, p0, h1, p1, h0, p2);
+    if (k + 4 < n) plan_wave(k + 4, p1, h0, p2, h1, p0);
+}
+
+int bwd_lds_rows16() {
+    int dev = 0, cap = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cap, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return 0;
+    size_t stat = 0;
+    for (const void* k : {reinterpret_cast<const void*>(&k_cbwd16_lds<8, false>), reinterpret_cast<const void*>(&k_cbwd16_lds<6, false>),
+                          reinterpret_cast<const void*>(&k_cbwd16_lds<8, true>), reinterpret_cast<const void*>(&k_cbwd16_lds<6, true>)}) {
+        hipFuncAttributes a{};
+        if (hipFuncGetAttributes(&a, k) != hipSuccess) return 0;
+        stat = std::max(stat, a.sharedSizeBytes);
+    }
+    if ((size_t)cap <= stat) return 0;
+    const size_t rows = ((size_t)cap - stat) / 128;
+    return rows < 2 ? 0 : (int)std::min<size_t>(rows - 1, BWD_LDS_MAXROWS);      // (less the row of zeros)
+}
+
+hipError_t launch_bwd16c_lds(const Plan& p, const int2* wlds, const int2* cw, const unsigned short* gz, int gz_rows,
+                             const int* hot_rows, int hot, float* gwpart, long long gw_ld, const BwdEpi16& epi,
+                             float* part, int T, int S, hipStream_t st) {
+    if (epi.mode != 1 || !epi.sinfo || !epi.h || !epi.gz_out || !epi.gdrive || !epi.ggain_part || !epi.gsum_part ||
+        !wlds || !hot_rows || hot < 1 || hot > BWD_LDS_MAXROWS || hot > gz_rows || S < 1 || (p.pb != 8 && p.pb != 6) ||
+        (p.pb == 6 && (long long)hot + gz_rows > PAIR6_MAX_ROWS))
+        return hipErrorInvalidValue;
+    if (p.nwave > 0) {
+        S = std::max(S, (p.nwave + 64 * BWD_LDS_WREC * BWD_LDS_NW - 1) / (64 * BWD_LDS_WREC * BWD_LDS_NW));
+        const void* k = p.pb == 6 ? (epi.skip_silent ? reinterpret_cast<const void*>(&k_cbwd16_lds<6, true>)
+                                                     : reinterpret_cast<const void*>(&k_cbwd16_lds<6, false>))
+                                  : (epi.skip_silent ? reinterpret_cast<const void*>(&k_cbwd16_lds<8, true>)
+                                                     : reinterpret_cast<const void*>(&k_cbwd16_lds<8, false>));
+        const size_t lds = (size_t)(hot + 1) * 128;           // (and a row of zeros)
+        const hipError_t attr = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (attr != hipSuccess) return attr;
+        const dim3 grid((unsigned)((long long)T * S));
+#define FG_CBWD_LDS(P, K) k_cbwd16_lds<P, K><<<grid, BWD_LDS_NW * 64, lds, st>>>(p, wlds, cw, (const bf16_t*)gz, gz_rows, \
+                                                                                   hot_rows, hot, gwpart, gw_ld, epi, part, T, S)
+        if (p.pb == 6) {
+            if (epi.skip_silent) FG_CBWD_LDS(6, true); else FG_CBWD_LDS(6, false);
+        } else {
+            if (epi.skip_silent) FG_CBWD_LDS(8, true); else FG_CBWD_LDS(8, false);
+        }
+#undef FG_CBWD_LDS
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    if (p.nsplit > 0) {
+        k_cbwd16_combine<1, false><<<nblocks((long long)p.nsplit * T * LPR), WG, 0, st>>>(p, part, epi, T);
         return hipGetLastError();
     }
     return hipSuccess;

@@ -269,6 +269,12 @@ hipError_t launch_fwd16c_lds(const Plan& p, const int2* cw, const unsigned short
 // row per pair of tiles, ceil(T / 2) rows (the sensory layer, mode 2, always takes one tile per workgroup)
 hipError_t launch_bwd16c(const Plan& p, const int2* cw, const unsigned short* gz, int gz_rows, float* gwpart,
                          long long gw_ld, const BwdEpi16& epi, float* part, int T, hipStream_t st, bool pair = false);
+// the last hop's backward with the descending layer's gradient staged in LDS (launch_bwd_lds over bfloat16 states;
+// one tile of 64 samples per workgroup), and the rows it can stage on the current device
+hipError_t launch_bwd16c_lds(const Plan& p, const int2* wlds, const int2* cw, const unsigned short* gz, int gz_rows,
+                             const int* hot_rows, int hot, float* gwpart, long long gw_ld, const BwdEpi16& epi,
+                             float* part, int T, int S, hipStream_t st);
+int bwd_lds_rows16();
 hipError_t launch_export16(const unsigned short* src, int rows, float* dst, int B, hipStream_t st);
 hipError_t launch_readout_bwd_h16_mfma(const float* dl, const float* owT, const int* dn_inv, int n_act, int rows,
                                        const BwdEpi16& epi, int B, hipStream_t st);

@@ -271,18 +271,20 @@ def test_pair_storage_changes_nothing(gpu_lib, monkeypatch, full, B, flags, tile
         assert np.array_equal(a, b), name
 
 
-@pytest.mark.parametrize("net,B,mode,pb,skip", [("full", 4096, "auto", "", ""), ("full", 4096, "1", "6", "1"),
-                                                 ("full", 512, "auto", "", ""), ("full", 96, "1", "", "1"),
-                                                 ("scaled", 160, "1", "6", "")])
-def test_backward_staged_in_lds_changes_nothing(gpu_lib, monkeypatch, full, net, B, mode, pb, skip):
+@pytest.mark.parametrize("net,B,mode,pb,skip,flags", [("full", 4096, "auto", "", "", 0), ("full", 4096, "1", "6", "1", 0),
+                                                       ("full", 512, "auto", "", "", 0), ("full", 96, "1", "", "1", 0),
+                                                       ("scaled", 160, "1", "6", "", 0), ("full", 4096, "auto", "", "", 1),
+                                                       ("full", 192, "1", "6", "1", 1)])
+def test_backward_staged_in_lds_changes_nothing(gpu_lib, monkeypatch, full, net, B, mode, pb, skip, flags):
     """The last hop's backward gathers the descending layer's gradient (1,332 rows, 170 kB a tile).  From 16 tiles up
     (FLYGUY_BWD_LDS=1: at every batch) it runs k_bwd_lds: each workgroup stages the 1,216 most gathered of those rows
     in LDS and gathers the other 116 (about 0.2% of the gathers) through the vector-memory path in the steps that
     need one.  Its sums are those of the one-tile kernel it replaces (FLYGUY_BWD_TILES=1, FLYGUY_BWD_LDS=0), term for
     term: all seven gradients are bit-identical on the benchmark network at B = 4096, 512 and 96 (three tiles: many
     workgroups per tile), with 8- and 6-byte pairs, with the backward's silent-row skip forced on (FLYGUY_BWD_SKIP=1)
-    and a third of the neurons silenced so that it is taken; and on the 1/16 network, whose 83 descending rows all fit
-    the LDS."""
+    and a third of the neurons silenced so that it is taken; on the 1/16 network, whose 83 descending rows all fit
+    the LDS; and over bfloat16 states (flags 1: k_cbwd16_lds against k_cbwd16) at B = 4096 and 192 (three 64-sample
+    tiles)."""
     s, params = full if net == "full" else scaled_3hop(16)
     P = [p.copy() for p in params]
     rng = np.random.default_rng(B + 7)
@@ -296,9 +298,9 @@ def test_backward_staged_in_lds_changes_nothing(gpu_lib, monkeypatch, full, net,
         monkeypatch.setenv("FLYGUY_BWD_SKIP", skip)
     out = {}
     for lds in ("0", mode):
-        say(f"{net} B {B}: FLYGUY_BWD_LDS={lds} pairs {pb or 'by plan'} skip {skip or 'by plan'}")
+        say(f"{net} B {B} flags {flags}: FLYGUY_BWD_LDS={lds} pairs {pb or 'by plan'} skip {skip or 'by plan'}")
         monkeypatch.setenv("FLYGUY_BWD_LDS", lds)
-        core = Core(s, P, max_batch=B)
+        core = Core(s, P, max_batch=B, flags=flags)
         lg = core.forward(obs)
         core.zero_grad()
         core.backward(dl)
