@@ -72,6 +72,15 @@ __global__ __launch_bounds__(WG) void k_pack(JobTable<PackJob, PACK_JOBS> t) {
 }
 
 // ------------------------------------------------------------------------------------------------ forward
+// 16-byte load of a line that the pass reads once (a row's own h, re-drive or drive-gradient line, a split row's
+// partial sums): not kept in the L2, so that the slab being gathered keeps its place there (float32, B=4096: hop 2
+// backward 1.524 -> 1.504 ms, hop 3 backward 0.381 -> 0.370 ms; loads of the pairs with the hint made every hop slower:
+// all tiles read the same pairs)
+__device__ __forceinline__ float4 ld_stream(const float4* p) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
 // The row's own inputs of the finish (re-drive row d, gain, threshold), loaded before the edge loop so that their
 // latency hides behind the gathers.
 struct FwdIn {
@@ -82,7 +91,7 @@ struct FwdIn {
 // the row for a split one; nullptr: none)
 __device__ __forceinline__ FwdIn fwd_inputs(const FwdEpi& e, const float4* recs, int i, int d, int tile, int sub) {
     FwdIn in{make_float4(0.f, 0.f, 0.f, 0.f), 0.f, 0.f, 0.f};
-    if (e.drive && d >= 0) in.dv = *at4u(e.drive, e.ldrive, tile, d, sub);
+    if (e.drive && d >= 0) in.dv = ld_stream(at4u(e.drive, e.ldrive, tile, d, sub));
     if (recs) {
         const float4 r = recs[i];
         in.g = r.x;
@@ -283,6 +292,8 @@ __global__ __launch_bounds__(FWD_LDS_NW * 64) void k_plug_bwd_lds(const float* _
     };
     auto fetch = [&](int j, Row& r) {          // its gradient line and connection range
         const bool ok = j < n_s;
+        // (a cached load: the sensory finish has just written these lines, and reading them with the streaming
+        // hint made hop 1's backward slower, 1.385 -> 1.412 ms at B=4096)
         r.g = ok ? gdt[(size_t)j * LPR + sub] : splat(0.f);
         r.f0 = ok ? in_crow[j] : 0;
         r.f1 = ok ? in_crow[j + 1] : 0;
@@ -346,11 +357,11 @@ __device__ __forceinline__ void add_parts(const float* __restrict__ part, Lay lp
     for (; k + 8 <= n; k += 8) {
         float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = *at4(part, lp, tile, y + k + u, sub);
+        for (int u = 0; u < 8; ++u) v[u] = ld_stream(at4(part, lp, tile, y + k + u, sub));
 #pragma unroll
         for (int u = 0; u < 8; ++u) add4(v[u], acc);
     }
-    for (; k < n; ++k) add4(*at4(part, lp, tile, y + k, sub), acc);
+    for (; k < n; ++k) add4(ld_stream(at4(part, lp, tile, y + k, sub)), acc);
 }
 
 __global__ __launch_bounds__(WG) void k_fwd_combine(Plan p, const float* __restrict__ part, Lay lp, FwdEpi epi, int T) {
@@ -427,9 +438,9 @@ __device__ __forceinline__ BwdIn bwd_inputs_h(const BwdEpi& e, int j, int d, int
         in.d = d <= -3 ? -d - 3 : d;
         load = d >= 0 && !e.first;
     }
-    if (load) in.gd = *at4u(e.gdrive, e.lgd, tile, in.d, sub);
+    if (load) in.gd = ld_stream(at4u(e.gdrive, e.lgd, tile, in.d, sub));
     in.h = h;
-    if constexpr (MODE == 2) in.z = *at4u(e.z, e.lz, tile, j, sub);
+    if constexpr (MODE == 2) in.z = ld_stream(at4u(e.z, e.lz, tile, j, sub));
     const float2 r = *reinterpret_cast<const float2*>(recs ? recs + i : e.info + j);
     in.gn = r.x;
     in.sp = r.y;
@@ -438,7 +449,7 @@ __device__ __forceinline__ BwdIn bwd_inputs_h(const BwdEpi& e, int j, int d, int
 template <int MODE>
 __device__ __forceinline__ BwdIn bwd_inputs(const BwdEpi& e, int j, int d, int tile, int sub) {
     if constexpr (MODE == 0) return bwd_inputs_h<0>(e, j, d, tile, sub, splat(0.f));
-    return bwd_inputs_h<MODE>(e, j, d, tile, sub, *at4u(e.h, e.lh, tile, j, sub));
+    return bwd_inputs_h<MODE>(e, j, d, tile, sub, ld_stream(at4u(e.h, e.lh, tile, j, sub)));
 }
 
 // A hop layer's neuron backward for (row, tile) from gh, the gradient of its output: gz = g gain with g = gh where the
@@ -552,7 +563,7 @@ __global__ __launch_bounds__(WG) void k_bwd(Plan p, const int2* __restrict__ cw,
     // neuron backward (MODE 1, 2) a row that fires on none of the tile's samples has g = 0 there, so its gathers are
     // skipped (NO_ROW reads zeros without touching memory); its sums and partials are zero either way.
     float4 hj = splat(0.f);
-    if (live) hj = MODE == 0 ? *at4(hs, lhs, tile, sg.x, sub) : *at4u(hs, lhs, tile, sg.x, sub);
+    if (live) hj = MODE == 0 ? *at4(hs, lhs, tile, sg.x, sub) : ld_stream(at4u(hs, lhs, tile, sg.x, sub));
     const bool quiet = MODE != 0 && epi.skip_silent && group_silent(hj);
     const Slab<TILED> slab(gz + (size_t)tile * lg.tile, lg.row, gz_rows, sub);
     // the partial of (position, tile) of this lane's slot: one contiguous 256-byte block per wave and step
@@ -619,8 +630,8 @@ __global__ __launch_bounds__(WG) void k_bwd2(Plan p, const int2* __restrict__ cw
     // the source row's own lines first, and on a tile where the row fires on no sample its gathers are skipped (k_bwd)
     float4 hja = splat(0.f), hjb = splat(0.f);
     if (live) {
-        hja = *at4u(hs, lhs, ta, sg.x, sub);
-        if (hasb) hjb = *at4u(hs, lhs, tb, sg.x, sub);
+        hja = ld_stream(at4u(hs, lhs, ta, sg.x, sub));
+        if (hasb) hjb = ld_stream(at4u(hs, lhs, tb, sg.x, sub));
     }
     const bool quiet_a = epi.skip_silent && group_silent(hja), quiet_b = epi.skip_silent && group_silent(hjb);
     const Slab<true> sa(gz + (size_t)ta * lg.tile, lg.row, gz_rows, sub);
@@ -827,7 +838,7 @@ __global__ __launch_bounds__(BWD_LDS_NW * 64) void k_bwd_lds(Plan p, const int2*
     // whether the group's segment is real (load_segment's test)
     auto live = [&](const Pre& it) { return it.wok && it.sok && it.sg.x >= 0 && it.sg.x < p.rows && it.sg.y < p.nslot; };
     // the h lines of a plan wave's rows (row 0's where a group has none: the reader masks them)
-    auto hline = [&](const Pre& it) { return *at4u(hs, lhs, tile, live(it) ? it.sg.x : 0, sub); };
+    auto hline = [&](const Pre& it) { return ld_stream(at4u(hs, lhs, tile, live(it) ? it.sg.x : 0, sub)); };
     // one step of plan wave `cur`: the gathers of its pairs `pr` (8 slots of each group) and the sums; returns the step's
     // weight-gradient partial of the lane's position
     // (slots past a segment's end hold the pair (no row, 0), which gathers zeros, as does a silent row's: every code
@@ -928,7 +939,7 @@ __global__ __launch_bounds__(BWD_LDS_NW * 64) void k_bwd_lds(Plan p, const int2*
         float4 gdv = splat(0.f);
         const bool add = whole && d >= 0 && !epi.first;
         if (__ballot(add)) {                          // (rare: a drive gradient written by a layer above)
-            const float4 g = *at4u(epi.gdrive, epi.lgd, tile, add ? dr : 0, sub);
+            const float4 g = ld_stream(at4u(epi.gdrive, epi.lgd, tile, add ? dr : 0, sub));
             gdv = sel4(add, g, gdv);
             asm volatile("" : "+v"(gdv.x), "+v"(gdv.y), "+v"(gdv.z), "+v"(gdv.w));
         }
