@@ -277,8 +277,8 @@ def test_pair_storage_changes_nothing(gpu_lib, monkeypatch, full, B, flags, tile
                                                        ("full", 192, "1", "6", "1", 1)])
 def test_backward_staged_in_lds_changes_nothing(gpu_lib, monkeypatch, full, net, B, mode, pb, skip, flags):
     """The last hop's backward gathers the descending layer's gradient (1,332 rows, 170 kB a tile).  From 16 tiles up
-    (FLYGUY_BWD_LDS=1: at every batch) it runs k_bwd_lds: each workgroup stages the 1,216 most gathered of those rows
-    in LDS and gathers the other 116 (about 0.2% of the gathers) through the vector-memory path in the steps that
+    (FLYGUY_BWD_LDS=1: at every batch) it runs k_bwd_lds: each workgroup stages the 1,231 most gathered of those rows
+    in LDS and gathers the other 101 (about 0.2% of the gathers) through the vector-memory path in the steps that
     need one.  Its sums are those of the one-tile kernel it replaces (FLYGUY_BWD_TILES=1, FLYGUY_BWD_LDS=0), term for
     term: all seven gradients are bit-identical on the benchmark network at B = 4096, 512 and 96 (three tiles: many
     workgroups per tile), with 8- and 6-byte pairs, with the backward's silent-row skip forced on (FLYGUY_BWD_SKIP=1)

@@ -108,3 +108,33 @@ def test_random_graph_bfloat16_against_its_oracle(gpu_lib, seed):
     core.backward(dl)
     for name, g, w in zip(NAMES, core.get(4), o.backward(dl)):
         assert rel(g, w) <= 1e-2, (name, rel(g, w))
+
+
+@pytest.mark.parametrize("seed", range(32, 40))
+def test_random_graph_backward_staged_in_lds(gpu_lib, monkeypatch, seed):
+    """The last hop's backward with its gathered rows staged in LDS (k_bwd_lds / k_cbwd16_lds, forced at every batch
+    with FLYGUY_BWD_LDS=1; a random graph's last layer fits the LDS whole) against the one-tile kernel it replaces
+    (FLYGUY_BWD_TILES=1, FLYGUY_BWD_LDS=0), on random graphs of 2-4 hops: logits and all seven gradients bit for bit,
+    over float32 states (even seeds) and bfloat16 states (odd seeds), at batches of one to three tiles."""
+    s, params, rng, hops, fan = case(seed)
+    flags = seed % 2
+    B = int(rng.choice([64, 128, 192] if flags else [32, 96, 160]))
+    obs = rng.standard_normal((B, 517)).astype(np.float32)
+    dl = (rng.standard_normal((B, 90)) / B).astype(np.float32)
+    monkeypatch.setenv("FLYGUY_BWD_TILES", "1")
+    out = {}
+    for lds in ("0", "1"):
+        say(f"random graph {seed}: sizes {s['sizes']}, hops {hops}, fan {fan}, B {B}, flags {flags}: "
+            f"FLYGUY_BWD_LDS={lds}")
+        monkeypatch.setenv("FLYGUY_BWD_LDS", lds)
+        core = Core(s, params, max_batch=B, flags=flags)
+        lg = core.forward(obs)
+        core.zero_grad()
+        core.backward(dl)
+        out[lds] = (lg, core.get(4))
+        del core
+    (l0, g0), (l1, g1) = out["0"], out["1"]
+    assert np.array_equal(l0, l1)
+    for name, a, b in zip(NAMES, g0, g1):
+        assert np.isfinite(b).all(), name
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
