@@ -3,6 +3,8 @@
   * float32 at B = 4096 on the synthetic 3-hop network (the benchmark batch): logits, KL loss, its logits gradient
     and all seven weight gradients against the float32 oracle (the reference's arithmetic); gradient additivity of
     eight pieces of 512 against the whole batch;
+  * float32 at B = 16384 on the synthetic network and its Erdos-Renyi control: batch independence of the logits
+    and additivity of the gradients over four pieces of 4096;
   * bfloat16 states on the full-size synthetic network and on its Erdos-Renyi control: logits and all seven
     gradients against the bfloat16 restatement (oracle/core16.py) at B = 128; at B = 16384 (the bfloat16 benchmark
     batch) batch independence of the logits and additivity of the gradients over four pieces of 4096;
@@ -205,6 +207,36 @@ def test_bf16_b16384_batch_independence_and_additivity(gpu_lib, request, graph):
         say(f"   grad {name:6s} 4 x 4096 vs 16384 rel {r:.2e}")
         assert r <= 1e-5, (name, r)
 
+
+
+@pytest.mark.parametrize("graph", ["lognormal", "er"])
+def test_fp32_b16384_batch_independence_and_additivity(gpu_lib, request, graph):
+    """Float32 at B = 16384 (512 tiles: the plug's LDS split, the last hop's LDS backward and the XCD mapping at four
+    times the benchmark's tiles): a sample's logits bit-identical in 32-sample slices and under a permutation of the
+    batch; the gradients of four pieces of 4096 add up to the whole batch's (<= 1e-5)."""
+    s, params = request.getfixturevalue(graph)
+    B = 16384
+    say(f"float32 full-size {graph}, B {B}")
+    core = Core(s, params, max_batch=B)
+    rng = np.random.default_rng(45)
+    obs = rng.standard_normal((B, 517)).astype(np.float32)
+    big = core.forward(obs)
+    assert np.isfinite(big).all()
+    for start in (0, 8192, B - 32):
+        assert np.array_equal(core.forward(obs[start:start + 32]), big[start:start + 32]), start
+    perm = rng.permutation(B)
+    assert np.array_equal(core.forward(obs[perm]), big[perm])
+    dl = (rng.standard_normal((B, 90)) / B).astype(np.float32)
+    core.forward(obs)
+    whole = _grads(core, dl)
+    core.zero_grad()
+    for i in range(0, B, 4096):
+        core.forward(obs[i:i + 4096])
+        core.backward(dl[i:i + 4096])
+    for name, a, b in zip(NAMES, core.get(4), whole):
+        r = rel(a, b)
+        say(f"   grad {name:6s} 4 x 4096 vs 16384 rel {r:.2e}")
+        assert r <= 1e-5, (name, r)
 
 # ------------------------------------------------------------------------------------------------ whole connectome
 @pytest.fixture(scope="module")
