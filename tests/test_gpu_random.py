@@ -1,5 +1,5 @@
 """Randomised parity: graphs drawn at random in the graph-file form (a few hundred to 1,500 neurons, skewed
-in-degree, random sensory and descending sets), indexed by FlyActor with 2-4 hops and fan 4, 8 or 16, then run
+in-degree, random sensory and descending sets), indexed by FlyActor with 2-4 hops (and 1 in one test) and fan 4, 8 or 16, then run
 through the library at a random batch against the float64 oracle, with the one-/two-tile choice and the silent-row
 skips set per case.  Bars as tests/test_gpu_parity.py (logits and states <= 1e-5, gradients <= 1e-4, relative to the
 largest entry; argmax identical off near-ties); the teaching step is held bit for bit to its parts; the bfloat16
@@ -138,3 +138,31 @@ def test_random_graph_backward_staged_in_lds(gpu_lib, monkeypatch, seed):
     for name, a, b in zip(NAMES, g0, g1):
         assert np.isfinite(b).all(), name
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
+
+
+@pytest.mark.parametrize("seed", range(40, 46))
+def test_random_graph_one_hop(gpu_lib, seed):
+    """A network of one hop (FlyActor's hops=1: the sensory layer feeds the layer the read-out reads, whose backward
+    is the sensory finish and has no hop above it to stage in LDS): float32 against the float64 oracle at the bars of
+    tests/test_gpu_parity.py at a batch of 32 or 96, and the bfloat16 core against its oracle at 64."""
+    g, rng = random_graph(seed)
+    torch.manual_seed(seed)
+    f = lively(FlyActor(g, 517, 90, hops=1, fan=8), seed)
+    s = structure(f)
+    params = params_from_torch(f, s)
+    B = int(rng.choice([32, 96]))
+    say(f"random graph {seed}, one hop: sizes {s['sizes']}, edges {[len(h['col']) for h in s['hop']]}, B {B}")
+    obs = rng.standard_normal((B, 517)).astype(np.float32)
+    core, o64, got, _ = check_forward(s, params, obs)
+    check_backward(core, o64, s, got, seed=seed)
+    obs16 = rng.standard_normal((64, 517)).astype(np.float32)
+    o = Core16(s, params)
+    want = o.forward(obs16)
+    c16 = Core(s, params, max_batch=64, flags=1)
+    got16 = c16.forward(obs16)
+    assert rel(got16, want) <= 1e-3, rel(got16, want)
+    dl = (rng.standard_normal(want.shape) + 0.2 * want).astype(np.float32)
+    c16.zero_grad()
+    c16.backward(dl)
+    for name, g16, w in zip(NAMES, c16.get(4), o.backward(dl)):
+        assert rel(g16, w) <= 1e-2, (name, rel(g16, w))
