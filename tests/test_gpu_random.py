@@ -1,5 +1,5 @@
 """Randomised parity: graphs drawn at random in the graph-file form (a few hundred to 1,500 neurons, skewed
-in-degree, random sensory and descending sets), indexed by FlyActor with 2-4 hops (1 in one test) and fan 4, 8 or
+in-degree, random sensory and descending sets), indexed by FlyActor with 2-4 hops (1, 5, 6, 9 in one test) and fan 4, 8 or
 16, then run through the library at a random batch against the float64 oracle, with the one-/two-tile choice and the
 silent-row skips set per case.  Bars as tests/test_gpu_parity.py (logits and states <= 1e-5, gradients <= 1e-4,
 relative to the largest entry; argmax identical off near-ties); the teaching step is held bit for bit to its parts;
@@ -140,18 +140,20 @@ def test_random_graph_backward_staged_in_lds(gpu_lib, monkeypatch, seed):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
 
 
-@pytest.mark.parametrize("seed", range(40, 46))
-def test_random_graph_one_hop(gpu_lib, seed):
-    """A network of one hop (FlyActor's hops=1: the sensory layer feeds the layer the read-out reads, whose backward
-    is the sensory finish and has no hop above it to stage in LDS): float32 against the float64 oracle at the bars of
-    tests/test_gpu_parity.py at a batch of 32 or 96, and the bfloat16 core against its oracle at 64."""
+@pytest.mark.parametrize("hops,seed", [(1, 40), (1, 41), (1, 42), (1, 43), (1, 44), (1, 45), (5, 50), (6, 51),
+                                       (9, 50)])
+def test_random_graph_one_and_many_hops(gpu_lib, hops, seed):
+    """Networks of one hop (FlyActor's hops=1: the sensory layer feeds the layer the read-out reads, whose backward
+    is the sensory finish and has no hop above it to stage in LDS) and of 5, 6 and 9 hops (beyond the profiler's 8
+    per-hop stages): float32 against the float64 oracle at the bars of tests/test_gpu_parity.py at a batch of 32 or
+    96, and the bfloat16 core against its oracle at 64."""
     g, rng = random_graph(seed)
     torch.manual_seed(seed)
-    f = lively(FlyActor(g, 517, 90, hops=1, fan=8), seed)
+    f = lively(FlyActor(g, 517, 90, hops=hops, fan=8), seed)
     s = structure(f)
     params = params_from_torch(f, s)
     B = int(rng.choice([32, 96]))
-    say(f"random graph {seed}, one hop: sizes {s['sizes']}, edges {[len(h['col']) for h in s['hop']]}, B {B}")
+    say(f"random graph {seed}, {hops} hops: sizes {s['sizes']}, edges {[len(h['col']) for h in s['hop']]}, B {B}")
     obs = rng.standard_normal((B, 517)).astype(np.float32)
     core, o64, got, _ = check_forward(s, params, obs)
     check_backward(core, o64, s, got, seed=seed)
