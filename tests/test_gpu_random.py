@@ -1,7 +1,7 @@
 """Randomised parity: graphs drawn at random in the graph-file form (a few hundred to 1,500 neurons, skewed
-in-degree, random sensory and descending sets), indexed by FlyActor with 2-4 hops (1, 5, 6, 9 in one test) and fan 4, 8 or
-16, then run through the library at a random batch against the float64 oracle, with the one-/two-tile choice and the
-silent-row skips set per case.  Bars as tests/test_gpu_parity.py (logits and states <= 1e-5, gradients <= 1e-4,
+in-degree, random sensory and descending sets), indexed by FlyActor with 2-4 hops (1, 5, 6, 9 in one test) and fan
+4, 8 or 16, then run through the library at a random batch against the float64 oracle, with the one-/two-tile choice
+and the silent-row skips set per case.  Bars as tests/test_gpu_parity.py (logits and states <= 1e-5, gradients <= 1e-4,
 relative to the largest entry; argmax identical off near-ties); the teaching step is held bit for bit to its parts;
 the bfloat16 core to its numpy oracle at the general-network bars of tests/test_gpu_core16.py."""
 from __future__ import annotations
