@@ -292,9 +292,8 @@ struct AdamSeg {
 hipError_t launch_adam(float* P, const float* G, float* M, float* V, float* EMA, const AdamSeg& s, float c1, float c2,
                        const float* gs_dev, float gs, float decay, hipStream_t st);
 hipError_t launch_export(const float* src, Lay ls, float* dst, int rows, int B, hipStream_t st);
-hipError_t launch_rowinfo(const int* nid, const int* drow, const float* gain, const float* theta, float4* info, int rows,
-                          hipStream_t st);
-// the same for up to ROW_JOBS layers in one launch
+// per row of a layer its record {gain[nid], softplus(theta[nid]), re-drive row, 0} (see FwdEpi::info), for up to
+// ROW_JOBS layers in one launch
 struct RowJob {
     const int *nid = nullptr, *drow = nullptr;
     float4* info = nullptr;

@@ -1524,12 +1524,6 @@ hipError_t launch_rowinfo_n(const RowJob* jobs, int n, const float* gain, const 
     return hipGetLastError();
 }
 
-hipError_t launch_rowinfo(const int* nid, const int* drow, const float* gain, const float* theta, float4* info, int rows,
-                          hipStream_t st) {
-    const RowJob j{nid, drow, info, rows};
-    return launch_rowinfo_n(&j, 1, gain, theta, st);
-}
-
 hipError_t launch_export(const float* src, Lay ls, float* dst, int rows, int B, hipStream_t st) {
     k_export<<<blocks((long long)rows * B), WG, 0, st>>>(src, ls, dst, rows, B);
     return hipGetLastError();
