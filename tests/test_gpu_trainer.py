@@ -395,6 +395,25 @@ def test_trainer_run_matches_replay(gpu_lib, tmp_path, capfd):
     _same(core, saved)
 
 
+
+@pytest.mark.parametrize("hops", [1, 5])
+def test_trainer_run_matches_replay_other_depths(gpu_lib, tmp_path, capfd, hops):
+    """The trainer on networks of one and of five hops: weights, running average and both Adam moments after four
+    steps bit-identical to the same draws fed through fc_teach_step."""
+    s, params = toy_net("b", hops, 8, seed=2)
+    data, chunks = _setup(tmp_path, s, params)
+    B, steps = 64, 4
+    rc = _run(tmp_path / "net.bin", tmp_path / "init.bin", data, tmp_path / "out", *_opts(B, steps))
+    say(capfd.readouterr().out)
+    assert rc == 0
+    step, adam_t, saved = _saved(tmp_path, s)
+    assert step == steps and adam_t == steps
+    ring = ot.scan_order(data, 2)
+    core = Core(s, params, max_batch=B)
+    _replay(core, ring, chunks, ot.MT19937_64(12345), steps, 0, B, OPTS["lr"], OPTS["lrn"], OPTS["lrp"], OPTS["lmin"],
+            OPTS["hl"], 0.0, OPTS["ema"])
+    _same(core, saved)
+
 def test_bf16_trainer_run_matches_replay(gpu_lib, tmp_path, capfd):
     """--bf16 1: the trainer on a bfloat16-state handle, step for step what fc_teach_step does on one."""
     s, params = toy_net("b", 3, 8, seed=2)
