@@ -168,14 +168,45 @@ def test_native_actor_like_core_check(gpu_lib):
     assert rel(a.cpu().numpy(), want_lg) <= 1e-5
 
 
-def test_hop_hip_matches_torch(gpu_lib):
-    """HopHip (the HopCuda interface): output and both gradients against the sparse product in float64."""
-    say("hop hip")
+@pytest.mark.parametrize("hops", [1, 5])
+def test_native_actor_other_depths(gpu_lib, hops):
+    """NativeFlyActor on networks of one and five hops: logits and the seven gradients against the PyTorch path in
+    float64, in one piece and in pieces of max_batch (batch 160, max_batch 64)."""
+    say(f"native actor, {hops} hops")
+    torch.manual_seed(1)
+    base = lively(FlyActor(toy("b"), 517, 90, hops=hops, fan=16), seed=hops)
+    nat = NativeFlyActor(toy("b"), 517, 90, hops=hops, fan=16, max_batch=64)
+    nat.load_state_dict(base.state_dict())
+    nat = nat.cuda()
+    rng = np.random.default_rng(hops)
+    obs = (rng.standard_normal((160, 517)) * 0.5).astype(np.float32)
+    R = rng.standard_normal((160, 90)).astype(np.float32)
+    opt = nat.native_adam(1e-3, 0.0)
+    assert opt is not None
+    for n in (64, 160):
+        want_lg, ref = _torch_reference(base, obs[:n], R[:n])
+        opt.zero_grad()
+        ln = nat(torch.as_tensor(obs[:n]).cuda())
+        ((ln * torch.as_tensor(R[:n]).cuda()).sum() + 0.1 * ln.pow(2).sum()).backward()
+        assert rel(ln.detach().cpu().numpy(), want_lg) <= 1e-5
+        got = grad_arrays(nat)
+        want = [ref.w.grad.numpy()[nat._wmap.cpu().numpy()], ref.gain.grad.numpy(), ref.theta.grad.numpy(),
+                ref.in_w.grad.numpy(), ref.in_b.grad.numpy(), ref.out.weight.grad.numpy().reshape(-1),
+                ref.out.bias.grad.numpy()]
+        for name, g, w in zip(NAMES, got, want):
+            assert rel(g.reshape(-1), w) <= 1e-4, (hops, n, name, rel(g.reshape(-1), w))
+
+
+@pytest.mark.parametrize("hops", [3, 1, 2, 5])
+def test_hop_hip_matches_torch(gpu_lib, hops):
+    """HopHip (the HopCuda interface): output and both gradients of every hop against the sparse product in float64,
+    then the whole actor through HopHip against the PyTorch path, on networks of one to five hops."""
+    say(f"hop hip, {hops} hops")
     from flyguy_amd.fly_hip import HopHip
     torch.manual_seed(0)
-    f = lively(FlyActor(toy("b"), 517, 90, hops=3, fan=16))
+    f = lively(FlyActor(toy("b"), 517, 90, hops=hops, fan=16))
     B = 64
-    for k in (1, 2, 3):
+    for k in range(1, hops + 1):
         n_src = f.sizes[k - 1]
         h = torch.rand(n_src, B, dtype=torch.float64)
         w = f.w.detach()[getattr(f, f"e{k}")].double()
