@@ -47,13 +47,15 @@ def test_fire_matches_pytorch(gpu_lib, rows, B):
         assert rel(a[fin].double().cpu().numpy(), b[fin].double().cpu().numpy()) <= 1e-5
 
 
-def test_actor_gradients_through_the_library(gpu_lib):
+@pytest.mark.parametrize("hops", [3, 1, 5])
+def test_actor_gradients_through_the_library(gpu_lib, hops):
     """FlyActor with kernel "hip" (HopHip products, FireHip activations): logits and every parameter's gradient
-    against the PyTorch path in float64 (fly.py:286-305), on a toy network with re-driven rows."""
-    say("actor gradients through HopHip and FireHip")
+    against the PyTorch path in float64 (fly.py:286-305), on toy networks of one, three and five hops (the deeper two
+    with re-driven rows; at one hop the toy network has none)."""
+    say(f"actor gradients through HopHip and FireHip, {hops} hops")
     torch.manual_seed(2)
-    f = lively(FlyActor(toy("b"), 517, 90, hops=3, fan=16))
-    assert any(len(getattr(f, f"s{k}")) for k in range(1, 4))          # re-driven sensory rows exist
+    f = lively(FlyActor(toy("b"), 517, 90, hops=hops, fan=16))
+    assert hops == 1 or any(len(getattr(f, f"s{k}")) for k in range(1, hops + 1))    # re-driven sensory rows
     x = torch.randn(96, 517)
     R = torch.randn(96, 90)
     g = copy.deepcopy(f).cuda()
