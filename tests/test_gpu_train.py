@@ -260,21 +260,24 @@ def _half_case(a, r, c, w, n_src, n_rows, B, crow, col, tcrow, tcol, tperm, seed
         assert r_ <= 1e-5, (name, B, r_)
 
 
-def test_hop_hip_half_matches_reference_rounding(gpu_lib):
+@pytest.mark.parametrize("hops", [3, 5])
+def test_hop_hip_half_matches_reference_rounding(gpu_lib, hops):
     """HopHip(half=True), the fp16 variant of HopCuda: relative to the largest entry <= 1e-5 (float32 sums of the
-    same binary16 operands), on toy hops and on a hop of the scaled benchmark shape whose heavy rows are split,
-    at B = 64 and at B = 96 (a 64-sample tile that is half past the batch)."""
-    say("hop hip half")
+    same binary16 operands), on every hop of toy networks of three and five hops and on a hop of the scaled benchmark
+    shape whose heavy rows are split, at B = 64 and at B = 96 (a 64-sample tile that is half past the batch)."""
+    say(f"hop hip half, {hops} hops")
     from flyguy_amd.synth import scaled_3hop
     torch.manual_seed(0)
-    f = lively(FlyActor(toy("b"), 517, 90, hops=3, fan=16))
+    f = lively(FlyActor(toy("b"), 517, 90, hops=hops, fan=16))
     for B in (64, 96):
-        for k in (1, 2, 3):
+        for k in range(1, hops + 1):
             n_src, crow, col = f.sizes[k - 1], getattr(f, f"crow{k}"), getattr(f, f"ci{k}")
             w = f.w.detach()[getattr(f, f"e{k}")].double()
             a = torch.sparse_csr_tensor(crow, col.long(), w, size=(len(crow) - 1, n_src))
             _half_case(a, getattr(f, f"r{k}"), getattr(f, f"c{k}"), w, n_src, len(crow) - 1, B, crow, col,
                        getattr(f, f"tcrow{k}"), getattr(f, f"tci{k}"), getattr(f, f"tperm{k}"), 10 * B + k)
+    if hops != 3:
+        return
     s, params = scaled_3hop(16)
     h = s["hop"][1]
     crow = torch.as_tensor(np.asarray(h["crow"], np.int64))
